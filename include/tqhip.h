@@ -1,0 +1,149 @@
+/* tqhip.h -- C ABI of the MI355X (gfx950) quantized linear-projection library.
+ *
+ * Drop-in for tiny-llm's kernel dispatch on the quantized-projection path.
+ * Reference paths below are relative to the tiny-llm source root.
+ *
+ * 1. Host-pointer entry points. Exactly the reference's dispatch signatures:
+ *    synchronous, caller-owned host buffers, no error return (a HIP failure
+ *    prints to stderr and aborts, as the reference's GPU variants do). Weights
+ *    are immutable for the life of the process (docs/optimization.md:147-149),
+ *    so each weight tensor is copied to HBM once and cached by its host
+ *    pointer and byte size; x and y go through a grow-only device workspace.
+ *    These are the functions registered as the "hip" variants.
+ *
+ * 2. Device-pointer entry points (suffix _dev). Same math on buffers already
+ *    in HBM, launched asynchronously on `stream` (a hipStream_t; NULL = the
+ *    default stream). They return 0 or a negative TQHIP_E* code and never abort.
+ *
+ * 3. Registry. The library carries its own copy of the reference registry for
+ *    these families (same names and behaviour, C++ namespace tinyqwen,
+ *    tiny-llm_amd/csrc/dispatch.h); the tqhip_set_* / tqhip_dispatch_* symbols
+ *    below expose it to C callers.
+ *
+ * Layouts (runtime/tiny_format.h:58-103, docs/weight_format.md:83-119):
+ *   i4 : every row is ceil(in_dim/G) groups of [scale fp16 | zero fp16 | G/2 code bytes],
+ *        low nibble = even element; weight = (q - zero) * scale.
+ *   VQ2: [codebook 256 x 4 fp16 = 2048 B][out_dim x in_dim/4 uint8 indices], in_dim % 4 == 0.
+ *   matmul: X is [K, N] column-major (x[n*K + k]), Y is [M, N] column-major (y[n*M + m]).
+ */
+#ifndef TQHIP_H
+#define TQHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TQHIP_OK 0
+#define TQHIP_EBADSHAPE (-1)    /* a dimension < 1, or in_dim % 4 != 0 for VQ2 */
+#define TQHIP_EBADGROUP (-2)    /* group_size odd or < 2 */
+#define TQHIP_ETOOLARGE (-3)    /* shape exceeds the kernel's 32-bit addressing */
+#define TQHIP_ELAUNCH (-4)      /* the kernel launch failed */
+
+/* ---- 1. host-pointer entry points (the "hip" variants) ------------------ */
+
+/* MatvecI4Fn, kernels/dispatch.h:151-152; replaces matvec_i4_ref (kernels/matvec/matvec_i4_ref.cpp:45). */
+void tqhip_matvec_i4(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size);
+
+/* MatvecPairI4Fn, kernels/dispatch.h:162-163 (no i4 pair kernel exists in the reference). */
+void tqhip_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2,
+                          int out_dim, int in_dim, int group_size);
+
+/* MatvecQkvI4Fn, kernels/dispatch.h:169-171 (no i4 qkv kernel exists in the reference). */
+void tqhip_matvec_qkv_i4(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x, float *yq,
+                         float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size);
+
+/* MatvecVQ2Fn, kernels/dispatch.h:187-188; replaces matvec_vq2_ref (kernels/matvec/matvec_vq2_ref.cpp:52). */
+void tqhip_matvec_vq2(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim);
+
+/* MatmulI4Fn, kernels/dispatch.h:249-250; replaces matmul_i4_ref (kernels/matvec/matmul_i4_ref.cpp:53). */
+void tqhip_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size);
+
+/* Drops every cached device copy of host weights (not in the reference: its
+ * CUDA variants keep their cache until exit). */
+void tqhip_release_weights(void);
+
+/* ---- 2. device-pointer entry points ------------------------------------- */
+
+int tqhip_matvec_i4_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                        void *stream);
+int tqhip_matvec_vq2_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, void *stream);
+int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                        void *stream);
+/* The portable fp32 one-wave-per-row i4 kernel, used by the fast path for
+ * group sizes it does not cover; exported for cross-checks. */
+int tqhip_matvec_i4_generic_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim,
+                                int group_size, void *stream);
+
+/* ---- 3. registry (kernels/dispatch.h:155-159, 191-195; set_matmul_i4_impl_by_name is new) */
+
+int tqhip_set_matvec_i4_impl_by_name(const char *name);   /* 1 = selected, 0 = unknown name */
+const char *tqhip_matvec_i4_impl_name(void);
+const char *tqhip_available_matvec_i4_impls(void);
+int tqhip_set_matvec_vq2_impl_by_name(const char *name);
+const char *tqhip_matvec_vq2_impl_name(void);
+const char *tqhip_available_matvec_vq2_impls(void);
+int tqhip_set_matmul_i4_impl_by_name(const char *name);
+void tqhip_dispatch_matvec_i4(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size);
+void tqhip_dispatch_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2,
+                                   int out_dim, int in_dim, int group_size);
+void tqhip_dispatch_matvec_qkv_i4(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x,
+                                  float *yq, float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size);
+void tqhip_dispatch_matvec_vq2(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim);
+void tqhip_dispatch_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size);
+void tqhip_dispatch_matmul_vq2(const uint8_t *w, const float *x, float *y, int M, int K, int N);
+
+/* ---- 4. byte accounting (runtime/tiny_format.h:73-78, 100-103) --------- */
+
+size_t tqhip_i4_row_bytes(int in_dim, int group_size);
+size_t tqhip_vq2_tensor_bytes(int rows, int cols);
+
+/* ---- 5. device plumbing for hosts without a HIP toolchain (tests, bench) */
+
+int tqhip_device_count(void);
+int tqhip_device_name(char *buf, int len);
+void *tqhip_malloc(size_t bytes);                 /* NULL on failure */
+int tqhip_free(void *p);
+int tqhip_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int tqhip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int tqhip_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int tqhip_memset(void *dst, int value, size_t bytes);
+int tqhip_synchronize(void);
+void *tqhip_stream_create(void);                  /* default priority */
+int tqhip_stream_destroy(void *stream);
+int tqhip_stream_synchronize(void *stream);
+void *tqhip_event_create(void);
+int tqhip_event_destroy(void *event);
+int tqhip_event_record(void *event, void *stream);
+int tqhip_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* A list of device-pointer calls run back to back on one stream, `repeats`
+ * times; used to time a whole decode step with one host call. */
+typedef struct tqhip_op {
+    int kind;                 /* TQHIP_OP_* */
+    const void *w;
+    const float *x;
+    float *y;
+    int out_dim, in_dim, n, group_size;
+} tqhip_op;
+#define TQHIP_OP_I4_MATVEC 1
+#define TQHIP_OP_VQ2_MATVEC 2
+#define TQHIP_OP_I4_MATMUL 3
+int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream);
+
+/* ---- 6. synthetic inputs (portable generator, identical on every host) -- */
+
+uint64_t tq_synth_seed(uint64_t base, int layer, const char *name);
+void tq_synth_i4(uint8_t *w, int out_dim, int in_dim, int group_size, uint64_t seed, float scale_lo,
+                 float scale_hi, float zero_lo, float zero_hi);
+void tq_synth_normal(float *x, long long n, uint64_t seed, float mean, float stddev);
+void tq_synth_vq2(uint8_t *w, int out_dim, int in_dim, uint64_t seed, float cb_std);
+uint16_t tq_f32_to_f16(float f);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TQHIP_H */

@@ -1,0 +1,101 @@
+"""i4 HQQ matvec on the GPU against the oracle (and the reference's golden outputs).
+
+Tolerance: rel L2 <= 1e-5 and max|err| <= 1e-3 * max|y_ref|.
+"""
+import numpy as np
+import pytest
+
+from conftest import golden, golden_names, max_abs_rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-5
+MAX_REL = 1e-3
+
+
+def assert_close(got, want, what=""):
+    l2, mx = rel_l2(got, want), max_abs_rel(got, want)
+    assert l2 <= REL_L2 and mx <= MAX_REL, f"{what}: rel_l2={l2:.3e} max_rel={mx:.3e}"
+
+
+@pytest.mark.parametrize("name", [n for n in golden_names("i4_") if "qkv" not in n and "pair" not in n])
+def test_golden_through_registry(gpu, name):
+    f = golden(name)
+    M, K, G = (int(v) for v in f["dims"])
+    assert gpu.set_matvec_i4_impl_by_name("hip")
+    got = gpu.matvec_i4(f["w"], f["x"], M, K, G)
+    assert_close(got, f["y"], name)
+    if name == "i4_kat_1x4_g4":
+        assert abs(got[0] - 28.0) < 1e-5  # tests/test_matvec_i4.cpp:212
+
+
+def test_golden_pair_and_qkv(gpu):
+    f = golden("i4_pair_16x256_g64")
+    M, K, G = (int(v) for v in f["dims"])
+    y1, y2 = gpu.matvec_pair_i4(f["w1"], f["w2"], f["x"], M, K, G)
+    assert_close(y1, f["y1"], "pair y1")
+    assert_close(y2, f["y2"], "pair y2")
+    f = golden("i4_qkv_48_16x256_g64")
+    q, kv, K, G = (int(v) for v in f["dims"])
+    yq, yk, yv = gpu.matvec_qkv_i4(f["wq"], f["wk"], f["wv"], f["x"], q, kv, K, G)
+    assert_close(yq, f["yq"], "qkv q")
+    assert_close(yk, f["yk"], "qkv k")
+    assert_close(yv, f["yv"], "qkv v")
+
+
+SHAPES = [
+    (1, 64, 64), (15, 896, 64), (16, 896, 64), (17, 896, 64), (128, 896, 64), (896, 896, 64),
+    (4864, 896, 64), (896, 4864, 64), (300, 2560, 64), (2560, 9728, 64), (333, 200, 64),
+    (257, 1024, 128), (100, 520, 40), (64, 4096, 256), (50, 100, 32), (7, 70, 6), (41, 1000, 48),
+]
+
+
+@pytest.mark.parametrize("M,K,G", SHAPES)
+def test_device_api_matches_oracle(gpu, orc, M, K, G):
+    w = gpu.synth_i4(M, K, G, seed=M * 131 + K)
+    x = gpu.synth_normal(K, seed=K + 7)
+    want = orc.matvec_i4(w, x, M, K, G, threads=8)
+    dw, dx = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x)
+    dy = gpu.DeviceBuffer(4 * M)
+    gpu.matvec_i4_dev(dw, dx, dy, M, K, G)
+    got = dy.download(np.float32, M)
+    assert_close(got, want, f"fast {M}x{K} G{G}")
+    gpu.matvec_i4_generic_dev(dw, dx, dy, M, K, G)
+    assert_close(dy.download(np.float32, M), want, f"generic {M}x{K} G{G}")
+
+
+def test_activation_extremes_per_group(gpu, orc):
+    # one huge and one tiny activation per group: the per-group exponent must keep precision
+    M, K, G = 64, 2560, 64
+    w = gpu.synth_i4(M, K, G, seed=99)
+    x = gpu.synth_normal(K, seed=98)
+    x[::64] *= 1e4
+    x[1::64] *= 1e-6
+    x[5 * 64:6 * 64] = 0.0
+    want = orc.matvec_i4(w, x, M, K, G)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
+    gpu.matvec_i4_dev(dw, dx, dy, M, K, G)
+    assert_close(dy.download(np.float32, M), want, "extremes")
+
+
+def test_headline_lm_head_shape_and_determinism(gpu, orc):
+    M, K, G = 151936, 2560, 64
+    w = gpu.synth_i4(M, K, G, seed=gpu.synth_seed(0, 0, "lm_head"))
+    x = gpu.synth_normal(K, seed=gpu.synth_seed(0, 0, "x"))
+    want = orc.matvec_i4(w, x, M, K, G, threads=16)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
+    gpu.matvec_i4_dev(dw, dx, dy, M, K, G)
+    y1 = dy.download(np.float32, M)
+    assert_close(y1, want, "lm_head 151936x2560")
+    gpu.matvec_i4_dev(dw, dx, dy, M, K, G)
+    assert np.array_equal(dy.download(np.float32, M), y1)  # fixed reduction order
+
+
+def test_bad_shapes_return_codes(gpu):
+    lib = gpu.lib()
+    assert lib.tqhip_matvec_i4_dev(None, None, None, 0, 64, 64, None) == gpu.EBADSHAPE
+    assert lib.tqhip_matvec_i4_dev(None, None, None, 4, 0, 64, None) == gpu.EBADSHAPE
+    assert lib.tqhip_matvec_i4_dev(None, None, None, 4, 64, 63, None) == gpu.EBADGROUP
+    assert lib.tqhip_matvec_i4_dev(None, None, None, 4, 64, 0, None) == gpu.EBADGROUP
+    assert lib.tqhip_matvec_vq2_dev(None, None, None, 4, 6, None) == gpu.EBADSHAPE
+    assert lib.tqhip_matmul_i4_dev(None, None, None, 4, 64, 0, 64, None) == gpu.EBADSHAPE

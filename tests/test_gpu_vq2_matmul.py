@@ -1,0 +1,61 @@
+"""VQ2 matvec and i4 matmul on the GPU against the oracle and the golden outputs.
+
+VQ2 tolerance: rel L2 <= 1e-5 and max|err| <= 1e-3 * max|y_ref| (north star matvec bar).
+matmul_i4 tolerance: rel L2 <= 2e-3 and max|err| <= 1e-3 * max|y_ref| (north star prefill bar).
+"""
+import numpy as np
+import pytest
+
+from conftest import golden, golden_names, max_abs_rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_close(got, want, l2_tol, what=""):
+    l2, mx = rel_l2(got, want), max_abs_rel(got, want)
+    assert l2 <= l2_tol and mx <= 1e-3, f"{what}: rel_l2={l2:.3e} max_rel={mx:.3e}"
+
+
+@pytest.mark.parametrize("name", golden_names("vq2_"))
+def test_vq2_golden_through_registry(gpu, name):
+    f = golden(name)
+    M, K = (int(v) for v in f["dims"])
+    assert gpu.set_matvec_vq2_impl_by_name("hip")
+    got = gpu.matvec_vq2(f["w"], f["x"], M, K)
+    assert_close(got, f["y"], 1e-5, name)
+    if name == "vq2_kat_1x4":
+        assert abs(got[0] - 20.0) < 1e-5  # tests/test_matvec_vq2.cpp:163
+
+
+def test_matmul_vq2_golden_decomposes(gpu):
+    f = golden("mm_vq2_48x192x5")
+    M, K, N = (int(v) for v in f["dims"])
+    assert_close(gpu.matmul_vq2(f["w"], f["x"], M, K, N), f["y"], 1e-5, "matmul_vq2")
+
+
+@pytest.mark.parametrize("M,K", [(3072, 1024), (1, 4), (513, 896), (4864, 896), (100, 52), (77, 1000), (16384, 2048)])
+def test_vq2_device_api_matches_oracle(gpu, orc, M, K):
+    w = gpu.synth_vq2(M, K, seed=M + K)
+    x = gpu.synth_normal(K, seed=K)
+    want = orc.matvec_vq2(w, x, M, K, threads=8)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
+    gpu.matvec_vq2_dev(dw, dx, dy, M, K)
+    assert_close(dy.download(np.float32, M), want, 1e-5, f"vq2 {M}x{K}")
+
+
+@pytest.mark.parametrize("name", golden_names("mm_i4_"))
+def test_matmul_i4_golden_through_registry(gpu, name):
+    f = golden(name)
+    M, K, N, G = (int(v) for v in f["dims"])
+    assert gpu.set_matmul_i4_impl_by_name("hip")
+    assert_close(gpu.matmul_i4(f["w"], f["x"], M, K, N, G), f["y"], 2e-3, name)
+
+
+@pytest.mark.parametrize("M,K,N,G", [(9728, 2560, 32, 64), (300, 896, 7, 64), (1000, 640, 48, 128)])
+def test_matmul_i4_device_api_matches_oracle(gpu, orc, M, K, N, G):
+    w = gpu.synth_i4(M, K, G, seed=M + N)
+    x = gpu.synth_normal(K * N, seed=N)
+    want = orc.matmul_i4(w, x, M, K, N, G, threads=16)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M * N)
+    gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G)
+    assert_close(dy.download(np.float32, M * N), want, 2e-3, f"matmul {M}x{K}x{N}")

@@ -1,0 +1,361 @@
+"""tiny-llm_amd -- MI355X (gfx950) quantized linear-projection path for tiny-llm.
+
+Python host side of libtqhip.so (HIP kernels + the C ABI in include/tqhip.h).
+It mirrors the reference registry's entry points (kernels/dispatch.h:151-253
+of tiny-llm) on numpy arrays, plus device-buffer helpers for tests and
+benchmarks. There is no CPU fallback: every compute call goes to the HIP
+library, and loading fails loudly if the library has not been built.
+
+The directory name is not a valid module name, so load it by path::
+
+    spec = importlib.util.spec_from_file_location("tiny_llm_amd", ".../tiny-llm_amd/__init__.py")
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtqhip.so")
+
+OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH = 0, -1, -2, -3, -4
+OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL = 1, 2, 3
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+
+
+class Op(ctypes.Structure):
+    """tqhip_op: one device-pointer call of a tqhip_run_ops list."""
+    _fields_ = [("kind", _i), ("w", _vp), ("x", _vp), ("y", _vp),
+                ("out_dim", _i), ("in_dim", _i), ("n", _i), ("group_size", _i)]
+
+
+_SIGS = {
+    # host-pointer entry points (the "hip" variants)
+    "tqhip_matvec_i4": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "tqhip_matvec_pair_i4": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "tqhip_matvec_qkv_i4": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
+    "tqhip_matvec_vq2": (None, [_vp, _vp, _vp, _i, _i]),
+    "tqhip_matmul_i4": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "tqhip_release_weights": (None, []),
+    # device-pointer entry points
+    "tqhip_matvec_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tqhip_matvec_i4_generic_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tqhip_matvec_vq2_dev": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "tqhip_matmul_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    # registry
+    "tqhip_set_matvec_i4_impl_by_name": (_i, [ctypes.c_char_p]),
+    "tqhip_matvec_i4_impl_name": (ctypes.c_char_p, []),
+    "tqhip_available_matvec_i4_impls": (ctypes.c_char_p, []),
+    "tqhip_set_matvec_vq2_impl_by_name": (_i, [ctypes.c_char_p]),
+    "tqhip_matvec_vq2_impl_name": (ctypes.c_char_p, []),
+    "tqhip_available_matvec_vq2_impls": (ctypes.c_char_p, []),
+    "tqhip_set_matmul_i4_impl_by_name": (_i, [ctypes.c_char_p]),
+    "tqhip_dispatch_matvec_i4": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "tqhip_dispatch_matvec_pair_i4": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "tqhip_dispatch_matvec_qkv_i4": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
+    "tqhip_dispatch_matvec_vq2": (None, [_vp, _vp, _vp, _i, _i]),
+    "tqhip_dispatch_matmul_i4": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "tqhip_dispatch_matmul_vq2": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    # byte accounting
+    "tqhip_i4_row_bytes": (_sz, [_i, _i]),
+    "tqhip_vq2_tensor_bytes": (_sz, [_i, _i]),
+    # device plumbing
+    "tqhip_device_count": (_i, []),
+    "tqhip_device_name": (_i, [ctypes.c_char_p, _i]),
+    "tqhip_malloc": (_vp, [_sz]),
+    "tqhip_free": (_i, [_vp]),
+    "tqhip_memcpy_h2d": (_i, [_vp, _vp, _sz]),
+    "tqhip_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "tqhip_memcpy_d2d": (_i, [_vp, _vp, _sz]),
+    "tqhip_memset": (_i, [_vp, _i, _sz]),
+    "tqhip_synchronize": (_i, []),
+    "tqhip_stream_create": (_vp, []),
+    "tqhip_stream_destroy": (_i, [_vp]),
+    "tqhip_stream_synchronize": (_i, [_vp]),
+    "tqhip_event_create": (_vp, []),
+    "tqhip_event_destroy": (_i, [_vp]),
+    "tqhip_event_record": (_i, [_vp, _vp]),
+    "tqhip_event_elapsed_ms": (_i, [_vp, _vp, _f32p]),
+    "tqhip_run_ops": (_i, [ctypes.POINTER(Op), _i, _i, _vp]),
+    # synthetic inputs
+    "tq_synth_seed": (ctypes.c_uint64, [ctypes.c_uint64, _i, ctypes.c_char_p]),
+    "tq_synth_i4": (None, [_vp, _i, _i, _i, ctypes.c_uint64, ctypes.c_float, ctypes.c_float,
+                           ctypes.c_float, ctypes.c_float]),
+    "tq_synth_normal": (None, [_vp, ctypes.c_longlong, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
+    "tq_synth_vq2": (None, [_vp, _i, _i, ctypes.c_uint64, ctypes.c_float]),
+    "tq_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+}
+
+EXPORTED = tuple(_SIGS)
+_LIB = None
+
+
+def build() -> str:
+    """Compiles libtqhip.so in-tree (hipcc, gfx950)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("tiny_llm_amd_build", os.path.join(HERE, "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.build()
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded HIP library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run tiny-llm_amd/build.py (no CPU fallback exists)")
+        cdll = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(cdll, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = cdll
+    return _LIB
+
+
+def _ptr(a) -> int:
+    if isinstance(a, DeviceBuffer):
+        return a.ptr
+    if isinstance(a, np.ndarray):
+        if not a.flags["C_CONTIGUOUS"]:
+            raise ValueError("array must be C-contiguous")
+        return a.ctypes.data
+    return int(a)
+
+
+def _check(status: int, what: str) -> None:
+    if status != OK:
+        raise RuntimeError(f"{what} failed with status {status}")
+
+
+# ---- layout and synthetic inputs -------------------------------------------------------------
+
+def i4_row_bytes(in_dim: int, group_size: int) -> int:
+    return ((in_dim + group_size - 1) // group_size) * (4 + group_size // 2)
+
+
+def vq2_tensor_bytes(rows: int, cols: int) -> int:
+    return 2048 + rows * (cols // 4)
+
+
+def synth_seed(base: int, layer: int, name: str) -> int:
+    return int(lib().tq_synth_seed(base, layer, name.encode()))
+
+
+def synth_i4(out_dim: int, in_dim: int, group_size: int, seed: int, scale=(0.002, 0.02),
+             zero=(0.0, 15.0)) -> np.ndarray:
+    """i4 weights in the interleaved layout; codes U{0..15}, scale/zero fp16(U[.])."""
+    w = np.empty(out_dim * i4_row_bytes(in_dim, group_size), dtype=np.uint8)
+    lib().tq_synth_i4(w.ctypes.data, out_dim, in_dim, group_size, seed, scale[0], scale[1], zero[0], zero[1])
+    return w
+
+
+def synth_normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    x = np.empty(n, dtype=np.float32)
+    lib().tq_synth_normal(x.ctypes.data, n, seed, mean, std)
+    return x
+
+
+def synth_vq2(out_dim: int, in_dim: int, seed: int, cb_std: float = 0.02) -> np.ndarray:
+    w = np.empty(vq2_tensor_bytes(out_dim, in_dim), dtype=np.uint8)
+    lib().tq_synth_vq2(w.ctypes.data, out_dim, in_dim, seed, cb_std)
+    return w
+
+
+# ---- the reference's dispatch entry points, host arrays ------------------------------------
+
+def matvec_i4(w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int, group_size: int) -> np.ndarray:
+    """tinyqwen::matvec_i4 (kernels/dispatch.h:151-159) through the registry."""
+    y = np.empty(out_dim, dtype=np.float32)
+    lib().tqhip_dispatch_matvec_i4(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, group_size)
+    return y
+
+
+def matvec_pair_i4(w1, w2, x, out_dim: int, in_dim: int, group_size: int):
+    y1 = np.empty(out_dim, dtype=np.float32)
+    y2 = np.empty(out_dim, dtype=np.float32)
+    lib().tqhip_dispatch_matvec_pair_i4(_ptr(w1), _ptr(w2), _ptr(x), _ptr(y1), _ptr(y2), out_dim, in_dim,
+                                        group_size)
+    return y1, y2
+
+
+def matvec_qkv_i4(wq, wk, wv, x, q_dim: int, kv_dim: int, in_dim: int, group_size: int):
+    yq = np.empty(q_dim, dtype=np.float32)
+    yk = np.empty(kv_dim, dtype=np.float32)
+    yv = np.empty(kv_dim, dtype=np.float32)
+    lib().tqhip_dispatch_matvec_qkv_i4(_ptr(wq), _ptr(wk), _ptr(wv), _ptr(x), _ptr(yq), _ptr(yk), _ptr(yv),
+                                       q_dim, kv_dim, in_dim, group_size)
+    return yq, yk, yv
+
+
+def matvec_vq2(w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int) -> np.ndarray:
+    y = np.empty(out_dim, dtype=np.float32)
+    lib().tqhip_dispatch_matvec_vq2(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim)
+    return y
+
+
+def matmul_i4(w: np.ndarray, x: np.ndarray, M: int, K: int, N: int, group_size: int) -> np.ndarray:
+    """Y[M,N] = W[M,K] X[K,N]; x is x[n*K+k] (N columns), result is y[n*M+m]."""
+    y = np.empty(M * N, dtype=np.float32)
+    lib().tqhip_dispatch_matmul_i4(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size)
+    return y
+
+
+def matmul_vq2(w: np.ndarray, x: np.ndarray, M: int, K: int, N: int) -> np.ndarray:
+    y = np.empty(M * N, dtype=np.float32)
+    lib().tqhip_dispatch_matmul_vq2(_ptr(w), _ptr(x), _ptr(y), M, K, N)
+    return y
+
+
+def set_matvec_i4_impl_by_name(name: str) -> bool:
+    return bool(lib().tqhip_set_matvec_i4_impl_by_name(name.encode()))
+
+
+def set_matvec_vq2_impl_by_name(name: str) -> bool:
+    return bool(lib().tqhip_set_matvec_vq2_impl_by_name(name.encode()))
+
+
+def set_matmul_i4_impl_by_name(name: str) -> bool:
+    return bool(lib().tqhip_set_matmul_i4_impl_by_name(name.encode()))
+
+
+def matvec_i4_impl_name() -> str:
+    return lib().tqhip_matvec_i4_impl_name().decode()
+
+
+def available_matvec_i4_impls() -> str:
+    return lib().tqhip_available_matvec_i4_impls().decode()
+
+
+def available_matvec_vq2_impls() -> str:
+    return lib().tqhip_available_matvec_vq2_impls().decode()
+
+
+# ---- device buffers ----------------------------------------------------------------------------
+
+class DeviceBuffer:
+    """An HBM allocation owned by Python (hipMalloc / hipFree through the library)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = lib().tqhip_malloc(max(1, self.nbytes))
+        if not p:
+            raise MemoryError(f"hipMalloc({self.nbytes}) failed")
+        self.ptr = int(p)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(a.nbytes)
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise ValueError("array larger than buffer")
+        _check(lib().tqhip_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes), "hipMemcpy H2D")
+
+    def download(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        if out.nbytes > self.nbytes:
+            raise ValueError("read past buffer end")
+        _check(lib().tqhip_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes), "hipMemcpy D2H")
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().tqhip_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def device_count() -> int:
+    return int(lib().tqhip_device_count())
+
+
+def device_name() -> str:
+    buf = ctypes.create_string_buffer(256)
+    return buf.value.decode() if lib().tqhip_device_name(buf, 256) == 0 else "unknown"
+
+
+def synchronize() -> None:
+    _check(lib().tqhip_synchronize(), "hipDeviceSynchronize")
+
+
+def matvec_i4_dev(w, x, y, out_dim: int, in_dim: int, group_size: int, stream=None) -> None:
+    _check(lib().tqhip_matvec_i4_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, group_size, stream),
+           "tqhip_matvec_i4_dev")
+
+
+def matvec_i4_generic_dev(w, x, y, out_dim: int, in_dim: int, group_size: int, stream=None) -> None:
+    _check(lib().tqhip_matvec_i4_generic_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, group_size, stream),
+           "tqhip_matvec_i4_generic_dev")
+
+
+def matvec_vq2_dev(w, x, y, out_dim: int, in_dim: int, stream=None) -> None:
+    _check(lib().tqhip_matvec_vq2_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, stream), "tqhip_matvec_vq2_dev")
+
+
+def matmul_i4_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None) -> None:
+    _check(lib().tqhip_matmul_i4_dev(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size, stream),
+           "tqhip_matmul_i4_dev")
+
+
+class Stream:
+    def __init__(self):
+        p = lib().tqhip_stream_create()
+        if not p:
+            raise RuntimeError("hipStreamCreate failed")
+        self.ptr = int(p)
+
+    def synchronize(self) -> None:
+        _check(lib().tqhip_stream_synchronize(self.ptr), "hipStreamSynchronize")
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().tqhip_stream_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = lib().tqhip_event_create()
+        if not p:
+            raise RuntimeError("hipEventCreate failed")
+        self.ptr = int(p)
+
+    def record(self, stream: "Stream | None" = None) -> None:
+        _check(lib().tqhip_event_record(self.ptr, stream.ptr if stream else None), "hipEventRecord")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        _check(lib().tqhip_event_elapsed_ms(self.ptr, end.ptr, ctypes.byref(ms)), "hipEventElapsedTime")
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().tqhip_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+def run_ops(ops: list, repeats: int, stream: "Stream | None" = None) -> None:
+    arr = (Op * len(ops))(*ops)
+    _check(lib().tqhip_run_ops(arr, len(ops), repeats, stream.ptr if stream else None), "tqhip_run_ops")

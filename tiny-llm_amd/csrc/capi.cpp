@@ -1,0 +1,341 @@
+// capi.cpp -- the C ABI declared in include/tqhip.h, and the "hip" registry variants.
+//
+// Host-pointer calls follow the reference's GPU-variant boundary
+// (kernels/matvec/matvec_f16_cuda_resident_coal_ws.cu:88-159): weights are
+// copied to HBM once and cached by host pointer + byte size, x/y go through a
+// grow-only device workspace, and the call returns after y is back on the
+// host. One mutex guards the cache and workspace, so concurrent callers (the
+// reference's MoE expert pool calls mv from several threads) are serialised.
+
+#include "../../include/tqhip.h"
+
+#include <mutex>
+#include <unordered_map>
+
+#include "dispatch.h"
+#include "tq_common.h"
+
+namespace tqhip {
+namespace {
+
+struct DeviceCopy {
+    void *d = nullptr;
+    size_t bytes = 0;
+    uint64_t print = 0;
+};
+
+// Sampled content fingerprint (FNV-1a over up to 4 x 64 bytes). The cache is
+// keyed by host pointer, as in the reference's CUDA variants; the fingerprint
+// catches the common way that contract gets broken by accident: a freed
+// weight buffer whose address is reused for a different tensor of the same
+// size. It is not a full content check.
+uint64_t fingerprint(const void *host, size_t bytes) {
+    const unsigned char *p = static_cast<const unsigned char *>(host);
+    uint64_t h = 0xCBF29CE484222325ull ^ bytes;
+    const size_t n = bytes < 64 ? bytes : 64;
+    const size_t offs[4] = {0, bytes / 3, (2 * bytes) / 3, bytes - n};
+    for (size_t o : offs)
+        for (size_t i = 0; i < n && o + i < bytes; ++i) {
+            h ^= p[o + i];
+            h *= 0x100000001B3ull;
+        }
+    return h;
+}
+
+struct HostBoundary {
+    std::mutex mu;
+    std::unordered_map<const void *, DeviceCopy> weights;
+    float *dx = nullptr;
+    size_t x_cap = 0;
+    float *dy = nullptr;
+    size_t y_cap = 0;
+    hipStream_t stream = nullptr;
+
+    hipStream_t get_stream() {
+        if (!stream) TQ_HIP_CHECK(hipStreamCreate(&stream));  // default priority
+        return stream;
+    }
+    const uint8_t *resident(const void *host, size_t bytes) {
+        const uint64_t fp = fingerprint(host, bytes);
+        auto it = weights.find(host);
+        if (it != weights.end() && it->second.bytes == bytes && it->second.print == fp)
+            return static_cast<const uint8_t *>(it->second.d);
+        DeviceCopy &dc = weights[host];
+        if (dc.d && dc.bytes != bytes) {
+            TQ_HIP_CHECK(hipStreamSynchronize(get_stream()));
+            TQ_HIP_CHECK(hipFree(dc.d));
+            dc.d = nullptr;
+        }
+        if (!dc.d) TQ_HIP_CHECK(hipMalloc(&dc.d, bytes));
+        TQ_HIP_CHECK(hipMemcpy(dc.d, host, bytes, hipMemcpyHostToDevice));
+        dc.bytes = bytes;
+        dc.print = fp;
+        return static_cast<const uint8_t *>(dc.d);
+    }
+    float *ensure(float *&p, size_t &cap, size_t n) {
+        if (n > cap) {
+            if (p) TQ_HIP_CHECK(hipFree(p));
+            p = nullptr;
+            TQ_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&p), n * sizeof(float)));
+            cap = n;
+        }
+        return p;
+    }
+    void release() {
+        for (auto &kv : weights)
+            if (kv.second.d) TQ_HIP_CHECK(hipFree(kv.second.d));
+        weights.clear();
+    }
+};
+
+HostBoundary &boundary() {
+    static HostBoundary b;
+    return b;
+}
+
+void check_status(int st, const char *what) {
+    if (st == kOk) return;
+    const char *msg = st == kBadShape    ? "bad shape"
+                      : st == kBadGroup  ? "bad group_size"
+                      : st == kTooLarge  ? "shape too large"
+                                         : "kernel launch failed";
+    die(what, msg);
+}
+
+void upload(float *d, const float *h, size_t n, hipStream_t s) {
+    TQ_HIP_CHECK(hipMemcpyAsync(d, h, n * sizeof(float), hipMemcpyHostToDevice, s));
+}
+void download(float *h, const float *d, size_t n, hipStream_t s) {
+    TQ_HIP_CHECK(hipMemcpyAsync(h, d, n * sizeof(float), hipMemcpyDeviceToHost, s));
+}
+
+}  // namespace
+}  // namespace tqhip
+
+using namespace tqhip;
+
+extern "C" {
+
+void tqhip_matvec_i4(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size) {
+    if (out_dim < 1 || in_dim < 1 || group_size < 2 || (group_size & 1)) check_status(kBadShape, "tqhip_matvec_i4");
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    hipStream_t s = hb.get_stream();
+    const uint8_t *dw = hb.resident(w, static_cast<size_t>(out_dim) * i4_row_bytes(in_dim, group_size));
+    float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
+    float *dy = hb.ensure(hb.dy, hb.y_cap, out_dim);
+    upload(dx, x, in_dim, s);
+    check_status(launch_i4_matvec(dw, dx, dy, out_dim, in_dim, group_size, s), "tqhip_matvec_i4");
+    download(y, dy, out_dim, s);
+    TQ_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+void tqhip_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2, int out_dim,
+                          int in_dim, int group_size) {
+    if (out_dim < 1 || in_dim < 1 || group_size < 2 || (group_size & 1))
+        check_status(kBadShape, "tqhip_matvec_pair_i4");
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    hipStream_t s = hb.get_stream();
+    const size_t wb = static_cast<size_t>(out_dim) * i4_row_bytes(in_dim, group_size);
+    const uint8_t *d1 = hb.resident(w1, wb);
+    const uint8_t *d2 = hb.resident(w2, wb);
+    float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
+    float *dy = hb.ensure(hb.dy, hb.y_cap, 2 * static_cast<size_t>(out_dim));
+    upload(dx, x, in_dim, s);
+    check_status(launch_i4_matvec(d1, dx, dy, out_dim, in_dim, group_size, s), "tqhip_matvec_pair_i4");
+    check_status(launch_i4_matvec(d2, dx, dy + out_dim, out_dim, in_dim, group_size, s), "tqhip_matvec_pair_i4");
+    download(y1, dy, out_dim, s);
+    download(y2, dy + out_dim, out_dim, s);
+    TQ_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+void tqhip_matvec_qkv_i4(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x, float *yq,
+                         float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size) {
+    if (q_dim < 1 || kv_dim < 1 || in_dim < 1 || group_size < 2 || (group_size & 1))
+        check_status(kBadShape, "tqhip_matvec_qkv_i4");
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    hipStream_t s = hb.get_stream();
+    const size_t rb = i4_row_bytes(in_dim, group_size);
+    const uint8_t *dq = hb.resident(wq, static_cast<size_t>(q_dim) * rb);
+    const uint8_t *dk = hb.resident(wk, static_cast<size_t>(kv_dim) * rb);
+    const uint8_t *dv = hb.resident(wv, static_cast<size_t>(kv_dim) * rb);
+    float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
+    float *dy = hb.ensure(hb.dy, hb.y_cap, static_cast<size_t>(q_dim) + 2 * static_cast<size_t>(kv_dim));
+    upload(dx, x, in_dim, s);
+    check_status(launch_i4_matvec(dq, dx, dy, q_dim, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
+    check_status(launch_i4_matvec(dk, dx, dy + q_dim, kv_dim, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
+    check_status(launch_i4_matvec(dv, dx, dy + q_dim + kv_dim, kv_dim, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
+    download(yq, dy, q_dim, s);
+    download(yk, dy + q_dim, kv_dim, s);
+    download(yv, dy + q_dim + kv_dim, kv_dim, s);
+    TQ_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+void tqhip_matvec_vq2(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim) {
+    if (out_dim < 1 || in_dim < 4 || in_dim % 4) check_status(kBadShape, "tqhip_matvec_vq2");
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    hipStream_t s = hb.get_stream();
+    const uint8_t *dw = hb.resident(w, vq2_bytes(out_dim, in_dim));
+    float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
+    float *dy = hb.ensure(hb.dy, hb.y_cap, out_dim);
+    upload(dx, x, in_dim, s);
+    check_status(launch_vq2_matvec(dw, dx, dy, out_dim, in_dim, s), "tqhip_matvec_vq2");
+    download(y, dy, out_dim, s);
+    TQ_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+void tqhip_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size) {
+    if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) check_status(kBadShape, "tqhip_matmul_i4");
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    hipStream_t s = hb.get_stream();
+    const uint8_t *dw = hb.resident(w, static_cast<size_t>(M) * i4_row_bytes(K, group_size));
+    float *dx = hb.ensure(hb.dx, hb.x_cap, static_cast<size_t>(K) * N);
+    float *dy = hb.ensure(hb.dy, hb.y_cap, static_cast<size_t>(M) * N);
+    upload(dx, x, static_cast<size_t>(K) * N, s);
+    check_status(launch_i4_matmul(dw, dx, dy, M, K, N, group_size, s), "tqhip_matmul_i4");
+    download(y, dy, static_cast<size_t>(M) * N, s);
+    TQ_HIP_CHECK(hipStreamSynchronize(s));
+}
+
+void tqhip_release_weights(void) {
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    if (hb.stream) TQ_HIP_CHECK(hipStreamSynchronize(hb.stream));
+    hb.release();
+}
+
+int tqhip_matvec_i4_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                        void *stream) {
+    return launch_i4_matvec(w, x, y, out_dim, in_dim, group_size, static_cast<hipStream_t>(stream));
+}
+int tqhip_matvec_i4_generic_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                                void *stream) {
+    return launch_i4_matvec_generic(w, x, y, out_dim, in_dim, group_size, static_cast<hipStream_t>(stream));
+}
+int tqhip_matvec_vq2_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, void *stream) {
+    return launch_vq2_matvec(w, x, y, out_dim, in_dim, static_cast<hipStream_t>(stream));
+}
+int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                        void *stream) {
+    return launch_i4_matmul(w, x, y, M, K, N, group_size, static_cast<hipStream_t>(stream));
+}
+
+int tqhip_set_matvec_i4_impl_by_name(const char *name) { return tinyqwen::set_matvec_i4_impl_by_name(name) ? 1 : 0; }
+const char *tqhip_matvec_i4_impl_name(void) { return tinyqwen::matvec_i4_impl_name(); }
+const char *tqhip_available_matvec_i4_impls(void) { return tinyqwen::available_matvec_i4_impls(); }
+int tqhip_set_matvec_vq2_impl_by_name(const char *name) {
+    return tinyqwen::set_matvec_vq2_impl_by_name(name) ? 1 : 0;
+}
+const char *tqhip_matvec_vq2_impl_name(void) { return tinyqwen::matvec_vq2_impl_name(); }
+const char *tqhip_available_matvec_vq2_impls(void) { return tinyqwen::available_matvec_vq2_impls(); }
+int tqhip_set_matmul_i4_impl_by_name(const char *name) { return tinyqwen::set_matmul_i4_impl_by_name(name) ? 1 : 0; }
+void tqhip_dispatch_matvec_i4(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size) {
+    tinyqwen::matvec_i4(w, x, y, out_dim, in_dim, group_size);
+}
+void tqhip_dispatch_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2,
+                                   int out_dim, int in_dim, int group_size) {
+    tinyqwen::matvec_pair_i4(w1, w2, x, y1, y2, out_dim, in_dim, group_size);
+}
+void tqhip_dispatch_matvec_qkv_i4(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x, float *yq,
+                                  float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size) {
+    tinyqwen::matvec_qkv_i4(wq, wk, wv, x, yq, yk, yv, q_dim, kv_dim, in_dim, group_size);
+}
+void tqhip_dispatch_matvec_vq2(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim) {
+    tinyqwen::matvec_vq2(w, x, y, out_dim, in_dim);
+}
+void tqhip_dispatch_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size) {
+    tinyqwen::matmul_i4(w, x, y, M, K, N, group_size);
+}
+void tqhip_dispatch_matmul_vq2(const uint8_t *w, const float *x, float *y, int M, int K, int N) {
+    tinyqwen::matmul_vq2(w, x, y, M, K, N);
+}
+
+size_t tqhip_i4_row_bytes(int in_dim, int group_size) { return i4_row_bytes(in_dim, group_size); }
+size_t tqhip_vq2_tensor_bytes(int rows, int cols) { return vq2_bytes(rows, cols); }
+
+int tqhip_device_count(void) {
+    int n = 0;
+    return hipGetDeviceCount(&n) == hipSuccess ? n : 0;
+}
+int tqhip_device_name(char *buf, int len) {
+    hipDeviceProp_t p;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return -1;
+    std::snprintf(buf, static_cast<size_t>(len), "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return 0;
+}
+void *tqhip_malloc(size_t bytes) {
+    void *p = nullptr;
+    return hipMalloc(&p, bytes) == hipSuccess ? p : nullptr;
+}
+int tqhip_free(void *p) { return hipFree(p) == hipSuccess ? 0 : -1; }
+int tqhip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) == hipSuccess ? 0 : -1;
+}
+int tqhip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+int tqhip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice) == hipSuccess ? 0 : -1;
+}
+int tqhip_memset(void *dst, int value, size_t bytes) { return hipMemset(dst, value, bytes) == hipSuccess ? 0 : -1; }
+int tqhip_synchronize(void) { return hipDeviceSynchronize() == hipSuccess ? 0 : -1; }
+void *tqhip_stream_create(void) {
+    hipStream_t s = nullptr;
+    return hipStreamCreate(&s) == hipSuccess ? static_cast<void *>(s) : nullptr;
+}
+int tqhip_stream_destroy(void *stream) {
+    return hipStreamDestroy(static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -1;
+}
+int tqhip_stream_synchronize(void *stream) {
+    return hipStreamSynchronize(static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -1;
+}
+void *tqhip_event_create(void) {
+    hipEvent_t e = nullptr;
+    return hipEventCreate(&e) == hipSuccess ? static_cast<void *>(e) : nullptr;
+}
+int tqhip_event_destroy(void *event) { return hipEventDestroy(static_cast<hipEvent_t>(event)) == hipSuccess ? 0 : -1; }
+int tqhip_event_record(void *event, void *stream) {
+    return hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -1;
+}
+int tqhip_event_elapsed_ms(void *start, void *stop, float *ms) {
+    if (hipEventSynchronize(static_cast<hipEvent_t>(stop)) != hipSuccess) return -1;
+    return hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)) == hipSuccess ? 0
+                                                                                                                 : -1;
+}
+
+int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int r = 0; r < repeats; ++r) {
+        for (int i = 0; i < n_ops; ++i) {
+            const tqhip_op &op = ops[i];
+            int st = kBadShape;
+            const uint8_t *w = static_cast<const uint8_t *>(op.w);
+            switch (op.kind) {
+                case TQHIP_OP_I4_MATVEC:
+                    st = launch_i4_matvec(w, op.x, op.y, op.out_dim, op.in_dim, op.group_size, s);
+                    break;
+                case TQHIP_OP_VQ2_MATVEC: st = launch_vq2_matvec(w, op.x, op.y, op.out_dim, op.in_dim, s); break;
+                case TQHIP_OP_I4_MATMUL:
+                    st = launch_i4_matmul(w, op.x, op.y, op.out_dim, op.in_dim, op.n, op.group_size, s);
+                    break;
+                default: break;
+            }
+            if (st != kOk) return st;
+        }
+    }
+    return kOk;
+}
+
+}  // extern "C"
+
+// Self-registration as the "hip" variants (kernels/dispatch.h:459-474 idiom).
+TINYQWEN_MATVEC_I4_VARIANT(tqhip_matvec_i4, "hip");
+TINYQWEN_MATVEC_I4_PAIR_VARIANT(tqhip_matvec_pair_i4, "hip");
+TINYQWEN_MATVEC_QKV_I4_VARIANT(tqhip_matvec_qkv_i4, "hip");
+TINYQWEN_MATVEC_VQ2_VARIANT(tqhip_matvec_vq2, "hip");
+TINYQWEN_MATMUL_I4_VARIANT(tqhip_matmul_i4, "hip");

@@ -1,0 +1,63 @@
+// tq_common.h -- shared definitions for the MI355X quantized-projection library.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+#include <hip/hip_runtime.h>
+
+namespace tqhip {
+
+// i4 group layout (runtime/tiny_format.h:58-78 of the reference):
+//   [scale fp16 | zero fp16 | group_size/2 bytes of codes], low nibble = even element.
+constexpr int kI4Header = 4;
+
+// VQ2 layout (runtime/tiny_format.h:80-103): [codebook 256 x 4 fp16][rows x cols/4 u8].
+constexpr int kVq2Dim = 4;
+constexpr int kVq2Entries = 256;
+constexpr int kVq2CodebookBytes = kVq2Entries * kVq2Dim * 2;
+
+inline int i4_group_bytes(int group_size) { return kI4Header + group_size / 2; }
+inline int i4_groups(int in_dim, int group_size) { return (in_dim + group_size - 1) / group_size; }
+inline size_t i4_row_bytes(int in_dim, int group_size) {
+    return static_cast<size_t>(i4_groups(in_dim, group_size)) * i4_group_bytes(group_size);
+}
+inline size_t vq2_bytes(int rows, int cols) {
+    return kVq2CodebookBytes + static_cast<size_t>(rows) * (static_cast<size_t>(cols) / kVq2Dim);
+}
+
+// Fail fast, as the reference's GPU variants do (TINYQWEN_CUDA_CHECK +
+// abort): the dispatch signatures have no error return.
+[[noreturn]] inline void die(const char *what, const char *detail) {
+    std::fprintf(stderr, "tqhip: %s: %s\n", what, detail);
+    std::fflush(stderr);
+    std::abort();
+}
+
+inline void check_hip(hipError_t e, const char *what) {
+    if (e != hipSuccess) die(what, hipGetErrorString(e));
+}
+
+#define TQ_HIP_CHECK(expr) ::tqhip::check_hip((expr), #expr)
+
+// Error codes returned by the device-pointer entry points.
+enum Status : int {
+    kOk = 0,
+    kBadShape = -1,      // a dimension is < 1, or in_dim % 4 != 0 for VQ2
+    kBadGroup = -2,      // group_size is odd or < 2
+    kTooLarge = -3,      // a byte offset does not fit the 32-bit buffer range
+    kLaunchFailed = -4,  // hipGetLastError after the launch was not hipSuccess
+};
+
+// Device-pointer launchers (defined in the .hip files). All return a Status.
+int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                     hipStream_t stream);
+int launch_i4_matvec_generic(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim,
+                             int group_size, hipStream_t stream);
+int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
+int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                     hipStream_t stream);
+
+}  // namespace tqhip
