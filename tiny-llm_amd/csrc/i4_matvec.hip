@@ -19,12 +19,14 @@
 //   * Every lane works on the same 16-byte column of every row ("window"
 //     offsets are row-invariant), so the activation operand, its group masks
 //     and the per-group constants are built once per workgroup into VGPRs.
-//   * A workgroup owns a contiguous range of 16-row tiles; each tile is one
-//     contiguous block of memory. The tile is streamed into LDS with
-//     coalesced 1 KB-per-instruction loads kept two tiles ahead in VGPRs,
-//     double-buffered in LDS, and the MFMA operands (codes and group headers)
-//     are read back from LDS. The row windows are split over the waves and the
+//   * Workgroups take 16-row tiles round-robin; each tile is one contiguous
+//     block of memory. The tile goes global -> LDS with 1 KB-per-instruction
+//     DMA loads (buffer_load ... lds) into a ring of 3..8 tile buffers, the
+//     first tiles being issued before the activation set-up so HBM is busy
+//     from the start; the MFMA operands (codes and group headers) are read
+//     back from LDS. The row windows are split over the waves and the
 //     per-wave partial sums are added in a fixed order (deterministic).
+//     (i4_matvec_lds is the same scheme staged through VGPRs instead.)
 //   * Rows longer than 48 windows use the register-only variant, which loads
 //     the operands straight from HBM.
 // Portable path (any even G): one wave per row, fp32 accumulation.
@@ -43,6 +45,22 @@ constexpr int kTile = 16;      // weight rows per MFMA tile
 constexpr int kPiece = 1024;   // bytes one wave streams per 16-byte-per-lane load
 constexpr unsigned kNibbles = 0x0F0F0F0Fu;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family word 3)
+#ifndef TQ_LDS_DEPTH
+#define TQ_LDS_DEPTH 1  // tiles in flight per workgroup beyond the one in LDS
+#endif
+#ifndef TQ_WAVES_PER_CU
+#define TQ_WAVES_PER_CU 16  // resident waves per CU the staged kernel's grid aims for
+#endif
+constexpr int kWavesPerCu = TQ_WAVES_PER_CU;
+#ifndef TQ_DMA_INFLIGHT_KB
+#define TQ_DMA_INFLIGHT_KB 96  // weight bytes in flight per CU the DMA ring aims for
+#endif
+constexpr size_t kInflightPerCu = static_cast<size_t>(TQ_DMA_INFLIGHT_KB) * 1024;
+constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
+constexpr int kMaxDepth = 8;              // DMA ring slots at most
+#ifndef TQ_USE_DMA
+#define TQ_USE_DMA 1  // stage tiles with global->LDS DMA (else through VGPRs)
+#endif
 
 // DPP controls (gfx9): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_ror:8, row_shr:n.
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppRor8 = 0x128;
@@ -97,26 +115,115 @@ struct Geom {
     int M, K, G, gb, Gr, row_bytes, T, NW;
     int rbp;      // LDS row pitch of a staged tile (>= row_bytes, odd multiple of 16)
     int pieces;   // 1 KB pieces per staged tile
+    int xoff;     // LDS byte offset of the activation set-up (staged kernel)
+    int tbuf;     // bytes of one DMA tile buffer (DMA-staged kernel)
+    int depth;    // DMA ring slots (DMA-staged kernel)
 };
 
-// LDS view of the activation set-up shared by both kernels.
+// LDS view of an activation set-up: groups gbase .. gbase+n-1 (the whole
+// vector for a workgroup-wide set-up, or the few groups one wave's windows
+// touch for a wave-local one).
 struct XPlanes {
-    int8_t *pl;    // 3 planes x Kp bytes, 8-element blocks in operand order
+    int8_t *pl;    // 3 planes x stride bytes, 8-element blocks in operand order
     int *pre;      // per group: inclusive prefix over its 8-element blocks of sum(X)
     float *gexp;   // 2^-f per group
+    int stride;    // bytes per plane
+    int gbase;     // first group held
+    int ngroups;   // groups held
 };
+
+// Wave-local set-up: 64 lanes x 8 elements cover the (at most 8) groups of G=64
+// or (at most 4) groups of G=128 that one wave's <= 3 windows touch.
+constexpr int kWaveXBytes = 3 * 64 * 8 + 64 * 4 + 8 * 4;  // planes + prefixes + exponents
+
+// The first 8-element block of activations each thread converts (fast path):
+// loaded at kernel entry, ahead of the weight stream, so its latency is not
+// stretched by the tile loads queued behind it.
+struct XFirst {
+    float v[8];
+};
+
+template <int GT>
+__device__ inline void load_x_first(XFirst &xf, const float *__restrict__ x, int K, int Kp) {
+    if constexpr (GT == 64 || GT == 128) {
+        // branch-free (clamped address, then masked) so the compiler can wait
+        // for exactly these loads while weight DMAs issued after them are pending
+        // clamped index, then masked: indices at or past K (threads past Kp
+        // included, as Kp >= K) give 0. The loads stay scalar-element loads so
+        // no wide load straddles the end of x.
+        const int b = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int k = 8 * b + i;
+            const float v = x[min(k, K - 1)];
+            xf.v[i] = k < K ? v : 0.f;
+        }
+        (void)Kp;
+    }
+}
+
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+
+__device__ inline unsigned lds_addr(const void *p) {
+    return static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)p));
+}
+
+// LDS reads the compiler does not see as such: it would otherwise wait for
+// every global->LDS transfer in flight before them (it cannot tell that these
+// addresses are not among the transfers' targets). Complete on return.
+__device__ inline float4 lds_read_f4(const float *p) {
+    float4 v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return v;
+}
+
+__device__ inline void lds_read4_u2(const int8_t *const (&p)[4], v2u (&v)[4]) {
+    asm volatile(
+        "ds_read_b64 %0, %4\n\tds_read_b64 %1, %5\n\tds_read_b64 %2, %6\n\tds_read_b64 %3, %7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+        : "v"(lds_addr(p[0])), "v"(lds_addr(p[1])), "v"(lds_addr(p[2])), "v"(lds_addr(p[3]))
+        : "memory");
+}
+
+__device__ inline void lds_read3_u32(const int *p1, const int *p0, const int *p2, int &v1, int &v0, float &v2) {
+    int r2;
+    asm volatile("ds_read_b32 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(v1), "=&v"(v0), "=&v"(r2)
+                 : "v"(lds_addr(p1)), "v"(lds_addr(p0)), "v"(lds_addr(p2))
+                 : "memory");
+    v2 = __builtin_bit_cast(float, r2);
+}
+
+// LDS stores the compiler does not see as such (same reason); they complete
+// before the next s_waitcnt lgkmcnt(0), which every barrier here includes.
+__device__ inline void lds_write3_u2(const void *p, int stride, v2u a, v2u b, v2u c) {
+    const unsigned o = lds_addr(p);
+    asm volatile("ds_write_b64 %0, %1\n\tds_write_b64 %2, %3\n\tds_write_b64 %4, %5"
+                 :
+                 : "v"(o), "v"(a), "v"(o + stride), "v"(b), "v"(o + 2 * stride), "v"(c)
+                 : "memory");
+}
+
+__device__ inline void lds_write_u32(const void *p, unsigned v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(lds_addr(p)), "v"(v) : "memory");
+}
 
 // ---- 1. activations -> per-group exponent, integer planes, prefix block sums
 // GT = 64 or 128: one lane per 8-element block, group max and prefix by DPP.
-template <int GT>
-__device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K, int Gr, int Kp) {
+// ONE_ROUND: the caller guarantees Kp / 8 <= blockDim.x, so only the values
+// already loaded by load_x_first are used (no further global loads here), and
+// the LDS stores go through lds_write_* (global->LDS transfers may be in
+// flight, and the compiler would wait for all of them before each store).
+template <int GT, bool ONE_ROUND = false>
+__device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K, int Gr, int Kp, const XFirst &xf) {
     if constexpr (GT == 64 || GT == 128) {
         constexpr int LPG = GT / 8;  // lanes (blocks) per group: 8 or 16
         const int nblk = Kp / 8;
         // every lane of a block-group takes part in the DPP steps, so the loop
         // runs whole waves and masks work past the last block instead
         const int stride = blockDim.x;
-        const int nrounds = (nblk + stride - 1) / stride;
+        const int nrounds = ONE_ROUND ? 1 : (nblk + stride - 1) / stride;
         const int lane = threadIdx.x & 63;
         for (int rd = 0; rd < nrounds; ++rd) {
             const int b = rd * stride + threadIdx.x;
@@ -126,7 +233,10 @@ __device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K,
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int k = 8 * b + i;
-                v[i] = (live && k < K) ? x[k] : 0.f;
+                if (ONE_ROUND || rd == 0)
+                    v[i] = xf.v[i];
+                else
+                    v[i] = (live && k < K) ? x[k] : 0.f;
                 m = fmaxf(m, fabsf(v[i]));
             }
             m = fmaxf(m, dpp_f<kDppXor1>(m));
@@ -160,11 +270,18 @@ __device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K,
                 s += (j >= 8) ? t : 0;
             }
             if (live) {
+                if constexpr (ONE_ROUND) {
+                    lds_write3_u2(xp.pl + 8 * b, Kp, v2u{w[0][0], w[0][1]}, v2u{w[1][0], w[1][1]},
+                                  v2u{w[2][0], w[2][1]});
+                    lds_write_u32(xp.pre + b, static_cast<unsigned>(s));
+                    if (j == 0) lds_write_u32(xp.gexp + b / LPG, __builtin_bit_cast(unsigned, ldexpf(1.f, -f)));
+                } else {
 #pragma unroll
-                for (int p = 0; p < 3; ++p)
-                    *reinterpret_cast<uint2 *>(xp.pl + p * Kp + 8 * b) = make_uint2(w[p][0], w[p][1]);
-                xp.pre[b] = s;
-                if (j == 0) xp.gexp[b / LPG] = ldexpf(1.f, -f);
+                    for (int p = 0; p < 3; ++p)
+                        *reinterpret_cast<uint2 *>(xp.pl + p * Kp + 8 * b) = make_uint2(w[p][0], w[p][1]);
+                    xp.pre[b] = s;
+                    if (j == 0) xp.gexp[b / LPG] = ldexpf(1.f, -f);
+                }
             }
         }
     } else {
@@ -210,14 +327,72 @@ __device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K,
     }
 }
 
+// Wave-local variant of prepare_x (GT = 64 or 128): lane l converts block l of
+// groups gfirst, gfirst+1, ... into this wave's own LDS slice. No barrier is
+// needed before build_operands: the same wave reads what it wrote.
+template <int GT>
+__device__ void prepare_x_wave(const XPlanes &xp, const float *__restrict__ x, int K, int Gr, const XFirst &xf) {
+    constexpr int LPG = GT / 8;
+    const int lane = threadIdx.x & 63;
+    const int j = lane & (LPG - 1);
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(xf.v[i]));
+    m = fmaxf(m, dpp_f<kDppXor1>(m));
+    m = fmaxf(m, dpp_f<kDppXor2>(m));
+    m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
+    if constexpr (LPG == 16) m = fmaxf(m, dpp_f<kDppRor8>(m));
+    const int f = group_exponent(m);
+    unsigned w[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int X = static_cast<int>(rintf(ldexpf(xf.v[i], f)));
+        sum += X;
+        int d[3];
+        planes_of(X, d[0], d[1], d[2]);
+        const int word = i & 1, byte = i >> 1;  // even elements -> first dword
+#pragma unroll
+        for (int p = 0; p < 3; ++p) w[p][word] |= (static_cast<unsigned>(d[p]) & 0xFFu) << (8 * byte);
+    }
+    int s = sum, t;
+    t = dpp_i<kDppShr1>(s);
+    s += (j >= 1) ? t : 0;
+    t = dpp_i<kDppShr2>(s);
+    s += (j >= 2) ? t : 0;
+    t = dpp_i<kDppShr4>(s);
+    s += (j >= 4) ? t : 0;
+    if constexpr (LPG == 16) {
+        t = dpp_i<kDppShr8>(s);
+        s += (j >= 8) ? t : 0;
+    }
+#pragma unroll
+    for (int p = 0; p < 3; ++p) *reinterpret_cast<uint2 *>(xp.pl + p * xp.stride + 8 * lane) = make_uint2(w[p][0], w[p][1]);
+    xp.pre[lane] = s;
+    if (j == 0) xp.gexp[lane / LPG] = ldexpf(1.f, -f);
+}
+
+// The 8 activations lane l of a wave-local set-up converts: block l of the
+// groups starting at gfirst (zeros past the vector end).
+template <int GT>
+__device__ inline void load_x_wave(XFirst &xf, const float *__restrict__ x, int K, int Gr, int gfirst) {
+    const int lane = threadIdx.x & 63;
+    const int g = gfirst + lane / (GT / 8);
+    const int k0 = g * GT + 8 * (lane & (GT / 8 - 1));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xf.v[i] = (g < Gr && k0 + i < K) ? x[k0 + i] : 0.f;
+}
+
 // ---- 2. per-lane, row-invariant activation operands and group constants for
 // windows t0 .. t0+nch-1 (CPW slots; unused slots get a zero operand).
-template <int GT, int CPW>
+// HIDDEN: read LDS through lds_read_* (needed where global->LDS transfers are
+// in flight, which the compiler would otherwise wait for before every read).
+template <int GT, int CPW, bool HIDDEN = false>
 __device__ void build_operands(const XPlanes &xp, const Geom &gm, int t0, int nch, v4i (&A0)[CPW], v4i (&A1)[CPW],
                                float (&E)[CPW], float (&C)[CPW], int (&HO)[CPW], unsigned (&HM)[CPW]) {
     const int G = GT ? GT : gm.G;
     const int gb = GT ? kI4Header + GT / 2 : gm.gb;
-    const int Gr = gm.Gr, rb = gm.row_bytes, Kp = Gr * G;
+    const int Gr = gm.Gr, rb = gm.row_bytes;
     const int lane = threadIdx.x & 63;
     const int am = lane & 15;  // activation-operand row = 4*slot + plane
     const int ah = am >> 2, ap = am & 3;
@@ -230,16 +405,28 @@ __device__ void build_operands(const XPlanes &xp, const Geom &gm, int t0, int nc
         const int gt = (kChunk * t) / gb;  // group holding the window's first byte
         // activation operand: all reads are issued unconditionally, then masked
         unsigned lo[4], hi[4];
+        const int8_t *src[4];
+        bool use[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {  // q = 2*u + dw
             const int o = kChunk * t + 4 * (4 * kq + q);
             const int g = o / gb;
             const int r = o - g * gb;
-            const bool use = own && o < rb && ap < 3 && r >= kI4Header && g - gt == ah;
-            const int blk = use ? (g * G + 2 * (r - kI4Header)) >> 3 : 0;
-            const uint2 v = *reinterpret_cast<const uint2 *>(xp.pl + apc * Kp + 8 * blk);
-            lo[q] = use ? v.x : 0u;
-            hi[q] = use ? v.y : 0u;
+            use[q] = own && o < rb && ap < 3 && r >= kI4Header && g - gt == ah;
+            const int blk = use[q] ? ((g - xp.gbase) * G + 2 * (r - kI4Header)) >> 3 : 0;  // local block
+            src[q] = xp.pl + apc * xp.stride + 8 * blk;
+        }
+        v2u v[4];
+        if constexpr (HIDDEN) {
+            lds_read4_u2(src, v);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = *reinterpret_cast<const v2u *>(src[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            lo[q] = use[q] ? v[q].x : 0u;
+            hi[q] = use[q] ? v[q].y : 0u;
         }
         A0[c] = v4i{static_cast<int>(lo[0]), static_cast<int>(hi[0]), static_cast<int>(lo[1]), static_cast<int>(hi[1])};
         A1[c] = v4i{static_cast<int>(lo[2]), static_cast<int>(hi[2]), static_cast<int>(lo[3]), static_cast<int>(hi[3])};
@@ -249,12 +436,23 @@ __device__ void build_operands(const XPlanes &xp, const Geom &gm, int t0, int nc
         const int dbeg = max(gq * gb + kI4Header, wbeg), dend = min((gq + 1) * gb, wend);
         const bool valid = own && gq < Gr && gq * gb < wend;
         int sum = 0;
-        if (valid && dend > dbeg) {
-            const int b0 = gq * (G / 8) + (dbeg - gq * gb - kI4Header) / 4;  // first block in the window
-            const int b1 = gq * (G / 8) + (dend - gq * gb - kI4Header) / 4;  // one past the last
-            sum = xp.pre[b1 - 1] - (b0 > gq * (G / 8) ? xp.pre[b0 - 1] : 0);
+        const int gl = min(max(gq - xp.gbase, 0), xp.ngroups - 1);  // local group (clamped when invalid)
+        const bool data = valid && dend > dbeg;
+        const int b0 = gl * (G / 8) + (dbeg - gq * gb - kI4Header) / 4;  // first block in the window
+        const int b1 = gl * (G / 8) + (dend - gq * gb - kI4Header) / 4;  // one past the last
+        float ge;
+        if constexpr (HIDDEN) {
+            // unconditional reads at clamped in-range indices, then masked
+            const int nb = xp.ngroups * (G / 8);
+            int p1, p0;
+            lds_read3_u32(xp.pre + min(max(b1 - 1, 0), nb - 1), xp.pre + min(max(b0 - 1, 0), nb - 1),
+                          reinterpret_cast<const int *>(xp.gexp + gl), p1, p0, ge);
+            if (data) sum = p1 - (b0 > gl * (G / 8) ? p0 : 0);
+        } else {
+            if (data) sum = xp.pre[b1 - 1] - (b0 > gl * (G / 8) ? xp.pre[b0 - 1] : 0);
+            ge = xp.gexp[gl];
         }
-        E[c] = valid ? xp.gexp[min(gq, Gr - 1)] : 0.f;
+        E[c] = valid ? ge : 0.f;
         C[c] = static_cast<float>(sum) * E[c];
         HO[c] = valid ? gq * gb : 0;
         HM[c] = valid ? 0xFFFFFFFFu : 0u;
@@ -283,7 +481,7 @@ __device__ __forceinline__ float window_step(float a, const v4i &d, unsigned h, 
 }
 
 __device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const uint8_t *w, int M, int row_bytes, int row0) {
-    const size_t rem = static_cast<size_t>(M - row0) * row_bytes;
+    const size_t rem = row0 < M ? static_cast<size_t>(M - row0) * row_bytes : 0;  // past the end: every load reads 0
     const int nrec = rem > 0xFFFFFFFFull ? -1 : static_cast<int>(static_cast<unsigned>(rem));
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w) + static_cast<size_t>(row0) * row_bytes,
                                              static_cast<short>(0), nrec, kBufferFlags);
@@ -293,8 +491,8 @@ __device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const uint8_t *w, int M, int 
 // LDS-staged kernel (rows of up to 48 windows).
 //   GT: compile-time group size (0 = run time). CPW: windows per wave.
 //   PW: 1 KB pieces per wave per tile. NWMAX: waves per workgroup bound.
-template <int GT, int CPW, int PW, int NWMAX>
-__global__ __launch_bounds__(64 * NWMAX, 4) void i4_matvec_lds(const uint8_t *__restrict__ w,
+template <int GT, int CPW, int PW, int NWMAX, int DEPTH>
+__global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_lds(const uint8_t *__restrict__ w,
                                                                const float *__restrict__ x, float *__restrict__ y,
                                                                Geom gm) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -309,15 +507,40 @@ __global__ __launch_bounds__(64 * NWMAX, 4) void i4_matvec_lds(const uint8_t *__
 
     unsigned char *stage = smem;                                         // [2][tbuf]
     float *part = reinterpret_cast<float *>(smem + 2 * tbuf);            // [2][16][NWP]
+    // The activation set-up lives in stage buffer 1 (free until tile 1 is
+    // stashed after the first barrier of the loop), or after part if too big.
+    // G = 64 / 128: each wave converts just the groups its windows touch into
+    // its own 2 KB slice; otherwise the workgroup converts the whole vector.
+    constexpr bool kWaveLocal = GT == 64 || GT == 128;
+    const int t0 = (gm.T * wave) / NW;
+    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
+    const int gfirst = (kChunk * t0) / (GT ? kI4Header + GT / 2 : gm.gb);
     XPlanes xp;
-    xp.pl = reinterpret_cast<int8_t *>(part + 2 * kTile * NWP);
-    xp.pre = reinterpret_cast<int *>(xp.pl + 3 * Kp);
-    xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
+    XFirst xf;
+    if constexpr (kWaveLocal) {
+        xp.pl = reinterpret_cast<int8_t *>(smem + gm.xoff + wave * kWaveXBytes);
+        xp.stride = 64 * 8;
+        xp.pre = reinterpret_cast<int *>(xp.pl + 3 * xp.stride);
+        xp.gexp = reinterpret_cast<float *>(xp.pre + 64);
+        xp.gbase = gfirst;
+        xp.ngroups = 64 / (G / 8);
+        load_x_wave<GT>(xf, x, gm.K, gm.Gr, gfirst);
+    } else {
+        xp.pl = reinterpret_cast<int8_t *>(smem + gm.xoff);
+        xp.stride = Kp;
+        xp.pre = reinterpret_cast<int *>(xp.pl + 3 * Kp);
+        xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
+        xp.gbase = 0;
+        xp.ngroups = gm.Gr;
+        load_x_first<GT>(xf, x, gm.K, Kp);
+    }
 
+    // Tiles are dealt round-robin (tile = blockIdx.x + i*gridDim.x): at any
+    // moment the whole grid streams one neighbourhood of the matrix, which
+    // HBM serves markedly faster than one distant range per workgroup.
     const int tiles = (M + kTile - 1) / kTile;
-    const int my0 = static_cast<int>(static_cast<long long>(tiles) * blockIdx.x / gridDim.x);
-    const int my1 = static_cast<int>(static_cast<long long>(tiles) * (blockIdx.x + 1) / gridDim.x);
-    const int ntile = my1 - my0;
+    const int ntile = blockIdx.x < static_cast<unsigned>(tiles) ? (tiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+    auto tile_of = [&](int i) { return static_cast<int>(blockIdx.x + static_cast<unsigned>(i) * gridDim.x); };
 
     // Pieces of a tile this lane moves: tile-relative byte offset and its LDS
     // destination (row-padded). Identical for every tile.
@@ -359,16 +582,18 @@ __global__ __launch_bounds__(64 * NWMAX, 4) void i4_matvec_lds(const uint8_t *__
         }
     };
 
-    // Tiles my0 and my0+1 start streaming before the activation set-up.
+    // The first tiles start streaming before the activation set-up.
     v4i V0[PW], V1[PW];
-    if (ntile > 0) issue(V0, my0);
-    if (ntile > 1) issue(V1, my0 + 1);
+    if (ntile > 0) issue(V0, tile_of(0));
+    if (DEPTH == 2 && ntile > 1) issue(V1, tile_of(1));
 
-    prepare_x<GT>(xp, x, gm.K, gm.Gr, Kp);
-    __syncthreads();
+    if constexpr (kWaveLocal) {
+        prepare_x_wave<GT>(xp, x, gm.K, gm.Gr, xf);
+    } else {
+        prepare_x<GT>(xp, x, gm.K, gm.Gr, Kp, xf);
+        __syncthreads();
+    }
 
-    const int t0 = (gm.T * wave) / NW;
-    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
     v4i A0[CPW], A1[CPW];
     float E[CPW], C[CPW];
     int HO[CPW];
@@ -385,7 +610,8 @@ __global__ __launch_bounds__(64 * NWMAX, 4) void i4_matvec_lds(const uint8_t *__
     }
 
     if (ntile > 0) stash(V0, stage);
-    if (ntile > 2) issue(V0, my0 + 2);
+    if (DEPTH == 2 && ntile > 2) issue(V0, tile_of(2));
+    if (DEPTH == 1 && ntile > 1) issue(V0, tile_of(1));
 
     auto reduce_prev = [&](int i) {  // partial sums of tile i (written before the last barrier)
         const float *pb = part + (i & 1) * (kTile * NWP);
@@ -399,7 +625,7 @@ __global__ __launch_bounds__(64 * NWMAX, 4) void i4_matvec_lds(const uint8_t *__
                 s += v.z;
                 s += v.w;
             }
-            const int row = (my0 + i) * kTile + threadIdx.x;
+            const int row = tile_of(i) * kTile + threadIdx.x;
             if (row < M) y[row] = s;
         }
     };
@@ -420,21 +646,197 @@ __global__ __launch_bounds__(64 * NWMAX, 4) void i4_matvec_lds(const uint8_t *__
 
     for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x) part[i] = 0.f;
 
-    // Pipeline: tile i is in LDS buffer i&1, tile i+1 in VGPRs (V1/V0 by parity),
+    if constexpr (DEPTH == 1) {
+        // tile i in LDS buffer i&1, tile i+1 in flight into V0
+        for (int i = 0; i < ntile; ++i) {
+            __syncthreads();
+            if (i + 1 < ntile) stash(V0, stage + ((i + 1) & 1) * tbuf);
+            if (i + 2 < ntile) issue(V0, tile_of(i + 2));
+            compute(i);
+            if (i > 0) reduce_prev(i - 1);
+        }
+        __syncthreads();
+        if (ntile > 0) reduce_prev(ntile - 1);
+        return;
+    }
+    // DEPTH 2: tile i is in LDS buffer i&1, tile i+1 in VGPRs (V1/V0 by parity),
     // tile i+2 being fetched.
     for (int i = 0; i < ntile; i += 2) {
         __syncthreads();
         if (i + 1 < ntile) stash(V1, stage + tbuf);
-        if (i + 3 < ntile) issue(V1, my0 + i + 3);
+        if (i + 3 < ntile) issue(V1, tile_of(i + 3));
         compute(i);
         if (i > 0) reduce_prev(i - 1);
         if (i + 1 >= ntile) break;
         __syncthreads();
         if (i + 2 < ntile) stash(V0, stage);
-        if (i + 4 < ntile) issue(V0, my0 + i + 4);
+        if (i + 4 < ntile) issue(V0, tile_of(i + 4));
         compute(i + 1);
         reduce_prev(i);
     }
+    __syncthreads();
+    if (ntile > 0) reduce_prev(ntile - 1);
+}
+
+// ============================================================================================
+// DMA-staged kernel (rows of up to 48 windows): like i4_matvec_lds, but tiles
+// go global -> LDS directly (buffer_load ... lds, 16 bytes per lane) into a
+// ring of D tile buffers (D = gm.depth, 3..8, picked on the host from the LDS
+// budget), so D tiles are in flight while the activation set-up runs and
+// D - 1 while a tile is contracted, without spending VGPRs on the staging.
+// Waits on the transfers are explicit (vmcnt counts of whole tiles).
+__device__ __forceinline__ void wait_vmem(int n) {
+    // s_waitcnt vmcnt(n) with expcnt/lgkmcnt left free (gfx9 encoding)
+    switch (n) {
+#define TQ_VMWAIT(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); break;
+        TQ_VMWAIT(0) TQ_VMWAIT(1) TQ_VMWAIT(2) TQ_VMWAIT(3) TQ_VMWAIT(4) TQ_VMWAIT(5) TQ_VMWAIT(6) TQ_VMWAIT(7)
+        TQ_VMWAIT(8) TQ_VMWAIT(9) TQ_VMWAIT(10) TQ_VMWAIT(11) TQ_VMWAIT(12) TQ_VMWAIT(13) TQ_VMWAIT(14)
+        TQ_VMWAIT(15) TQ_VMWAIT(16) TQ_VMWAIT(17) TQ_VMWAIT(18) TQ_VMWAIT(19) TQ_VMWAIT(20) TQ_VMWAIT(21)
+        TQ_VMWAIT(22) TQ_VMWAIT(23) TQ_VMWAIT(24) TQ_VMWAIT(25) TQ_VMWAIT(26) TQ_VMWAIT(27) TQ_VMWAIT(28)
+#undef TQ_VMWAIT
+        default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break;
+    }
+}
+
+// Global->LDS copy of one tile: each of this wave's PW DMAs moves 1 KB
+// (16 bytes per lane, source byte poff[s], landing at dst + pdst[s] + 16*lane).
+// (Not a template: clang's host pass rejected the template form in the kernel
+// and silently dropped the kernel's host stub. pw is a constant at every call.)
+// Every lane of every DMA is live (no branch), so the compiler can count the
+// transfers issued after earlier loads and the per-wave count is exactly pw.
+__device__ __forceinline__ void dma_tile(const uint8_t *w, int M, int rb, int tile, unsigned char *dst, const int *poff,
+                                         const int *pdst, int pw) {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(w, M, rb, tile * kTile);
+#pragma unroll
+    for (int s = 0; s < pw; ++s)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(dst + pdst[s]), 16,
+                                                 poff[s], 0, 0, 0);
+}
+
+// Workgroup barrier for LDS traffic that leaves weight DMAs in flight: waits
+// for this wave's own LDS operations only (a __syncthreads() here would also
+// wait for every pending global->LDS transfer). The empty asm statements keep
+// the compiler from moving memory accesses across it.
+__device__ inline void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt untouched
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int GT, int CPW, int PW, int NWMAX>
+__global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_dma(const uint8_t *__restrict__ w,
+                                                                             const float *__restrict__ x,
+                                                                             float *__restrict__ y, Geom gm) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int NW = gm.NW;
+    const int M = gm.M, rb = gm.row_bytes;
+    const int G = GT ? GT : gm.G;
+    const int Kp = gm.Gr * G;
+    const int NWP = (NW + 3) & ~3;
+    const int tbuf = gm.tbuf;  // one tile as in memory + 64 bytes of slack, multiple of 16, >= 1 KB
+    const int D = gm.depth;    // ring slots, 3..8
+
+    unsigned char *stage = smem;                                 // [D][tbuf]
+    float *part = reinterpret_cast<float *>(smem + D * tbuf);    // [2][16][NWP]
+    XPlanes xp;
+    xp.pl = reinterpret_cast<int8_t *>(part + 2 * kTile * NWP);
+    xp.stride = Kp;
+    xp.pre = reinterpret_cast<int *>(xp.pl + 3 * Kp);
+    xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
+    xp.gbase = 0;
+    xp.ngroups = gm.Gr;
+    XFirst xf;
+    load_x_first<GT>(xf, x, gm.K, Kp);
+
+    const int tiles = (M + kTile - 1) / kTile;
+    const int ntile = blockIdx.x < static_cast<unsigned>(tiles) ? (tiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+    auto tile_of = [&](int i) { return static_cast<int>(blockIdx.x + static_cast<unsigned>(i) * gridDim.x); };
+    const int last = max(ntile - 1, 0);
+
+    // 1 KB pieces of a tile this wave moves (piece j -> wave j % NW). Every
+    // wave issues exactly PW DMAs per tile (surplus slots repeat the last
+    // piece), so the wait counts below are exact. The last piece is moved
+    // back to end at the buffer's end; the bytes it shares with the piece
+    // before it are written twice with the same values.
+    int poff[PW], pdst[PW];
+#pragma unroll
+    for (int s = 0; s < PW; ++s) {
+        const int j = min(wave + s * NW, gm.pieces - 1);
+        pdst[s] = min(kPiece * j, tbuf - kPiece);
+        poff[s] = pdst[s] + 16 * lane;
+    }
+    // the first three tiles go out before the activation set-up (repeats of
+    // the last tile when the workgroup has fewer; they are never read) ...
+    dma_tile(w, M, rb, tile_of(0), stage, poff, pdst, PW);
+    dma_tile(w, M, rb, tile_of(min(1, last)), stage + tbuf, poff, pdst, PW);
+    dma_tile(w, M, rb, tile_of(min(2, last)), stage + 2 * tbuf, poff, pdst, PW);
+
+    prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
+    // ... and the rest of the ring once the activations have been read
+    for (int t = 3; t < D; ++t) dma_tile(w, M, rb, tile_of(min(t, last)), stage + t * tbuf, poff, pdst, PW);
+    lds_barrier();
+    const int t0 = (gm.T * wave) / NW;
+    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
+    v4i A0[CPW], A1[CPW];
+    float E[CPW], C[CPW];
+    int HO[CPW];
+    unsigned HM[CPW];
+    build_operands<GT, CPW, true>(xp, gm, t0, nch, A0, A1, E, C, HO, HM);
+    const int bn = lane & 15, kq = lane >> 4;
+    int RO[CPW], RH[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int t = t0 + min(c, nch - 1);
+        RO[c] = bn * rb + kChunk * t + 16 * kq;
+        RH[c] = bn * rb + HO[c];
+    }
+    for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x) lds_write_u32(part + i, 0u);
+
+    auto reduce_prev = [&](int i) {  // partial sums of tile i (written before the last barrier)
+        const float *pb = part + (i & 1) * (kTile * NWP);
+        if (threadIdx.x < kTile) {
+            const float *pr = pb + threadIdx.x * NWP;
+            float s = 0.f;
+            for (int q = 0; q < NWP / 4; ++q) {  // fixed order; padding slots hold 0
+                const float4 v = lds_read_f4(pr + 4 * q);
+                s += v.x;
+                s += v.y;
+                s += v.z;
+                s += v.w;
+            }
+            const int row = tile_of(i) * kTile + threadIdx.x;
+            if (row < M) y[row] = s;
+        }
+    };
+
+    int b = 0;  // ring slot of tile i
+    for (int i = 0; i < ntile; ++i) {
+        // tiles issued so far: D at the start, then one per iteration from
+        // i = 1 while tiles remain; tile i has landed once at most the later
+        // ones are pending
+        const int later = D + max(0, min(i - 1, ntile - D)) - i - 1;
+        wait_vmem(later * PW);
+        lds_barrier();  // every wave's pieces of tile i are in LDS; tile i-1's slot is free
+        if (i >= 1 && i + D - 1 < ntile)
+            dma_tile(w, M, rb, tile_of(i + D - 1), stage + (b == 0 ? D - 1 : b - 1) * tbuf, poff, pdst, PW);
+        const unsigned char *buf = stage + b * tbuf;
+        float a = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const v4i d = *reinterpret_cast<const v4i *>(buf + RO[c]);
+            const unsigned h = *reinterpret_cast<const unsigned *>(buf + RH[c]) & HM[c];
+            a = window_step(a, d, h, A0[c], A1[c], E[c], C[c]);
+        }
+        a += __shfl_xor(a, 16);  // the four group slots of each row
+        a += __shfl_xor(a, 32);
+        if (lane < kTile) lds_write_u32(part + (i & 1) * (kTile * NWP) + lane * NWP + wave, __builtin_bit_cast(unsigned, a));
+        if (i > 0) reduce_prev(i - 1);
+        b = b == D - 1 ? 0 : b + 1;
+    }
+    wait_vmem(0);  // no DMA may still be writing this workgroup's LDS at exit
     __syncthreads();
     if (ntile > 0) reduce_prev(ntile - 1);
 }
@@ -455,17 +857,20 @@ __global__ __launch_bounds__(1024, 4) void i4_matvec_reg(const uint8_t *__restri
     float *part = reinterpret_cast<float *>(smem);  // [16][NWP]
     XPlanes xp;
     xp.pl = reinterpret_cast<int8_t *>(part + kTile * NWP);
+    xp.stride = Kp;
     xp.pre = reinterpret_cast<int *>(xp.pl + 3 * Kp);
     xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
+    xp.gbase = 0;
+    xp.ngroups = gm.Gr;
 
     const int tiles = (M + kTile - 1) / kTile;
-    const int my0 = static_cast<int>(static_cast<long long>(tiles) * blockIdx.x / gridDim.x);
-    const int my1 = static_cast<int>(static_cast<long long>(tiles) * (blockIdx.x + 1) / gridDim.x);
 
     const int t0 = (gm.T * wave) / NW;
     const int nch = (gm.T * (wave + 1)) / NW - t0;
     const int bn = lane & 15, kq = lane >> 4;
-    prepare_x<GT>(xp, x, gm.K, gm.Gr, Kp);
+    XFirst xf;
+    load_x_first<GT>(xf, x, gm.K, Kp);
+    prepare_x<GT>(xp, x, gm.K, gm.Gr, Kp, xf);
     for (int i = threadIdx.x; i < kTile * NWP; i += blockDim.x) part[i] = 0.f;
     __syncthreads();
     v4i A0[CPW], A1[CPW];
@@ -477,7 +882,7 @@ __global__ __launch_bounds__(1024, 4) void i4_matvec_reg(const uint8_t *__restri
 #pragma unroll
     for (int c = 0; c < CPW; ++c) DO[c] = kChunk * (t0 + min(c, nch - 1)) + 16 * kq;
 
-    for (int tile = my0; tile < my1; ++tile) {
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {  // round-robin, as in i4_matvec_lds
         const int row0 = tile * kTile;
         const __amdgpu_buffer_rsrc_t rs = rows_rsrc(w, M, rb, row0);
         const int lb = (min(row0 + bn, M - 1) - row0) * rb;
@@ -570,17 +975,51 @@ int launch_with_lds(KernelT kernel, int grid, int threads, size_t lds, const uin
 }
 
 template <int GT, int CPW, int PW, int NWMAX>
+int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
+    static bool raised = false;
+    const int tiles = (gm.M + kTile - 1) / kTile;
+    const int NWP = (gm.NW + 3) & ~3;
+    Geom g2 = gm;
+    const size_t tile = static_cast<size_t>(kTile) * gm.row_bytes;
+    const size_t tbuf = std::max<size_t>((tile + kChunk + 15) / 16 * 16, kPiece);
+    const size_t fixed = static_cast<size_t>(2 * kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
+    // Workgroups per CU: as many as the wave budget allows (at most 2) while a
+    // three-slot ring still fits. Ring depth: enough tiles in flight per CU
+    // for the HBM latency-bandwidth product, within the LDS left.
+    if ((GT == 64 || GT == 128) && static_cast<size_t>(gm.Gr) * GT / 8 > static_cast<size_t>(64 * gm.NW))
+        return kTooLarge;  // the activation set-up assumes one 8-element block per thread
+    int wgs = std::max(1, std::min(2, kWavesPerCu / gm.NW));
+    while (wgs > 1 && static_cast<size_t>(wgs) * (3 * tbuf + fixed) > kLdsBytes) --wgs;
+    if (3 * tbuf + fixed > kLdsBytes) return kTooLarge;
+    const int grid = std::max(1, std::min(tiles, device_cus() * wgs));
+    const int per_wg = (tiles + grid - 1) / grid;
+    const size_t lds_cap = kLdsBytes / wgs;
+    int depth = static_cast<int>(std::min<size_t>(kMaxDepth, (lds_cap - fixed) / tbuf));
+    const size_t want = (kInflightPerCu + static_cast<size_t>(wgs) * tile - 1) / (static_cast<size_t>(wgs) * tile) + 1;
+    depth = std::max(3, std::min({depth, static_cast<int>(want), std::max(3, per_wg)}));
+    g2.tbuf = static_cast<int>(tbuf);
+    g2.depth = depth;
+    const size_t lds = depth * tbuf + fixed;
+    return launch_with_lds(i4_matvec_dma<GT, CPW, PW, NWMAX>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, raised);
+}
+
+template <int GT, int CPW, int PW, int NWMAX, int DEPTH = TQ_LDS_DEPTH>
 int launch_lds(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
+    if (TQ_USE_DMA) return launch_dma<GT, CPW, PW, NWMAX>(w, x, y, gm, stream);
     static bool raised = false;
     const int tiles = (gm.M + kTile - 1) / kTile;
     const int NWP = (gm.NW + 3) & ~3;
     const size_t tbuf = static_cast<size_t>(kTile) * gm.rbp + kChunk;
-    const size_t lds = 2 * tbuf + static_cast<size_t>(2 * kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
-    // 16 resident waves per CU when LDS allows it.
-    const int by_waves = std::max(1, 16 / NWMAX);
+    const size_t base = 2 * tbuf + static_cast<size_t>(2 * kTile * NWP) * 4;
+    Geom g2 = gm;
+    const size_t xbytes = (GT == 64 || GT == 128) ? static_cast<size_t>(gm.NW) * kWaveXBytes : xplanes_bytes(gm);
+    const bool inside = xbytes <= tbuf;
+    g2.xoff = static_cast<int>(inside ? tbuf : base);
+    const size_t lds = (inside ? base : base + xbytes) + 16;
+    const int by_waves = std::max(1, kWavesPerCu / NWMAX);
     const int by_lds = std::max(1, static_cast<int>((160 * 1024) / lds));
     const int grid = std::max(1, std::min(tiles, device_cus() * std::min(by_waves, by_lds)));
-    return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX>, grid, 64 * gm.NW, lds, w, x, y, gm, stream, raised);
+    return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX, DEPTH>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, raised);
 }
 
 template <int GT, int CPW>
@@ -673,6 +1112,9 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
     if (((rbp / 16) & 1) == 0) rbp += 16;  // odd multiple of 16: 16-row column reads avoid bank conflicts
     gm.rbp = rbp;
     gm.pieces = static_cast<int>((static_cast<size_t>(kTile) * rb + kPiece - 1) / kPiece);
+    gm.xoff = 0;
+    gm.tbuf = 0;
+    gm.depth = 0;
     int st;
     if (group_size == 64)
         st = launch_mfma_for<64>(w, x, y, gm, stream);
