@@ -51,7 +51,11 @@ def test_matmul_i4_golden_through_registry(gpu, name):
     assert_close(gpu.matmul_i4(f["w"], f["x"], M, K, N, G), f["y"], 2e-3, name)
 
 
-@pytest.mark.parametrize("M,K,N,G", [(9728, 2560, 32, 64), (300, 896, 7, 64), (1000, 640, 48, 128)])
+# Tile configurations: N <= 32, N <= 64 and larger; ragged M/N/K; group sizes
+# 32, 96, 128 (MFMA path) and 40 (not a multiple of 32: per-column matvec path).
+@pytest.mark.parametrize("M,K,N,G", [(9728, 2560, 32, 64), (300, 896, 7, 64), (1000, 640, 48, 128),
+                                     (520, 2560, 130, 64), (129, 100, 65, 32), (200, 384, 70, 96),
+                                     (64, 200, 40, 40), (1, 64, 1, 64), (33, 1000, 129, 64)])
 def test_matmul_i4_device_api_matches_oracle(gpu, orc, M, K, N, G):
     w = gpu.synth_i4(M, K, G, seed=M + N)
     x = gpu.synth_normal(K * N, seed=N)
@@ -59,3 +63,41 @@ def test_matmul_i4_device_api_matches_oracle(gpu, orc, M, K, N, G):
     dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M * N)
     gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G)
     assert_close(dy.download(np.float32, M * N), want, 2e-3, f"matmul {M}x{K}x{N}")
+
+
+def test_matmul_i4_per_token_scale_extremes(gpu, orc):
+    """Token columns of very different magnitude (1e30, 1e-30, 0, N(0,1)) each
+    keep the bar on their own: the fp16 staging scales every column by its own
+    power of two."""
+    M, K, N, G = 256, 640, 40, 64
+    w = gpu.synth_i4(M, K, G, seed=5)
+    x = gpu.synth_normal(K * N, seed=6).reshape(N, K).copy()
+    x[1] *= 1e30
+    x[2] *= 1e-30
+    x[3] = 0.0
+    x[4, ::7] = 0.0
+    x = x.reshape(-1)
+    want = orc.matmul_i4(w, x, M, K, N, G, threads=16).reshape(N, M)
+    got = gpu.matmul_i4(w, x, M, K, N, G).reshape(N, M)
+    assert np.all(got[3] == 0.0)
+    for n in range(N):
+        if n == 3:
+            continue
+        assert_close(got[n], want[n], 2e-3, f"column {n}")
+
+
+def test_matmul_i4_prefill_shape_sampled_rows(gpu, orc):
+    """The prefill configuration (9728 weight rows, K 2560, 512 tokens) in one
+    launch; rows are independent, so three 64-row blocks are checked against
+    the oracle run on those rows alone."""
+    M, K, N, G = 9728, 2560, 512, 64
+    w = gpu.synth_i4(M, K, G, seed=11)
+    x = gpu.synth_normal(K * N, seed=12)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M * N)
+    gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G)
+    got = dy.download(np.float32, M * N).reshape(N, M)
+    rb = orc.i4_row_bytes(K, G)
+    for r0 in (0, 4800, M - 64):
+        sub = np.ascontiguousarray(w[r0 * rb:(r0 + 64) * rb])
+        want = orc.matmul_i4(sub, x, 64, K, N, G, threads=16).reshape(N, 64)
+        assert_close(got[:, r0:r0 + 64], want, 2e-3, f"rows {r0}..{r0 + 63}")

@@ -121,6 +121,13 @@ def lib() -> ctypes.CDLL:
     return _LIB
 
 
+def _stream(s):
+    """None (the default stream), a Stream, or a raw hipStream_t value."""
+    if s is None:
+        return None
+    return s.ptr if isinstance(s, Stream) else int(s)
+
+
 def _ptr(a) -> int:
     if isinstance(a, DeviceBuffer):
         return a.ptr
@@ -297,21 +304,21 @@ def synchronize() -> None:
 
 
 def matvec_i4_dev(w, x, y, out_dim: int, in_dim: int, group_size: int, stream=None) -> None:
-    _check(lib().tqhip_matvec_i4_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, group_size, stream),
+    _check(lib().tqhip_matvec_i4_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, group_size, _stream(stream)),
            "tqhip_matvec_i4_dev")
 
 
 def matvec_i4_generic_dev(w, x, y, out_dim: int, in_dim: int, group_size: int, stream=None) -> None:
-    _check(lib().tqhip_matvec_i4_generic_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, group_size, stream),
+    _check(lib().tqhip_matvec_i4_generic_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, group_size, _stream(stream)),
            "tqhip_matvec_i4_generic_dev")
 
 
 def matvec_vq2_dev(w, x, y, out_dim: int, in_dim: int, stream=None) -> None:
-    _check(lib().tqhip_matvec_vq2_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, stream), "tqhip_matvec_vq2_dev")
+    _check(lib().tqhip_matvec_vq2_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, _stream(stream)), "tqhip_matvec_vq2_dev")
 
 
 def matmul_i4_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None) -> None:
-    _check(lib().tqhip_matmul_i4_dev(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size, stream),
+    _check(lib().tqhip_matmul_i4_dev(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size, _stream(stream)),
            "tqhip_matmul_i4_dev")
 
 
