@@ -4,19 +4,30 @@
 Step (the default workload): the batch=1 decode matvec
 set of a Qwen2.5-0.5B-shaped i4 HQQ@64 model -- 24 layers of independent
 seeded weights, each q 896x896, k 128x896, v 128x896, o 896x896, gate 4864x896,
-up 4864x896, down 896x4864, plus lm_head 151936x896: 169 i4 matvec launches on
-one stream, inputs resident in HBM.
+up 4864x896, down 896x4864, plus lm_head 151936x896 -- issued the way the
+reference runtime calls them (qwen_forward_token: mv_qkv, mv o, mv_pair
+gate/up, mv down; lm_head matvec_i4): 97 launches on one stream, inputs
+resident in HBM.
 
 Printed (one JSON line on stdout):
   value        algorithmic GB/s of the whole step; bytes per matvec are the
                reference's own definition weight_bytes + 4*(M+K)
-               (benchmarks/bench_kernels.cpp:487), i.e. 280,664,064 B per step
+               (benchmarks/bench_kernels.cpp:487): 280,664,064 B per step
   us_per_layer_set  time of one layer's 7 matvecs (the 24-layer part / 24)
+  roofline     the kernel with the largest share of the step's time (the
+               staged i4 MFMA matvec, every in_dim=896 launch): algorithmic
+               bytes of its launches / their time, those launches timed back
+               to back in step order with HIP events on the launch stream,
+               against 8 TB/s. traffic = HBM bytes per launch from the committed
+               rocprofv3 FETCH_SIZE/WRITE_SIZE summary, when present
   headline     BASELINE configs[2] lm_head 151936x2560 alone, rotated over
                3 copies (657 MB > 2x the 256 MB MALL) so reads come from HBM
-  roofline     the dominant kernel (the i4 MFMA matvec instance used for
-               in_dim=896) over the step's launches: HIP-event duration of its
-               launches back to back on the launch stream, against 8 TB/s
+  prefill      BASELINE configs[4] dequant-GEMM 9728x2560 at 32/128/512
+               tokens: us, TFLOP/s and fraction of the dense fp16 MFMA peak
+  vq2          BASELINE configs[3] VQ2 matvec 3072x1024 and VQ2 151936x896,
+               rotated copies, us and GB/s
+  host_call    the reference-signature host-pointer entry point (x H2D,
+               kernel, y D2H; weights cached in HBM), PCIe-inclusive us
   cpu_baseline the compiled reference's `ref` matvec (oracle/_ref, tiny-llm's
                kernels/matvec/matvec_i4_ref.cpp built unmodified), row-split
                over host threads, on the same step; the C++ restatement is
@@ -38,6 +49,7 @@ import numpy as np
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 PEAK_GBS = 8000.0
+PEAK_MFMA_TFLOPS = 2500.0  # dense fp16/bf16
 METRIC = "i4 matvec achieved HBM GB/s (% of MI355X peak); µs per layer matvec set"
 G = 64
 HIDDEN, INTER, VOCAB = 896, 4864, 151936
@@ -67,60 +79,183 @@ class Workload:
 
     def __init__(self, tq):
         self.tq = tq
-        self.host = []   # (name, M, K, w_host, x_host) kept for the CPU baseline
-        self.ops = []
+        self.host = []   # (name, M, K, w_host, x_host) per matrix, kept for the CPU baseline
+        self.ops = []    # device calls of one step
+        self.op_bytes = []
+        self.op_in_dim = []
         self.bufs = []
         t0 = time.time()
         for layer in range(N_LAYERS):
+            mats = {}
             xs = {}
             for name, M, K in LAYER:
                 # q/k/v share the attention input, gate/up share the MLP input
                 key = {"q": "attn", "k": "attn", "v": "attn", "gate": "mlp", "up": "mlp"}.get(name, name)
                 if key not in xs:
-                    xs[key] = tq.synth_normal(K, seed=tq.synth_seed(0, layer, "x_" + key))
-                self._add(f"L{layer}.{name}", M, K, tq.synth_i4(M, K, G, seed=tq.synth_seed(0, layer, name)), xs[key])
-        self._add("lm_head", VOCAB, HIDDEN, tq.synth_i4(VOCAB, HIDDEN, G, seed=tq.synth_seed(0, -1, "lm_head")),
-                  tq.synth_normal(HIDDEN, seed=tq.synth_seed(0, -1, "x_final")))
-        log(f"[bench] workload: {len(self.ops)} matvecs, {self.bytes / 1e6:.1f} MB algorithmic per step, "
-            f"generated+uploaded in {time.time() - t0:.1f}s")
+                    xs[key] = self._dev(tq.synth_normal(K, seed=tq.synth_seed(0, layer, "x_" + key)))
+                w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, layer, name))
+                mats[name] = (self._dev(w), xs[key], self._dev(None, 4 * M), M, K)
+                self.host.append((f"L{layer}.{name}", M, K, w, xs[key][1]))
+            q, k, v, o = mats["q"], mats["k"], mats["v"], mats["o"]
+            gate, up, down = mats["gate"], mats["up"], mats["down"]
+            self._op(tq.Op(tq.OP_I4_QKV, q[0].ptr, q[1][0].ptr, q[2].ptr, q[3], HIDDEN, 1, G,
+                           k[0].ptr, v[0].ptr, k[2].ptr, v[2].ptr, k[3]), [q, k, v])
+            self._op(tq.Op(tq.OP_I4_MATVEC, o[0].ptr, o[1][0].ptr, o[2].ptr, o[3], o[4], 1, G), [o])
+            self._op(tq.Op(tq.OP_I4_PAIR, gate[0].ptr, gate[1][0].ptr, gate[2].ptr, gate[3], HIDDEN, 1, G,
+                           up[0].ptr, None, up[2].ptr, None, 0), [gate, up])
+            self._op(tq.Op(tq.OP_I4_MATVEC, down[0].ptr, down[1][0].ptr, down[2].ptr, down[3], down[4], 1, G), [down])
+        w = tq.synth_i4(VOCAB, HIDDEN, G, seed=tq.synth_seed(0, -1, "lm_head"))
+        xf = self._dev(tq.synth_normal(HIDDEN, seed=tq.synth_seed(0, -1, "x_final")))
+        lm = (self._dev(w), xf, self._dev(None, 4 * VOCAB), VOCAB, HIDDEN)
+        self.host.append(("lm_head", VOCAB, HIDDEN, w, xf[1]))
+        self._op(tq.Op(tq.OP_I4_MATVEC, lm[0].ptr, xf[0].ptr, lm[2].ptr, VOCAB, HIDDEN, 1, G), [lm])
+        log(f"[bench] workload: {len(self.host)} matvecs in {len(self.ops)} launches, "
+            f"{self.bytes / 1e6:.1f} MB algorithmic per step, generated+uploaded in {time.time() - t0:.1f}s")
 
-    def _add(self, name, M, K, w, x):
+    def _dev(self, host, nbytes=None):
         tq = self.tq
-        dw, dx, dy = tq.DeviceBuffer.from_array(w), tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
-        self.bufs += [dw, dx, dy]
-        self.host.append((name, M, K, w, x))
-        self.ops.append(tq.Op(tq.OP_I4_MATVEC, dw.ptr, dx.ptr, dy.ptr, M, K, 1, G))
+        if host is None:
+            b = tq.DeviceBuffer(nbytes)
+            self.bufs.append(b)
+            return b
+        b = tq.DeviceBuffer.from_array(host)
+        self.bufs.append(b)
+        return (b, host) if host.dtype == np.float32 else b
+
+    def _op(self, op, mats):
+        self.ops.append(op)
+        self.op_bytes.append(sum(algo_bytes(m[3], m[4]) for m in mats))
+        self.op_in_dim.append(mats[0][4])
 
     @property
     def bytes(self):
-        return sum(algo_bytes(M, K) for _, M, K, _, _ in self.host)
+        return sum(self.op_bytes)
 
 
-def time_ops(tq, ops, reps, warmup, stream):
+def time_ops(tq, ops, reps, warmup, stream, batches=1):
+    """ms per pass over `ops`: HIP events around `reps` back-to-back passes on
+    `stream`; with batches > 1, the median over that many such measurements."""
     tq.run_ops(ops, warmup, stream)
     stream.synchronize()
-    e0, e1 = tq.Event(), tq.Event()
-    e0.record(stream)
-    tq.run_ops(ops, reps, stream)
-    e1.record(stream)
-    return e0.elapsed_ms(e1) / reps
+    out = []
+    for _ in range(batches):
+        e0, e1 = tq.Event(), tq.Event()
+        e0.record(stream)
+        tq.run_ops(ops, reps, stream)
+        e1.record(stream)
+        out.append(e0.elapsed_ms(e1) / reps)
+    return float(np.median(out))
 
 
-def headline(tq, stream, reps=60):
-    """configs[2] lm_head 151936x2560, 3 rotated copies (657 MB)."""
+def headline(tq, stream, reps=20):
+    """configs[2] lm_head 151936x2560, 3 rotated copies (657 MB): median of 7
+    batches of 20 rotations (60 launches each)."""
     M, K = VOCAB, 2560
     w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -1, "lm_head_2560"))
     x = tq.synth_normal(K, seed=tq.synth_seed(0, -1, "x_2560"))
     copies = [tq.DeviceBuffer.from_array(w) for _ in range(3)]
     dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
     ops = [tq.Op(tq.OP_I4_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, G) for c in copies]
-    ms = time_ops(tq, ops, reps, 5, stream) / len(ops)
+    ms = time_ops(tq, ops, reps, 5, stream, batches=7) / len(ops)
     gbs = algo_bytes(M, K) / (ms * 1e-3) / 1e9
     for c in copies:
         c.free()
     return {"shape": "151936x2560 G64 (BASELINE configs[2] lm_head)", "us": round(ms * 1e3, 2),
             "gbs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4), "bytes": algo_bytes(M, K),
             "rotation": "3 copies, 657 MB"}
+
+
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "i4_matvec_dma_decode_step_traffic.json")
+
+
+def roofline(tq, work, stream, reps):
+    """The in_dim=896 launches (qkv, o, gate/up pair, lm_head) all run the staged
+    MFMA matvec with 8 windows per row (i4_matvec_dma2<64,1,1,8> for the layer
+    projections, i4_matvec_dma<64,1,1,8> for lm_head). Timed back to back in
+    step order with events at both ends; back-to-back launches leave no gaps,
+    so the mean per launch is the kernels' mean duration."""
+    dom = [i for i, k in enumerate(work.op_in_dim) if k == HIDDEN]
+    ops = [work.ops[i] for i in dom]
+    ms = time_ops(tq, ops, reps, 2, stream, batches=5)
+    b_dom = sum(work.op_bytes[i] for i in dom)
+    achieved = b_dom / (ms * 1e-3) / 1e9
+    traffic = None
+    try:
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        pass
+    return {"bound": "hbm", "kernel": "i4_matvec_dma2<64,1,1,8> + i4_matvec_dma<64,1,1,8> (every in_dim=896 "
+                                      "launch: qkv, o, gate/up pair, lm_head)",
+            "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
+            "traffic": traffic, "launches": len(dom), "bytes_per_launch": b_dom // len(dom),
+            "avg_launch_us": round(ms * 1e3 / len(dom), 3)}
+
+
+def prefill(tq, stream, reps=30):
+    """W 9728x2560 i4 HQQ@64 times X of 32/128/512 tokens."""
+    M, K = 9728, 2560
+    w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -1, "prefill_w"))
+    dw = tq.DeviceBuffer.from_array(w)
+    rows = []
+    for n in (32, 128, 512):
+        x = tq.synth_normal(K * n, seed=tq.synth_seed(0, n, "prefill_x"))
+        dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M * n)
+        ops = [tq.Op(tq.OP_I4_MATMUL, dw.ptr, dx.ptr, dy.ptr, M, K, n, G)]
+        ms = time_ops(tq, ops, reps, 3, stream)
+        fl = 2.0 * M * K * n
+        tf = fl / (ms * 1e-3) / 1e12
+        rows.append({"tokens": n, "us": round(ms * 1e3, 2), "tflops": round(tf, 1),
+                     "mfma_frac": round(tf / PEAK_MFMA_TFLOPS, 4),
+                     "gbs": round((M * (K // G) * (4 + G // 2) + 4 * (K + M) * n) / (ms * 1e-3) / 1e9, 1)})
+        dx.free()
+        dy.free()
+    dw.free()
+    return {"shape": "W 9728x2560 G64, X 2560 x tokens (BASELINE configs[4])",
+            "mfma": "v_mfma_f32_32x32x16_f16, fp32 accumulate", "tokens": rows}
+
+
+def vq2(tq, stream, reps=20):
+    """VQ2 matvec: BASELINE configs[3] 3072x1024 and the reference's VQ2 lm_head
+    shape 151936x896 (kernels_baseline.csv:32), rotated over enough copies to
+    exceed 2x the 256 MB MALL; median of 7 batches."""
+    rows = []
+    for M, K, ncopy in ((3072, 1024, 700), (151936, 896, 16)):
+        w = tq.synth_vq2(M, K, seed=tq.synth_seed(0, -3, f"vq2_{M}"))
+        x = tq.synth_normal(K, seed=tq.synth_seed(0, -3, f"vq2x_{M}"))
+        copies = [tq.DeviceBuffer.from_array(w) for _ in range(ncopy)]
+        dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
+        ops = [tq.Op(tq.OP_VQ2_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, 0) for c in copies]
+        ms = time_ops(tq, ops, max(1, reps * 3 // ncopy), 1, stream, batches=7) / len(ops)
+        b = 2048 + M * (K // 4) + 4 * (M + K)
+        rows.append({"shape": f"{M}x{K}", "us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b, "copies": ncopy})
+        for c in copies:
+            c.free()
+        dx.free()
+        dy.free()
+    return rows
+
+
+def host_call(tq, reps=50):
+    """The reference-signature entry point (tqhip_matvec_i4: host x in, host y out,
+    weights cached in HBM after the first call): PCIe-inclusive latency per call."""
+    rows = []
+    for M, K in ((4864, HIDDEN), (VOCAB, 2560)):
+        w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -2, f"host_{M}"))
+        x = tq.synth_normal(K, seed=tq.synth_seed(0, -2, f"hostx_{M}"))
+        y = np.empty(M, np.float32)
+        f = tq.lib().tqhip_matvec_i4
+        args = (w.ctypes.data, x.ctypes.data, y.ctypes.data, M, K, G)
+        for _ in range(3):
+            f(*args)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            f(*args)
+        us = (time.perf_counter() - t0) / reps * 1e6
+        rows.append({"shape": f"{M}x{K}", "us": round(us, 2), "gbs": round(algo_bytes(M, K) / (us * 1e-6) / 1e9, 1)})
+    tq.lib().tqhip_release_weights()
+    return rows
 
 
 def cpu_baseline(work, budget_s=12.0):
@@ -183,6 +318,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU reference timing")
     ap.add_argument("--no-headline", action="store_true", help="skip the 151936x2560 rotated headline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill dequant-GEMM timings")
+    ap.add_argument("--no-host-call", action="store_true", help="skip the host-pointer (PCIe-inclusive) timing")
+    ap.add_argument("--no-vq2", action="store_true", help="skip the VQ2 matvec timings")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="first run one device-to-device copy of MB MiB (a known-size kernel for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the matvec would shard by "
@@ -195,29 +335,48 @@ def main():
         sys.exit(1)
     log(f"[bench] device: {tq.device_name()}")
     stream = tq.Stream()
+    if args.copy_calibration > 0:
+        nb = args.copy_calibration << 20
+        a, b = tq.DeviceBuffer(nb), tq.DeviceBuffer(nb)
+        tq.lib().tqhip_memset(a.ptr, 1, nb)
+        tq.synchronize()
+        tq.lib().tqhip_memcpy_d2d(b.ptr, a.ptr, nb)
+        tq.synchronize()
+        log(f"[bench] calibration copy: {nb} bytes device to device")
+        a.free()
+        b.free()
     work = Workload(tq)
 
     # whole step
     tq.synchronize()
-    ms_step = time_ops(tq, work.ops, args.steps, args.warmup, stream)
+    ms_step = time_ops(tq, work.ops, args.steps, args.warmup, stream)  # exactly --steps timed steps
     value = work.bytes / (ms_step * 1e-3) / 1e9
     log(f"[bench] step: {ms_step * 1e3:.1f} us, {value:.1f} GB/s")
     # the 24 layers alone
     layer_ops = work.ops[:-1]
     ms_layers = time_ops(tq, layer_ops, args.steps, 2, stream)
     us_layer = ms_layers * 1e3 / N_LAYERS
-    log(f"[bench] layer set: {us_layer:.2f} us per layer")
-    # dominant kernel: the in_dim=896 launches (q,k,v,o,gate,up x 24 + lm_head) back to back
-    dom = [op for op in work.ops if op.in_dim == HIDDEN]
-    dom_bytes = sum(algo_bytes(op.out_dim, op.in_dim) for op in dom)
-    ms_dom = time_ops(tq, dom, args.steps, 2, stream)
-    per_launch_us = ms_dom * 1e3 / len(dom)
-    achieved = dom_bytes / len(dom) / (per_launch_us * 1e-6) / 1e9
-    log(f"[bench] dominant kernel: {len(dom)} launches/step, {per_launch_us:.2f} us avg, {achieved:.1f} GB/s")
+    log(f"[bench] layer set: {us_layer:.2f} us per layer ({len(layer_ops) // N_LAYERS} launches)")
+    roof = roofline(tq, work, stream, args.steps)
+    log(f"[bench] dominant kernel: {roof['launches']} launches/step, {roof['avg_launch_us']} us avg, "
+        f"{roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of 8 TB/s)")
 
     head = None if args.no_headline else headline(tq, stream)
     if head:
         log(f"[bench] headline 151936x2560: {head['us']} us, {head['gbs']} GB/s ({100 * head['frac']:.1f}% of 8 TB/s)")
+    pre = None if args.no_prefill else prefill(tq, stream)
+    if pre:
+        for r in pre["tokens"]:
+            log(f"[bench] prefill 9728x2560 x{r['tokens']}: {r['us']} us, {r['tflops']} TFLOP/s "
+                f"({100 * r['mfma_frac']:.1f}% of dense fp16 MFMA)")
+
+    v = None if args.no_vq2 else vq2(tq, stream)
+    if v:
+        log("[bench] vq2 matvec: " + ", ".join(f"{r['shape']} {r['us']} us {r['gbs']} GB/s" for r in v))
+    host = None if args.no_host_call else host_call(tq)
+    if host:
+        log(f"[bench] host-pointer call (x H2D + kernel + y D2H, weights cached): " +
+            ", ".join(f"{r['shape']} {r['us']} us" for r in host))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -228,19 +387,20 @@ def main():
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "i8xi8->i32 MFMA, f32 epilogue", "data": "synthetic",
+        "vs_baseline": None, "dtype": "u4 codes x f32 activations (i8 MFMA, i32 accumulate, f32 epilogue)",
+        "data": "synthetic (BASELINE distributions, seeded)",
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "us_per_layer_set": round(us_layer, 2),
         "config": {"workload": "BASELINE configs[1]: Qwen2.5-0.5B-shaped i4 HQQ@64 decode matvec set, batch=1, "
-                               "24 layers x (q,k,v,o 896/128x896; gate,up 4864x896; down 896x4864) + lm_head "
-                               "151936x896, independent seeded weights",
-                   "bytes_per_step": work.bytes, "launches_per_step": len(work.ops), "group_size": G},
-        "roofline": {"bound": "hbm", "kernel": "i4_matvec_mfma<1> (in_dim 896 launches)",
-                     "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": None,
-                     "launches": len(dom), "bytes_per_launch": dom_bytes // len(dom),
-                     "avg_launch_us": round(per_launch_us, 3)},
+                               "24 layers x (qkv 896/128/128x896, o 896x896, gate/up pair 4864x896, "
+                               "down 896x4864) + lm_head 151936x896, independent seeded weights",
+                   "bytes_per_step": work.bytes, "matvecs_per_step": len(work.host),
+                   "launches_per_step": len(work.ops), "group_size": G},
+        "roofline": roof,
         "headline": head,
+        "prefill": pre,
+        "vq2": v,
+        "host_call": host,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

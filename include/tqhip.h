@@ -70,6 +70,12 @@ void tqhip_release_weights(void);
 int tqhip_matvec_i4_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
                         void *stream);
 int tqhip_matvec_vq2_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, void *stream);
+/* The pair and qkv forms (kernels/dispatch.h:162-163, 169-171) on device
+ * buffers: one launch covers all the matrices when the staged kernel applies. */
+int tqhip_matvec_pair_i4_dev(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2, int out_dim,
+                             int in_dim, int group_size, void *stream);
+int tqhip_matvec_qkv_i4_dev(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x, float *yq,
+                            float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size, void *stream);
 int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                         void *stream);
 /* The portable fp32 one-wave-per-row i4 kernel, used by the fast path for
@@ -127,11 +133,20 @@ typedef struct tqhip_op {
     const float *x;
     float *y;
     int out_dim, in_dim, n, group_size;
+    const void *w2, *w3;      /* PAIR: w2 / y2; QKV: k = (w2, y2), v = (w3, y3) */
+    float *y2, *y3;
+    int out_dim2;             /* QKV: kv_dim (out_dim is q_dim) */
 } tqhip_op;
 #define TQHIP_OP_I4_MATVEC 1
 #define TQHIP_OP_VQ2_MATVEC 2
 #define TQHIP_OP_I4_MATMUL 3
+#define TQHIP_OP_I4_PAIR 4
+#define TQHIP_OP_I4_QKV 5
 int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream);
+/* As tqhip_run_ops, with a HIP event pair around every call; op_ms[i] gets the
+ * mean event-to-event time of call i over the repeats (kernel duration as the
+ * stream sees it). */
+int tqhip_run_ops_timed(const tqhip_op *ops, int n_ops, int repeats, void *stream, float *op_ms);
 
 /* ---- 6. synthetic inputs (portable generator, identical on every host) -- */
 

@@ -30,6 +30,16 @@ def test_library_exports_every_header_symbol(tqa):
         assert hasattr(lib, n)
 
 
+def test_library_exports_only_the_c_abi(tqa):
+    """The tinyqwen registry copy inside the library is not exported (it would
+    interpose on tiny-llm's own registry when linked into it)."""
+    out = subprocess.run(["nm", "-D", "--defined-only", tqa.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    names = [line.split()[-1] for line in out.splitlines() if line.strip() and line.split()[-2] in "TtDdBbRrVvWw"]
+    assert names and all(n.startswith(("tqhip_", "tq_")) for n in names), [n for n in names
+                                                                           if not n.startswith(("tqhip_", "tq_"))]
+
+
 def test_python_bindings_cover_the_header(tqa):
     assert set(header_functions()) <= set(tqa.EXPORTED)
 

@@ -99,3 +99,56 @@ def test_bad_shapes_return_codes(gpu):
     assert lib.tqhip_matvec_i4_dev(None, None, None, 4, 64, 0, None) == gpu.EBADGROUP
     assert lib.tqhip_matvec_vq2_dev(None, None, None, 4, 6, None) == gpu.EBADSHAPE
     assert lib.tqhip_matmul_i4_dev(None, None, None, 4, 64, 0, 64, None) == gpu.EBADSHAPE
+
+
+# qkv / pair on device buffers: one launch over all the matrices (the staged
+# kernel) or one per matrix (rows past its window limit, group sizes it does
+# not cover). Each output must equal the single-matrix launch bit for bit (same
+# kernel configuration, fixed reduction order) and meet the bar against the oracle.
+@pytest.mark.parametrize("q,kv,K,G", [(896, 128, 896, 64), (4096, 1024, 2560, 64), (100, 17, 520, 40),
+                                      (64, 16, 4864, 64), (40, 8, 1000, 128), (24, 24, 200, 6)])
+def test_qkv_dev_one_launch_matches_single_and_oracle(gpu, orc, q, kv, K, G):
+    ws = [gpu.synth_i4(m, K, G, seed=1000 + i) for i, m in enumerate((q, kv, kv))]
+    x = gpu.synth_normal(K, seed=7)
+    dws = [gpu.DeviceBuffer.from_array(w) for w in ws]
+    dx = gpu.DeviceBuffer.from_array(x)
+    dys = [gpu.DeviceBuffer(4 * m) for m in (q, kv, kv)]
+    gpu.matvec_qkv_i4_dev(*dws, dx, *dys, q, kv, K, G)
+    got = [d.download(np.float32, m) for d, m in zip(dys, (q, kv, kv))]
+    for i, (w, m) in enumerate(zip(ws, (q, kv, kv))):
+        single = gpu.DeviceBuffer(4 * m)
+        gpu.matvec_i4_dev(dws[i], dx, single, m, K, G)
+        assert np.array_equal(got[i], single.download(np.float32, m)), f"qkv matrix {i} differs from its own launch"
+        assert_close(got[i], orc.matvec_i4(w, x, m, K, G, threads=16), f"qkv {i}")
+
+
+@pytest.mark.parametrize("M,K,G", [(4864, 896, 64), (9728, 2560, 64), (33, 130, 64), (300, 4864, 64)])
+def test_pair_dev_one_launch_matches_single_and_oracle(gpu, orc, M, K, G):
+    w1, w2 = gpu.synth_i4(M, K, G, seed=21), gpu.synth_i4(M, K, G, seed=22)
+    x = gpu.synth_normal(K, seed=23)
+    d1, d2, dx = gpu.DeviceBuffer.from_array(w1), gpu.DeviceBuffer.from_array(w2), gpu.DeviceBuffer.from_array(x)
+    y1, y2 = gpu.DeviceBuffer(4 * M), gpu.DeviceBuffer(4 * M)
+    gpu.matvec_pair_i4_dev(d1, d2, dx, y1, y2, M, K, G)
+    for w, dw, dy in ((w1, d1, y1), (w2, d2, y2)):
+        single = gpu.DeviceBuffer(4 * M)
+        gpu.matvec_i4_dev(dw, dx, single, M, K, G)
+        got = dy.download(np.float32, M)
+        assert np.array_equal(got, single.download(np.float32, M))
+        assert_close(got, orc.matvec_i4(w, x, M, K, G, threads=16), "pair")
+
+
+def test_run_ops_pair_and_qkv_kinds(gpu, orc):
+    """The op-list runner's PAIR and QKV kinds give the same outputs as the entry points."""
+    K, G, q, kv = 896, 64, 896, 128
+    ws = [gpu.synth_i4(m, K, G, seed=50 + i) for i, m in enumerate((q, kv, kv, 4864, 4864))]
+    x = gpu.synth_normal(K, seed=51)
+    dws = [gpu.DeviceBuffer.from_array(w) for w in ws]
+    dx = gpu.DeviceBuffer.from_array(x)
+    dys = [gpu.DeviceBuffer(4 * m) for m in (q, kv, kv, 4864, 4864)]
+    ops = [gpu.Op(gpu.OP_I4_QKV, dws[0].ptr, dx.ptr, dys[0].ptr, q, K, 1, G, dws[1].ptr, dws[2].ptr, dys[1].ptr,
+                  dys[2].ptr, kv),
+           gpu.Op(gpu.OP_I4_PAIR, dws[3].ptr, dx.ptr, dys[3].ptr, 4864, K, 1, G, dws[4].ptr, None, dys[4].ptr, None, 0)]
+    gpu.run_ops(ops, 2)
+    gpu.synchronize()
+    for w, d, m in zip(ws, dys, (q, kv, kv, 4864, 4864)):
+        assert_close(d.download(np.float32, m), orc.matvec_i4(w, x, m, K, G, threads=16), "run_ops")

@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtqhip.so")
 
 OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH = 0, -1, -2, -3, -4
-OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL = 1, 2, 3
+OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV = 1, 2, 3, 4, 5
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -33,7 +33,8 @@ _sz = ctypes.c_size_t
 class Op(ctypes.Structure):
     """tqhip_op: one device-pointer call of a tqhip_run_ops list."""
     _fields_ = [("kind", _i), ("w", _vp), ("x", _vp), ("y", _vp),
-                ("out_dim", _i), ("in_dim", _i), ("n", _i), ("group_size", _i)]
+                ("out_dim", _i), ("in_dim", _i), ("n", _i), ("group_size", _i),
+                ("w2", _vp), ("w3", _vp), ("y2", _vp), ("y3", _vp), ("out_dim2", _i)]
 
 
 _SIGS = {
@@ -48,6 +49,8 @@ _SIGS = {
     "tqhip_matvec_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tqhip_matvec_i4_generic_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tqhip_matvec_vq2_dev": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "tqhip_matvec_pair_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "tqhip_matvec_qkv_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matmul_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     # registry
     "tqhip_set_matvec_i4_impl_by_name": (_i, [ctypes.c_char_p]),
@@ -84,6 +87,7 @@ _SIGS = {
     "tqhip_event_record": (_i, [_vp, _vp]),
     "tqhip_event_elapsed_ms": (_i, [_vp, _vp, _f32p]),
     "tqhip_run_ops": (_i, [ctypes.POINTER(Op), _i, _i, _vp]),
+    "tqhip_run_ops_timed": (_i, [ctypes.POINTER(Op), _i, _i, _vp, _f32p]),
     # synthetic inputs
     "tq_synth_seed": (ctypes.c_uint64, [ctypes.c_uint64, _i, ctypes.c_char_p]),
     "tq_synth_i4": (None, [_vp, _i, _i, _i, ctypes.c_uint64, ctypes.c_float, ctypes.c_float,
@@ -317,6 +321,17 @@ def matvec_vq2_dev(w, x, y, out_dim: int, in_dim: int, stream=None) -> None:
     _check(lib().tqhip_matvec_vq2_dev(_ptr(w), _ptr(x), _ptr(y), out_dim, in_dim, _stream(stream)), "tqhip_matvec_vq2_dev")
 
 
+def matvec_pair_i4_dev(w1, w2, x, y1, y2, out_dim: int, in_dim: int, group_size: int, stream=None) -> None:
+    _check(lib().tqhip_matvec_pair_i4_dev(_ptr(w1), _ptr(w2), _ptr(x), _ptr(y1), _ptr(y2), out_dim, in_dim,
+                                          group_size, _stream(stream)), "tqhip_matvec_pair_i4_dev")
+
+
+def matvec_qkv_i4_dev(wq, wk, wv, x, yq, yk, yv, q_dim: int, kv_dim: int, in_dim: int, group_size: int,
+                      stream=None) -> None:
+    _check(lib().tqhip_matvec_qkv_i4_dev(_ptr(wq), _ptr(wk), _ptr(wv), _ptr(x), _ptr(yq), _ptr(yk), _ptr(yv), q_dim,
+                                         kv_dim, in_dim, group_size, _stream(stream)), "tqhip_matvec_qkv_i4_dev")
+
+
 def matmul_i4_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None) -> None:
     _check(lib().tqhip_matmul_i4_dev(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size, _stream(stream)),
            "tqhip_matmul_i4_dev")
@@ -365,4 +380,13 @@ class Event:
 
 def run_ops(ops: list, repeats: int, stream: "Stream | None" = None) -> None:
     arr = (Op * len(ops))(*ops)
-    _check(lib().tqhip_run_ops(arr, len(ops), repeats, stream.ptr if stream else None), "tqhip_run_ops")
+    _check(lib().tqhip_run_ops(arr, len(ops), repeats, _stream(stream)), "tqhip_run_ops")
+
+
+def run_ops_timed(ops: list, repeats: int, stream: "Stream | None" = None) -> np.ndarray:
+    """Runs the list `repeats` times with an event pair around every call; returns mean ms per call."""
+    arr = (Op * len(ops))(*ops)
+    out = np.zeros(len(ops), np.float32)
+    _check(lib().tqhip_run_ops_timed(arr, len(ops), repeats, _stream(stream), out.ctypes.data_as(_f32p)),
+           "tqhip_run_ops_timed")
+    return out

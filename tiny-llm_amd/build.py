@@ -54,8 +54,15 @@ def build(verbose: bool = False) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as pool:
         objs = list(pool.map(_compile, SOURCES))
+    # Only the C ABI is exported: the library's copy of the tinyqwen registry
+    # stays internal, so linking it into tiny-llm (which has its own) cannot
+    # interpose one registry on the other.
+    vers = os.path.join(BUILD_DIR, "exports.map")
+    with open(vers, "w") as f:
+        f.write("{ global: tqhip_*; tq_*; local: *; };\n")
     tmp = LIB + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"]
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread",
+           f"-Wl,--version-script={vers}"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

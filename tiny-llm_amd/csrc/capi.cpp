@@ -10,6 +10,7 @@
 #include "../../include/tqhip.h"
 
 #include <mutex>
+#include <vector>
 #include <unordered_map>
 
 #include "dispatch.h"
@@ -143,8 +144,10 @@ void tqhip_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, 
     float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
     float *dy = hb.ensure(hb.dy, hb.y_cap, 2 * static_cast<size_t>(out_dim));
     upload(dx, x, in_dim, s);
-    check_status(launch_i4_matvec(d1, dx, dy, out_dim, in_dim, group_size, s), "tqhip_matvec_pair_i4");
-    check_status(launch_i4_matvec(d2, dx, dy + out_dim, out_dim, in_dim, group_size, s), "tqhip_matvec_pair_i4");
+    const uint8_t *ws[2] = {d1, d2};
+    float *ys[2] = {dy, dy + out_dim};
+    const int ms[2] = {out_dim, out_dim};
+    check_status(launch_i4_matvec_group(2, ws, ys, ms, dx, in_dim, group_size, s), "tqhip_matvec_pair_i4");
     download(y1, dy, out_dim, s);
     download(y2, dy + out_dim, out_dim, s);
     TQ_HIP_CHECK(hipStreamSynchronize(s));
@@ -164,9 +167,10 @@ void tqhip_matvec_qkv_i4(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv
     float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
     float *dy = hb.ensure(hb.dy, hb.y_cap, static_cast<size_t>(q_dim) + 2 * static_cast<size_t>(kv_dim));
     upload(dx, x, in_dim, s);
-    check_status(launch_i4_matvec(dq, dx, dy, q_dim, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
-    check_status(launch_i4_matvec(dk, dx, dy + q_dim, kv_dim, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
-    check_status(launch_i4_matvec(dv, dx, dy + q_dim + kv_dim, kv_dim, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
+    const uint8_t *ws[3] = {dq, dk, dv};
+    float *ys[3] = {dy, dy + q_dim, dy + q_dim + kv_dim};
+    const int ms[3] = {q_dim, kv_dim, kv_dim};
+    check_status(launch_i4_matvec_group(3, ws, ys, ms, dx, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
     download(yq, dy, q_dim, s);
     download(yk, dy + q_dim, kv_dim, s);
     download(yv, dy + q_dim + kv_dim, kv_dim, s);
@@ -211,6 +215,20 @@ void tqhip_release_weights(void) {
 int tqhip_matvec_i4_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
                         void *stream) {
     return launch_i4_matvec(w, x, y, out_dim, in_dim, group_size, static_cast<hipStream_t>(stream));
+}
+int tqhip_matvec_pair_i4_dev(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2, int out_dim,
+                             int in_dim, int group_size, void *stream) {
+    const uint8_t *ws[2] = {w1, w2};
+    float *ys[2] = {y1, y2};
+    const int ms[2] = {out_dim, out_dim};
+    return launch_i4_matvec_group(2, ws, ys, ms, x, in_dim, group_size, static_cast<hipStream_t>(stream));
+}
+int tqhip_matvec_qkv_i4_dev(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x, float *yq,
+                            float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size, void *stream) {
+    const uint8_t *ws[3] = {wq, wk, wv};
+    float *ys[3] = {yq, yk, yv};
+    const int ms[3] = {q_dim, kv_dim, kv_dim};
+    return launch_i4_matvec_group(3, ws, ys, ms, x, in_dim, group_size, static_cast<hipStream_t>(stream));
 }
 int tqhip_matvec_i4_generic_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
                                 void *stream) {
@@ -308,27 +326,58 @@ int tqhip_event_elapsed_ms(void *start, void *stop, float *ms) {
                                                                                                                  : -1;
 }
 
+static int launch_op(const tqhip_op &op, hipStream_t s) {
+    const uint8_t *w = static_cast<const uint8_t *>(op.w);
+    switch (op.kind) {
+        case TQHIP_OP_I4_MATVEC: return launch_i4_matvec(w, op.x, op.y, op.out_dim, op.in_dim, op.group_size, s);
+        case TQHIP_OP_I4_PAIR:
+        case TQHIP_OP_I4_QKV: {
+            const int n = op.kind == TQHIP_OP_I4_PAIR ? 2 : 3;
+            const uint8_t *ws[3] = {w, static_cast<const uint8_t *>(op.w2), static_cast<const uint8_t *>(op.w3)};
+            float *ys[3] = {op.y, op.y2, op.y3};
+            const int ms[3] = {op.out_dim, op.kind == TQHIP_OP_I4_PAIR ? op.out_dim : op.out_dim2, op.out_dim2};
+            return launch_i4_matvec_group(n, ws, ys, ms, op.x, op.in_dim, op.group_size, s);
+        }
+        case TQHIP_OP_VQ2_MATVEC: return launch_vq2_matvec(w, op.x, op.y, op.out_dim, op.in_dim, s);
+        case TQHIP_OP_I4_MATMUL: return launch_i4_matmul(w, op.x, op.y, op.out_dim, op.in_dim, op.n, op.group_size, s);
+        default: return kBadShape;
+    }
+}
+
 int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     for (int r = 0; r < repeats; ++r) {
         for (int i = 0; i < n_ops; ++i) {
-            const tqhip_op &op = ops[i];
-            int st = kBadShape;
-            const uint8_t *w = static_cast<const uint8_t *>(op.w);
-            switch (op.kind) {
-                case TQHIP_OP_I4_MATVEC:
-                    st = launch_i4_matvec(w, op.x, op.y, op.out_dim, op.in_dim, op.group_size, s);
-                    break;
-                case TQHIP_OP_VQ2_MATVEC: st = launch_vq2_matvec(w, op.x, op.y, op.out_dim, op.in_dim, s); break;
-                case TQHIP_OP_I4_MATMUL:
-                    st = launch_i4_matmul(w, op.x, op.y, op.out_dim, op.in_dim, op.n, op.group_size, s);
-                    break;
-                default: break;
-            }
+            const int st = launch_op(ops[i], s);
             if (st != kOk) return st;
         }
     }
     return kOk;
+}
+
+int tqhip_run_ops_timed(const tqhip_op *ops, int n_ops, int repeats, void *stream, float *op_ms) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (n_ops < 1 || repeats < 1) return kBadShape;
+    std::vector<hipEvent_t> ev(2 * static_cast<size_t>(n_ops));
+    for (auto &e : ev)
+        if (hipEventCreate(&e) != hipSuccess) return kLaunchFailed;
+    for (int i = 0; i < n_ops; ++i) op_ms[i] = 0.f;
+    int st = kOk;
+    for (int r = 0; r < repeats && st == kOk; ++r) {
+        for (int i = 0; i < n_ops && st == kOk; ++i) {
+            if (hipEventRecord(ev[2 * i], s) != hipSuccess) st = kLaunchFailed;
+            if (st == kOk) st = launch_op(ops[i], s);
+            if (st == kOk && hipEventRecord(ev[2 * i + 1], s) != hipSuccess) st = kLaunchFailed;
+        }
+        if (st == kOk && hipEventSynchronize(ev.back()) != hipSuccess) st = kLaunchFailed;
+        for (int i = 0; i < n_ops && st == kOk; ++i) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) st = kLaunchFailed;
+            op_ms[i] += ms / repeats;
+        }
+    }
+    for (auto &e : ev) (void)hipEventDestroy(e);
+    return st;
 }
 
 }  // extern "C"

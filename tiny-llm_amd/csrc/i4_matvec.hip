@@ -56,8 +56,16 @@ constexpr int kWavesPerCu = TQ_WAVES_PER_CU;
 #define TQ_DMA_INFLIGHT_KB 96  // weight bytes in flight per CU the DMA ring aims for
 #endif
 constexpr size_t kInflightPerCu = static_cast<size_t>(TQ_DMA_INFLIGHT_KB) * 1024;
+#ifndef TQ_DMA_WAVES_PER_CU
+#define TQ_DMA_WAVES_PER_CU 32  // resident waves per CU the DMA-staged kernels aim for
+#endif
+constexpr int kDmaWavesPerCu = TQ_DMA_WAVES_PER_CU;
+// Occupancy bound of a DMA-staged instance: three windows per wave need more
+// than the 64 VGPRs that eight waves per SIMD leave.
+constexpr int dma_waves_per_simd(int cpw) { return cpw >= 3 ? std::min(6, kDmaWavesPerCu / 4) : kDmaWavesPerCu / 4; }
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
 constexpr int kMaxDepth = 8;              // DMA ring slots at most
+constexpr int kMaxGroup = 3;              // matrices sharing x in one DMA-staged launch (qkv)
 #ifndef TQ_USE_DMA
 #define TQ_USE_DMA 1  // stage tiles with global->LDS DMA (else through VGPRs)
 #endif
@@ -118,7 +126,32 @@ struct Geom {
     int xoff;     // LDS byte offset of the activation set-up (staged kernel)
     int tbuf;     // bytes of one DMA tile buffer (DMA-staged kernel)
     int depth;    // DMA ring slots (DMA-staged kernel)
+    // DMA-staged kernel: 1..3 matrices sharing x (pair / qkv), their tiles
+    // numbered one after the other; tile_end[j] = tiles of matrices 0..j.
+    int nmat;
+    int tile_end[kMaxGroup];
+    int mrows[kMaxGroup];
+    const uint8_t *mw[kMaxGroup];
+    float *my[kMaxGroup];
 };
+
+// Matrix j of the group that holds global tile t, and t's index within it
+// (selects, not indexing: a dynamic index into the kernel argument would put
+// it in scratch memory).
+struct TileRef {
+    const uint8_t *w;
+    float *y;
+    int M, tile;
+};
+__device__ inline TileRef locate_tile(const Geom &gm, int t) {
+    const bool a = t >= gm.tile_end[0], b = t >= gm.tile_end[1];
+    TileRef r;
+    r.w = b ? gm.mw[2] : a ? gm.mw[1] : gm.mw[0];
+    r.y = b ? gm.my[2] : a ? gm.my[1] : gm.my[0];
+    r.M = b ? gm.mrows[2] : a ? gm.mrows[1] : gm.mrows[0];
+    r.tile = t - (b ? gm.tile_end[1] : a ? gm.tile_end[0] : 0);
+    return r;
+}
 
 // LDS view of an activation set-up: groups gbase .. gbase+n-1 (the whole
 // vector for a workgroup-wide set-up, or the few groups one wave's windows
@@ -725,14 +758,14 @@ __device__ inline void lds_barrier() {
 }
 
 template <int GT, int CPW, int PW, int NWMAX>
-__global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_dma(const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec_dma(const uint8_t *__restrict__ w,
                                                                              const float *__restrict__ x,
                                                                              float *__restrict__ y, Geom gm) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int NW = gm.NW;
-    const int M = gm.M, rb = gm.row_bytes;
+    const int rb = gm.row_bytes;  // (w, y, gm.M: see gm.mw / gm.my / gm.mrows)
     const int G = GT ? GT : gm.G;
     const int Kp = gm.Gr * G;
     const int NWP = (NW + 3) & ~3;
@@ -751,7 +784,7 @@ __global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_dma(con
     XFirst xf;
     load_x_first<GT>(xf, x, gm.K, Kp);
 
-    const int tiles = (M + kTile - 1) / kTile;
+    const int tiles = gm.tile_end[gm.nmat - 1];
     const int ntile = blockIdx.x < static_cast<unsigned>(tiles) ? (tiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
     auto tile_of = [&](int i) { return static_cast<int>(blockIdx.x + static_cast<unsigned>(i) * gridDim.x); };
     const int last = max(ntile - 1, 0);
@@ -768,15 +801,19 @@ __global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_dma(con
         pdst[s] = min(kPiece * j, tbuf - kPiece);
         poff[s] = pdst[s] + 16 * lane;
     }
+    auto dma = [&](int i, unsigned char *dst) {
+        const TileRef r = locate_tile(gm, tile_of(i));
+        dma_tile(r.w, r.M, rb, r.tile, dst, poff, pdst, PW);
+    };
     // the first three tiles go out before the activation set-up (repeats of
     // the last tile when the workgroup has fewer; they are never read) ...
-    dma_tile(w, M, rb, tile_of(0), stage, poff, pdst, PW);
-    dma_tile(w, M, rb, tile_of(min(1, last)), stage + tbuf, poff, pdst, PW);
-    dma_tile(w, M, rb, tile_of(min(2, last)), stage + 2 * tbuf, poff, pdst, PW);
+    dma(0, stage);
+    dma(min(1, last), stage + tbuf);
+    dma(min(2, last), stage + 2 * tbuf);
 
     prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
     // ... and the rest of the ring once the activations have been read
-    for (int t = 3; t < D; ++t) dma_tile(w, M, rb, tile_of(min(t, last)), stage + t * tbuf, poff, pdst, PW);
+    for (int t = 3; t < D; ++t) dma(min(t, last), stage + t * tbuf);
     lds_barrier();
     const int t0 = (gm.T * wave) / NW;
     const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
@@ -807,8 +844,9 @@ __global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_dma(con
                 s += v.z;
                 s += v.w;
             }
-            const int row = tile_of(i) * kTile + threadIdx.x;
-            if (row < M) y[row] = s;
+            const TileRef r = locate_tile(gm, tile_of(i));
+            const int row = r.tile * kTile + threadIdx.x;
+            if (row < r.M) r.y[row] = s;
         }
     };
 
@@ -821,7 +859,7 @@ __global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_dma(con
         wait_vmem(later * PW);
         lds_barrier();  // every wave's pieces of tile i are in LDS; tile i-1's slot is free
         if (i >= 1 && i + D - 1 < ntile)
-            dma_tile(w, M, rb, tile_of(i + D - 1), stage + (b == 0 ? D - 1 : b - 1) * tbuf, poff, pdst, PW);
+            dma(i + D - 1, stage + (b == 0 ? D - 1 : b - 1) * tbuf);
         const unsigned char *buf = stage + b * tbuf;
         float a = 0.f;
 #pragma unroll
@@ -839,6 +877,100 @@ __global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_dma(con
     wait_vmem(0);  // no DMA may still be writing this workgroup's LDS at exit
     __syncthreads();
     if (ntile > 0) reduce_prev(ntile - 1);
+}
+
+// Small-grid variant of i4_matvec_dma: every workgroup owns at most two tiles
+// (blockIdx.x and blockIdx.x + gridDim.x), as in decode-size projections. The
+// tiles' DMAs go out first, the activation loads after them, and the set-up
+// waits for all of them at once: no ring, no repeated tiles.
+template <int GT, int CPW, int PW, int NWMAX>
+__global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec_dma2(const uint8_t *__restrict__ w,
+                                                                              const float *__restrict__ x,
+                                                                              float *__restrict__ y, Geom gm) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int NW = gm.NW;
+    const int rb = gm.row_bytes;
+    const int G = GT ? GT : gm.G;
+    const int Kp = gm.Gr * G;
+    const int NWP = (NW + 3) & ~3;
+    const int tbuf = gm.tbuf;
+
+    unsigned char *stage = smem;                               // [2][tbuf]
+    float *part = reinterpret_cast<float *>(smem + 2 * tbuf);  // [2][16][NWP]
+    XPlanes xp;
+    xp.pl = reinterpret_cast<int8_t *>(part + 2 * kTile * NWP);
+    xp.stride = Kp;
+    xp.pre = reinterpret_cast<int *>(xp.pl + 3 * Kp);
+    xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
+    xp.gbase = 0;
+    xp.ngroups = gm.Gr;
+
+    const int tiles = gm.tile_end[gm.nmat - 1];
+    const int t0i = blockIdx.x, t1i = blockIdx.x + gridDim.x;
+    const int ntile = (t0i < tiles ? 1 : 0) + (t1i < tiles ? 1 : 0);
+    if (ntile == 0) return;  // (the host sizes the grid so this does not happen)
+    int poff[PW], pdst[PW];
+#pragma unroll
+    for (int s = 0; s < PW; ++s) {
+        const int j = min(wave + s * NW, gm.pieces - 1);
+        pdst[s] = min(kPiece * j, tbuf - kPiece);
+        poff[s] = pdst[s] + 16 * lane;
+    }
+    {
+        const TileRef r = locate_tile(gm, t0i);
+        dma_tile(r.w, r.M, rb, r.tile, stage, poff, pdst, PW);
+    }
+    if (ntile > 1) {
+        const TileRef r = locate_tile(gm, t1i);
+        dma_tile(r.w, r.M, rb, r.tile, stage + tbuf, poff, pdst, PW);
+    }
+    XFirst xf;
+    load_x_first<GT>(xf, x, gm.K, Kp);
+    prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
+    wait_vmem(0);   // this wave's tile pieces (the activation loads are already in)
+    for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x)
+        if (i % NWP >= NW) part[i] = 0.f;  // padding slots of the fixed-order sums
+    lds_barrier();  // every wave's pieces and activation planes are in LDS
+    const int t0 = (gm.T * wave) / NW;
+    const int nch = (gm.T * (wave + 1)) / NW - t0;
+    v4i A0[CPW], A1[CPW];
+    float E[CPW], C[CPW];
+    int HO[CPW];
+    unsigned HM[CPW];
+    build_operands<GT, CPW, false>(xp, gm, t0, nch, A0, A1, E, C, HO, HM);  // nothing in flight any more
+    const int bn = lane & 15, kq = lane >> 4;
+    for (int i = 0; i < ntile; ++i) {
+        const unsigned char *buf = stage + i * tbuf;
+        float a = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const int t = t0 + min(c, nch - 1);
+            const v4i d = *reinterpret_cast<const v4i *>(buf + bn * rb + kChunk * t + 16 * kq);
+            const unsigned h = *reinterpret_cast<const unsigned *>(buf + bn * rb + HO[c]) & HM[c];
+            a = window_step(a, d, h, A0[c], A1[c], E[c], C[c]);
+        }
+        a += __shfl_xor(a, 16);
+        a += __shfl_xor(a, 32);
+        if (lane < kTile) part[i * (kTile * NWP) + lane * NWP + wave] = a;
+    }
+    __syncthreads();
+    if (threadIdx.x < kTile * ntile) {
+        const int i = threadIdx.x / kTile, rr = threadIdx.x % kTile;
+        const float4 *pr = reinterpret_cast<const float4 *>(part + i * (kTile * NWP) + rr * NWP);
+        float s = 0.f;
+        for (int q = 0; q < NWP / 4; ++q) {  // fixed order
+            const float4 v = pr[q];
+            s += v.x;
+            s += v.y;
+            s += v.z;
+            s += v.w;
+        }
+        const TileRef r = locate_tile(gm, i == 0 ? t0i : t1i);
+        const int row = r.tile * kTile + rr;
+        if (row < r.M) r.y[row] = s;
+    }
 }
 
 // ============================================================================================
@@ -977,7 +1109,7 @@ int launch_with_lds(KernelT kernel, int grid, int threads, size_t lds, const uin
 template <int GT, int CPW, int PW, int NWMAX>
 int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
     static bool raised = false;
-    const int tiles = (gm.M + kTile - 1) / kTile;
+    const int tiles = gm.tile_end[gm.nmat - 1];
     const int NWP = (gm.NW + 3) & ~3;
     Geom g2 = gm;
     const size_t tile = static_cast<size_t>(kTile) * gm.row_bytes;
@@ -988,7 +1120,23 @@ int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     // for the HBM latency-bandwidth product, within the LDS left.
     if ((GT == 64 || GT == 128) && static_cast<size_t>(gm.Gr) * GT / 8 > static_cast<size_t>(64 * gm.NW))
         return kTooLarge;  // the activation set-up assumes one 8-element block per thread
-    int wgs = std::max(1, std::min(2, kWavesPerCu / gm.NW));
+    int wgs = std::max(1, std::min(4, 4 * dma_waves_per_simd(CPW) / gm.NW));
+    {
+        // at most two tiles per workgroup: the small-grid kernel, one wave of workgroups
+        static bool raised2 = false;
+        const size_t lds2 = 2 * tbuf + fixed;
+        int wgs2 = wgs;
+        while (wgs2 > 1 && static_cast<size_t>(wgs2) * lds2 > kLdsBytes) --wgs2;
+        const int slots = device_cus() * wgs2;
+        if (lds2 <= kLdsBytes && tiles <= 2 * slots) {
+            Geom g2 = gm;
+            g2.tbuf = static_cast<int>(tbuf);
+            g2.depth = 2;
+            const int grid2 = tiles <= slots ? tiles : (tiles + 1) / 2;
+            return launch_with_lds(i4_matvec_dma2<GT, CPW, PW, NWMAX>, grid2, 64 * gm.NW, lds2, w, x, y, g2, stream,
+                                   raised2);
+        }
+    }
     while (wgs > 1 && static_cast<size_t>(wgs) * (3 * tbuf + fixed) > kLdsBytes) --wgs;
     if (3 * tbuf + fixed > kLdsBytes) return kTooLarge;
     const int grid = std::max(1, std::min(tiles, device_cus() * wgs));
@@ -1115,6 +1263,13 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
     gm.xoff = 0;
     gm.tbuf = 0;
     gm.depth = 0;
+    gm.nmat = 1;
+    for (int j = 0; j < kMaxGroup; ++j) {
+        gm.tile_end[j] = (out_dim + kTile - 1) / kTile;
+        gm.mrows[j] = out_dim;
+        gm.mw[j] = w;
+        gm.my[j] = y;
+    }
     int st;
     if (group_size == 64)
         st = launch_mfma_for<64>(w, x, y, gm, stream);
@@ -1124,6 +1279,61 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
         st = launch_mfma_for<0>(w, x, y, gm, stream);
     if (st == kTooLarge) return launch_i4_matvec_generic(w, x, y, out_dim, in_dim, group_size, stream);
     return st;
+}
+
+// Matvecs of n (<= 3) matrices that share x, in_dim and group_size (the
+// reference's pair and qkv forms): one DMA-staged launch whose tiles run over
+// the matrices one after the other, else one launch per matrix.
+int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, const int *out_dim, const float *x,
+                           int in_dim, int group_size, hipStream_t stream) {
+    if (n < 1 || n > kMaxGroup || in_dim < 1) return kBadShape;
+    if (group_size < 2 || (group_size & 1)) return kBadGroup;
+    for (int j = 0; j < n; ++j)
+        if (out_dim[j] < 1) return kBadShape;
+    const size_t rb = i4_row_bytes(in_dim, group_size);
+    const int T = static_cast<int>((rb + kChunk - 1) / kChunk);
+    const bool grouped = n > 1 && TQ_USE_DMA && (group_size % 8 == 0) && group_size >= 40 && T <= 48 &&
+                         rb * kTile * 2 < (1ull << 31);
+    if (!grouped) {
+        for (int j = 0; j < n; ++j) {
+            const int st = launch_i4_matvec(w[j], x, y[j], out_dim[j], in_dim, group_size, stream);
+            if (st != kOk) return st;
+        }
+        return kOk;
+    }
+    Geom gm;
+    gm.M = out_dim[0];
+    gm.K = in_dim;
+    gm.G = group_size;
+    gm.gb = i4_group_bytes(group_size);
+    gm.Gr = i4_groups(in_dim, group_size);
+    gm.row_bytes = static_cast<int>(rb);
+    gm.T = T;
+    gm.NW = 1;
+    gm.rbp = 0;
+    gm.pieces = static_cast<int>((static_cast<size_t>(kTile) * rb + kPiece - 1) / kPiece);
+    gm.xoff = 0;
+    gm.tbuf = 0;
+    gm.depth = 0;
+    gm.nmat = n;
+    int end = 0;
+    for (int j = 0; j < kMaxGroup; ++j) {
+        const int jj = std::min(j, n - 1);  // unused slots repeat the last matrix (never selected)
+        if (j < n) end += (out_dim[j] + kTile - 1) / kTile;
+        gm.tile_end[j] = end;
+        gm.mrows[j] = out_dim[jj];
+        gm.mw[j] = w[jj];
+        gm.my[j] = y[jj];
+    }
+    const int st = group_size == 64    ? launch_mfma_for<64>(w[0], x, y[0], gm, stream)
+                   : group_size == 128 ? launch_mfma_for<128>(w[0], x, y[0], gm, stream)
+                                       : launch_mfma_for<0>(w[0], x, y[0], gm, stream);
+    if (st != kTooLarge) return st;
+    for (int j = 0; j < n; ++j) {  // the staged kernel does not fit: one launch per matrix
+        const int sj = launch_i4_matvec(w[j], x, y[j], out_dim[j], in_dim, group_size, stream);
+        if (sj != kOk) return sj;
+    }
+    return kOk;
 }
 
 }  // namespace tqhip

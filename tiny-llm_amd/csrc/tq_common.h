@@ -56,6 +56,9 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
                      hipStream_t stream);
 int launch_i4_matvec_generic(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim,
                              int group_size, hipStream_t stream);
+// n (1..3) matrices sharing x, in_dim and group_size (pair / qkv), one launch where possible.
+int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, const int *out_dim, const float *x,
+                           int in_dim, int group_size, hipStream_t stream);
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                      hipStream_t stream);
