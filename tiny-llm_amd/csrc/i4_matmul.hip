@@ -33,7 +33,6 @@ typedef float f16x __attribute__((ext_vector_type(16)));
 typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
 constexpr int kStepK = 64;             // K elements per main-loop step
-constexpr int kRowHalves = kStepK + 8;  // LDS row stride in halves (144 B: conflict-free 16-byte reads)
 constexpr int kThreads = 256;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
 
@@ -42,13 +41,22 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, size_t byte
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), nrec, kBufferFlags);
 }
 
-// ---- 1. X (fp32, column n = token) -> fp16 * 2^e_n, rows padded to Kp
+// ---- 1. X (fp32, column n = token) -> fp16 * 2^e_n, rows padded to Kp.
+// One workgroup per token; the column is read once into registers (Kp <= 256 *
+// kXRegs), its max taken, then converted and stored. Longer columns: two passes.
+constexpr int kXRegs = 16;
 __global__ __launch_bounds__(256) void x_to_f16(const float *__restrict__ x, int K, int Kp, _Float16 *__restrict__ xh,
                                                   float *__restrict__ xinv) {
     const int n = blockIdx.x;
     const float *xc = x + static_cast<size_t>(n) * K;
+    float v[kXRegs];
     float m = 0.f;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(xc[k]));
+#pragma unroll
+    for (int i = 0; i < kXRegs; ++i) {
+        const int k = threadIdx.x + i * 256;
+        v[i] = k < K ? xc[k] : 0.f;
+        m = fmaxf(m, fabsf(v[i]));
+    }
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     __shared__ float wm[4];
     if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
@@ -61,8 +69,33 @@ __global__ __launch_bounds__(256) void x_to_f16(const float *__restrict__ x, int
         e = min(max(15 - E, -120), 120);
     }
     _Float16 *hc = xh + static_cast<size_t>(n) * Kp;
-    for (int k = threadIdx.x; k < Kp; k += blockDim.x)
-        hc[k] = static_cast<_Float16>(k < K ? ldexpf(xc[k], e) : 0.f);
+#pragma unroll
+    for (int i = 0; i < kXRegs; ++i) {
+        const int k = threadIdx.x + i * 256;
+        if (k < Kp) hc[k] = static_cast<_Float16>(ldexpf(v[i], e));
+    }
+    if (threadIdx.x == 0) xinv[n] = ldexpf(1.f, -e);
+}
+
+__global__ __launch_bounds__(256) void x_to_f16_long(const float *__restrict__ x, int K, int Kp,
+                                                       _Float16 *__restrict__ xh, float *__restrict__ xinv) {
+    const int n = blockIdx.x;
+    const float *xc = x + static_cast<size_t>(n) * K;
+    float m = 0.f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(xc[k]));
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __shared__ float wm[4];
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    int e = 0;
+    if (m > 0.f && m <= 3.0e38f) {
+        int E;
+        frexpf(m, &E);
+        e = min(max(15 - E, -120), 120);
+    }
+    _Float16 *hc = xh + static_cast<size_t>(n) * Kp;
+    for (int k = threadIdx.x; k < Kp; k += blockDim.x) hc[k] = static_cast<_Float16>(k < K ? ldexpf(xc[k], e) : 0.f);
     if (threadIdx.x == 0) xinv[n] = ldexpf(1.f, -e);
 }
 
@@ -79,107 +112,156 @@ __device__ inline unsigned fma_pair_f16(float q0, float q1, float s, float c) {
     return r;
 }
 
-// Dequantizes 32 consecutive elements (16 code bytes, low nibble first) of one
-// group to fp16: q * scale - zero * scale with one rounding to fp16 (within
-// one fp16 rounding of the reference's fp32 (q - zero) * scale).
-__device__ inline void dequant32(const unsigned (&c)[4], unsigned hdr, bool valid, u4v (&out)[2][2]) {
-    const float s = valid ? half_bits_f(hdr) : 0.f;
-    const float nzs = valid ? -(half_bits_f(hdr >> 16) * s) : 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const unsigned lo = c[d] & 0x0F0F0F0Fu;         // elements 8d + 0, 2, 4, 6
-        const unsigned hi = (c[d] >> 4) & 0x0F0F0F0Fu;  // elements 8d + 1, 3, 5, 7
-        unsigned pk[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const float q0 = static_cast<float>((lo >> (8 * b)) & 0xFFu);
-            const float q1 = static_cast<float>((hi >> (8 * b)) & 0xFFu);
-            pk[b] = fma_pair_f16(q0, q1, s, nzs);
-        }
-        out[d >> 1][d & 1] = u4v{pk[0], pk[1], pk[2], pk[3]};
+// 8 consecutive elements (one code dword, low nibble first) of one group as
+// the fp16 MFMA operand: q * scale - zero * scale, rounded once (within one
+// fp16 rounding of the reference's fp32 (q - zero) * scale).
+// Byte b of v as a float (v_cvt_f32_ubyte{b}: no separate extract).
+template <int B>
+__device__ inline float ubyte_f(unsigned v) {
+    float f;
+    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
+    if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
+    if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
+    if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
+    return f;
+}
+
+__device__ inline h8 dequant8(unsigned c, float s, float nzs) {
+    const unsigned lo = c & 0x0F0F0F0Fu;         // elements 0, 2, 4, 6
+    const unsigned hi = (c >> 4) & 0x0F0F0F0Fu;  // elements 1, 3, 5, 7
+    u4v pk;
+    pk[0] = fma_pair_f16(ubyte_f<0>(lo), ubyte_f<0>(hi), s, nzs);
+    pk[1] = fma_pair_f16(ubyte_f<1>(lo), ubyte_f<1>(hi), s, nzs);
+    pk[2] = fma_pair_f16(ubyte_f<2>(lo), ubyte_f<2>(hi), s, nzs);
+    pk[3] = fma_pair_f16(ubyte_f<3>(lo), ubyte_f<3>(hi), s, nzs);
+    return __builtin_bit_cast(h8, pk);
+}
+
+__device__ __forceinline__ void wait_vm(int n) {
+    // s_waitcnt vmcnt(n), expcnt / lgkmcnt untouched (gfx9 encoding)
+    switch (n) {
+#define TQ_VMWAIT(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); break;
+        TQ_VMWAIT(0) TQ_VMWAIT(1) TQ_VMWAIT(2) TQ_VMWAIT(3) TQ_VMWAIT(4) TQ_VMWAIT(5) TQ_VMWAIT(6) TQ_VMWAIT(7)
+        TQ_VMWAIT(8) TQ_VMWAIT(9) TQ_VMWAIT(10) TQ_VMWAIT(11) TQ_VMWAIT(12) TQ_VMWAIT(13) TQ_VMWAIT(14)
+        TQ_VMWAIT(15) TQ_VMWAIT(16) TQ_VMWAIT(17) TQ_VMWAIT(18) TQ_VMWAIT(19) TQ_VMWAIT(20) TQ_VMWAIT(21)
+        TQ_VMWAIT(22) TQ_VMWAIT(23) TQ_VMWAIT(24) TQ_VMWAIT(25) TQ_VMWAIT(26) TQ_VMWAIT(27) TQ_VMWAIT(28)
+#undef TQ_VMWAIT
+        default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break;
     }
 }
 
+// Workgroup barrier that waits for this wave's LDS operations only (global ->
+// LDS transfers of later steps stay in flight).
+__device__ inline void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+constexpr int kWDwords = 10;                    // per row and step
+constexpr int kWStage1 = 128 * kWDwords * 4;    // bytes of W per step and 128 rows
+constexpr int kWDma1 = 128 * kWDwords / 64 / 4; // dword DMAs per wave per step and 128 rows (= 5)
+
+// Byte offsets, within a row, of one step's W data: per 32-element half t the
+// group header and the first of its 16 code bytes (each half lies in one group
+// as G % 32 == 0). Uniform across the workgroup (scalar arithmetic).
+struct StepOffsets {
+    int hdr[2], code[2];
+    bool valid[2];
+};
+__device__ __forceinline__ StepOffsets step_offsets(int s, int G, int gb, int groups) {
+    StepOffsets o;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int k = s * kStepK + 32 * t;
+        const int g = k / G;
+        o.valid[t] = g < groups;
+        const int gc = min(g, groups - 1);  // past the last group: any valid bytes, masked later
+        o.hdr[t] = gc * gb;
+        o.code[t] = gc * gb + 4 + (k - gc * G) / 2;
+    }
+    return o;
+}
+
+// One step's global -> LDS DMAs of one wave (nw dword DMAs of W, nx 16-byte
+// DMAs of X, the X part starting xbase bytes into the stage); every lane of
+// every DMA is live, so the count per wave and step is fixed. Per lane only a
+// select and an add depend on the step. (Not a lambda in the kernel: HIP
+// compiles those for the host too, where the DMA builtin does not exist.)
+__device__ __forceinline__ void issue_step(__amdgpu_buffer_rsrc_t wr, __amdgpu_buffer_rsrc_t xr, unsigned char *st,
+                                           const int *wrow, const int *wsel, int nw, const int *xoff, int nx,
+                                           int xbase, int wave, int s, const StepOffsets &o) {
+#pragma unroll
+    for (int q = 0; q < nw; ++q) {
+        // wsel: slot 0/1 -> header of half 0/1; slot 2+4t+i -> code dword i of half t
+        const int sl = wsel[q];
+        const int t = sl < 2 ? sl : (sl - 2) >> 2;
+        const int base = sl < 2 ? (t ? o.hdr[1] : o.hdr[0]) : (t ? o.code[1] : o.code[0]) + 4 * ((sl - 2) & 3);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wr, (__attribute__((address_space(3))) void *)(st + 256 * (wave * nw + q)), 4, wrow[q] + base, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < nx; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (__attribute__((address_space(3))) void *)(st + xbase + 1024 * (wave * nx + q)), 16,
+            xoff[q] + s * kStepK * 2, 0, 0, 0);
+}
+
 // ---- 2. MFMA tile kernel
-//   WM x WN blocks of 32x32 per wave, WAVES_M x WAVES_N waves (= 4).
-template <int WM, int WN, int WAVES_M, int WAVES_N>
+//   4 waves; wave w owns weight rows 32*WM*w .. +32*WM of the workgroup's
+//   BM = 128 * WM and all BN = 32 * WN tokens. Per 64-element K step,
+//   global -> LDS DMA brings
+//     W: per row 10 dwords [header of half 0, header of half 1, 8 code dwords]
+//        (each 32-element half lies in one group as G % 32 == 0);
+//     X: BN rows x 128 B of fp16, 16-byte chunks XOR-swizzled by row (c ^ (r & 7))
+//   into a ring of S stages issued S - 1 steps ahead. Each wave dequantizes its
+//   A operands from the raw codes in LDS straight into registers; every X (B)
+//   operand read from LDS feeds WM MFMAs.
+template <int WM, int WN>
 __global__ __launch_bounds__(kThreads) void i4_matmul_mfma(const uint8_t *__restrict__ w,
                                                            const _Float16 *__restrict__ xh,
                                                            const float *__restrict__ xinv, float *__restrict__ y,
-                                                           int M, int N, int K, int Kp, int G, int row_bytes) {
-    static_assert(WAVES_M * WAVES_N == 4, "four waves");
-    constexpr int BM = 32 * WM * WAVES_M;
-    constexpr int BN = 32 * WN * WAVES_N;
-    constexpr int UNITS = 2 * BM / kThreads;  // 32-element W units per thread per step
-    constexpr int XCH = BN * 8 / kThreads;    // 16-byte X chunks per thread per step
-    static_assert(UNITS >= 1 && XCH >= 1, "tile too small for the thread count");
-    __shared__ __align__(16) _Float16 sw[2][BM * kRowHalves];
-    __shared__ __align__(16) _Float16 sx[2][BN * kRowHalves];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+                                                           int M, int N, int K, int Kp, int G, int row_bytes, int S) {
+    constexpr int BM = 128 * WM;
+    constexpr int BN = 32 * WN;
+    constexpr int WStage = kWStage1 * WM;
+    constexpr int WDma = kWDma1 * WM;
+    constexpr int XStage = BN * 128;
+    constexpr int P = WDma + WN;  // DMAs per wave per step
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int gb = 4 + G / 2;
     const int groups = (K + G - 1) / G;
     const int steps = Kp / kStepK;
+    const int stage_bytes = WStage + XStage;
 
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + static_cast<size_t>(m0) * row_bytes,
                                                 static_cast<size_t>(M - m0) * row_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh + static_cast<size_t>(n0) * Kp,
                                                 static_cast<size_t>(N - n0) * Kp * 2);
 
-    // per-thread load slots
-    int urow[UNITS], uhalf[UNITS];
+    // this wave's W DMAs: dword d = 64 * (wave * WDma + q) + lane of the stage
+    int wrow[WDma], wslot[WDma];
 #pragma unroll
-    for (int u = 0; u < UNITS; ++u) {
-        const int id = tid + u * kThreads;
-        urow[u] = id >> 1;
-        uhalf[u] = id & 1;
+    for (int q = 0; q < WDma; ++q) {
+        const int d = 64 * (wave * WDma + q) + lane;
+        wrow[q] = (d / kWDwords) * row_bytes;
+        wslot[q] = d % kWDwords;
     }
-    int xrow[XCH], xcol[XCH];
+    // this wave's X DMAs: 16-byte position p = 64 * (wave * WN + q) + lane
+    int xoff[WN];
 #pragma unroll
-    for (int c = 0; c < XCH; ++c) {
-        const int id = tid + c * kThreads;
-        xrow[c] = id >> 3;  // token within the tile
-        xcol[c] = id & 7;   // 16-byte chunk within the 128-byte step slice
+    for (int q = 0; q < WN; ++q) {
+        const int p = 64 * (wave * WN + q) + lane;
+        const int r = p >> 3, c = (p & 7) ^ (r & 7);
+        xoff[q] = r * Kp * 2 + 16 * c;
     }
-
-    unsigned wc[UNITS][4], wh[UNITS];
-    bool wv[UNITS];
-    u4v xv[XCH];
-    auto load_step = [&](int s) {
-#pragma unroll
-        for (int u = 0; u < UNITS; ++u) {
-            const int k0 = s * kStepK + 32 * uhalf[u];
-            const int g = k0 / G;
-            wv[u] = g < groups;
-            const int gg = min(g, groups - 1);
-            const int base = urow[u] * row_bytes + gg * gb;
-            const int cb = base + 4 + (k0 - gg * G) / 2;
-            wh[u] = __builtin_amdgcn_raw_buffer_load_b32(wr, base, 0, 0);
-#pragma unroll
-            for (int d = 0; d < 4; ++d) wc[u][d] = __builtin_amdgcn_raw_buffer_load_b32(wr, cb + 4 * d, 0, 0);
-        }
-#pragma unroll
-        for (int c = 0; c < XCH; ++c)
-            xv[c] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                                xr, (xrow[c] * Kp + s * kStepK) * 2 + 16 * xcol[c], 0, 0));
-    };
-    auto store_step = [&](int b) {
-#pragma unroll
-        for (int u = 0; u < UNITS; ++u) {
-            u4v o[2][2];
-            dequant32(wc[u], wh[u], wv[u], o);
-            _Float16 *dst = &sw[b][urow[u] * kRowHalves + 32 * uhalf[u]];
-            *reinterpret_cast<u4v *>(dst) = o[0][0];
-            *reinterpret_cast<u4v *>(dst + 8) = o[0][1];
-            *reinterpret_cast<u4v *>(dst + 16) = o[1][0];
-            *reinterpret_cast<u4v *>(dst + 24) = o[1][1];
-        }
-#pragma unroll
-        for (int c = 0; c < XCH; ++c) *reinterpret_cast<u4v *>(&sx[b][xrow[c] * kRowHalves + 8 * xcol[c]]) = xv[c];
+    auto issue = [&](int s, int slot) {
+        issue_step(wr, xr, smem + slot * stage_bytes, wrow, wslot, WDma, xoff, WN, WStage, wave, s,
+                   step_offsets(s, G, gb, groups));
     };
 
     f16x acc[WM][WN];
@@ -188,49 +270,72 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma(const uint8_t *__rest
 #pragma unroll
         for (int j = 0; j < WN; ++j) acc[i][j] = f16x{};
 
-    const int li = lane & 31, lk = 8 * (lane >> 5);
-    load_step(0);
-    store_step(0);
-    __syncthreads();
+    const int li = lane & 31, kq = lane >> 5;
+    int issued = 0;
+    for (; issued < S - 1 && issued < steps; ++issued) issue(issued, issued);
+    int slot = 0;
     for (int s = 0; s < steps; ++s) {
-        const int b = s & 1;
-        if (s + 1 < steps) load_step(s + 1);
+        wait_vm((issued - s - 1) * P);  // this wave's part of step s has landed
+        lds_barrier();                  // every wave's part has; step s - 1's slot is free
+        if (issued < steps) {
+            issue(issued, issued % S);
+            ++issued;
+        }
+        const unsigned char *st = smem + slot * stage_bytes;
+        const StepOffsets so = step_offsets(s, G, gb, groups);
+        // all of the step's LDS operands first, so their latencies overlap
+        unsigned hd[WM][2], c[WM][4];
 #pragma unroll
-        for (int kk = 0; kk < kStepK; kk += 16) {
-            h8 a[WM], bb[WN];
+        for (int i = 0; i < WM; ++i) {
+            const unsigned *wrw = reinterpret_cast<const unsigned *>(st) + (32 * (WM * wave + i) + li) * kWDwords;
+            hd[i][0] = wrw[0];
+            hd[i][1] = wrw[1];
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
-                a[i] = *reinterpret_cast<const h8 *>(&sw[b][(32 * (wm * WM + i) + li) * kRowHalves + kk + lk]);
+            for (int kk = 0; kk < 4; ++kk) c[i][kk] = wrw[2 + 2 * kk + kq];
+        }
+        const unsigned char *sx = st + WStage;
+        h8 b[4][WN];
 #pragma unroll
-            for (int j = 0; j < WN; ++j)
-                bb[j] = *reinterpret_cast<const h8 *>(&sx[b][(32 * (wn * WN + j) + li) * kRowHalves + kk + lk]);
+        for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
+            for (int j = 0; j < WN; ++j) {
+                const int r = 32 * j + li;
+                b[kk][j] = *reinterpret_cast<const h8 *>(sx + r * 128 + 16 * ((2 * kk + kq) ^ (r & 7)));
+            }
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const float s0 = so.valid[0] ? half_bits_f(hd[i][0]) : 0.f;
+            const float s1 = so.valid[1] ? half_bits_f(hd[i][1]) : 0.f;
+            const float z0 = so.valid[0] ? -(half_bits_f(hd[i][0] >> 16) * s0) : 0.f;
+            const float z1 = so.valid[1] ? -(half_bits_f(hd[i][1] >> 16) * s1) : 0.f;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const h8 a = kk < 2 ? dequant8(c[i][kk], s0, z0) : dequant8(c[i][kk], s1, z1);
 #pragma unroll
                 for (int j = 0; j < WN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bb[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[kk][j], acc[i][j], 0, 0, 0);
+            }
         }
-        if (s + 1 < steps) store_step(b ^ 1);
-        __syncthreads();
+        slot = slot == S - 1 ? 0 : slot + 1;
     }
+    wait_vm(0);
 
     // epilogue: lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
-        const int n = n0 + 32 * (wn * WN + j) + li;
+        const int n = n0 + 32 * j + li;
         if (n >= N) continue;
         const float sc = xinv[n];
         float *yc = y + static_cast<size_t>(n) * M;
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const int m = m0 + 32 * (wm * WM + i) + 8 * r4 + 4 * (lane >> 5);
+                const int m = m0 + 32 * (WM * wave + i) + 8 * r4 + 4 * kq;
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     if (m + q < M) yc[m + q] = acc[i][j][4 * r4 + q] * sc;
             }
-        }
     }
 }
 
@@ -261,15 +366,29 @@ void *workspace_at_least(size_t bytes) {
     return ws.ptr;
 }
 
-template <int WM, int WN, int WAVES_M, int WAVES_N>
+template <int WM, int WN>
 int launch_tiles(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y, int M, int N, int K, int Kp, int G,
                  int rb, hipStream_t stream) {
-    constexpr int BM = 32 * WM * WAVES_M, BN = 32 * WN * WAVES_N;
+    constexpr int BM = 128 * WM, BN = 32 * WN;
+    constexpr int stage = kWStage1 * WM + BN * 128;
+    const int S = std::max(2, std::min(4, (80 * 1024) / stage));  // ring depth within 80 KB of LDS
+    const size_t lds = static_cast<size_t>(S) * stage;
+    static bool raised = false;
+    if (lds > 64 * 1024 && !raised) {
+        TQ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(i4_matmul_mfma<WM, WN>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        raised = true;
+    }
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
-    hipLaunchKernelGGL((i4_matmul_mfma<WM, WN, WAVES_M, WAVES_N>), grid, dim3(kThreads), 0, stream, w, xh, xinv, y, M,
-                       N, K, Kp, G, rb);
+    hipLaunchKernelGGL((i4_matmul_mfma<WM, WN>), grid, dim3(kThreads), lds, stream, w, xh, xinv, y, M, N, K, Kp, G,
+                       rb, S);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
+
+// Token blocks of 32 per wave (WN). Measured on MI355X at 9728x2560: one
+// block for <= 32 tokens, two for <= 64, three above (128-token tiles and two
+// row blocks per wave were slower: fewer workgroups, more registers).
+int pick_wn(int N) { return N <= 32 ? 1 : N <= 64 ? 2 : 3; }
 
 }  // namespace
 
@@ -292,12 +411,17 @@ int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, i
     unsigned char *ws = static_cast<unsigned char *>(workspace_at_least(xh_bytes + 4 * static_cast<size_t>(N)));
     _Float16 *xh = reinterpret_cast<_Float16 *>(ws);
     float *xinv = reinterpret_cast<float *>(ws + xh_bytes);
-    hipLaunchKernelGGL(x_to_f16, dim3(N), dim3(256), 0, stream, x, K, static_cast<int>(Kp), xh, xinv);
+    if (Kp <= static_cast<size_t>(256 * kXRegs))
+        hipLaunchKernelGGL(x_to_f16, dim3(N), dim3(256), 0, stream, x, K, static_cast<int>(Kp), xh, xinv);
+    else
+        hipLaunchKernelGGL(x_to_f16_long, dim3(N), dim3(256), 0, stream, x, K, static_cast<int>(Kp), xh, xinv);
     if (hipGetLastError() != hipSuccess) return kLaunchFailed;
     const int ikp = static_cast<int>(Kp), irb = static_cast<int>(rb);
-    if (N <= 32) return launch_tiles<2, 1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
-    if (N <= 64) return launch_tiles<2, 1, 2, 2>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
-    return launch_tiles<2, 2, 2, 2>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+    switch (pick_wn(N)) {
+        case 1: return launch_tiles<1, 1>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+        case 2: return launch_tiles<1, 2>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+        default: return launch_tiles<1, 3>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+    }
 }
 
 }  // namespace tqhip
