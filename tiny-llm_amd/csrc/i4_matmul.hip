@@ -170,7 +170,9 @@ struct StepOffsets {
     int hdr[2], code[2];
     bool valid[2];
 };
-__device__ __forceinline__ StepOffsets step_offsets(int s, int G, int gb, int groups) {
+template <int GT>
+__device__ __forceinline__ StepOffsets step_offsets(int s, int Grt, int gb, int groups) {
+    const int G = GT ? GT : Grt;  // a compile-time group size turns the divisions into shifts
     StepOffsets o;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -218,7 +220,7 @@ __device__ __forceinline__ void issue_step(__amdgpu_buffer_rsrc_t wr, __amdgpu_b
 //   into a ring of S stages issued S - 1 steps ahead. Each wave dequantizes its
 //   A operands from the raw codes in LDS straight into registers; every X (B)
 //   operand read from LDS feeds WM MFMAs.
-template <int WM, int WN>
+template <int WM, int WN, int GT>
 __global__ __launch_bounds__(kThreads) void i4_matmul_mfma(const uint8_t *__restrict__ w,
                                                            const _Float16 *__restrict__ xh,
                                                            const float *__restrict__ xinv, float *__restrict__ y,
@@ -233,6 +235,7 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma(const uint8_t *__rest
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    if constexpr (GT != 0) G = GT;
     const int gb = 4 + G / 2;
     const int groups = (K + G - 1) / G;
     const int steps = Kp / kStepK;
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma(const uint8_t *__rest
     }
     auto issue = [&](int s, int slot) {
         issue_step(wr, xr, smem + slot * stage_bytes, wrow, wslot, WDma, xoff, WN, WStage, wave, s,
-                   step_offsets(s, G, gb, groups));
+                   step_offsets<GT>(s, G, gb, groups));
     };
 
     f16x acc[WM][WN];
@@ -273,16 +276,17 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma(const uint8_t *__rest
     const int li = lane & 31, kq = lane >> 5;
     int issued = 0;
     for (; issued < S - 1 && issued < steps; ++issued) issue(issued, issued);
-    int slot = 0;
+    int slot = 0, islot = issued == S ? 0 : issued;  // ring slots of step s and of the next issue
     for (int s = 0; s < steps; ++s) {
         wait_vm((issued - s - 1) * P);  // this wave's part of step s has landed
         lds_barrier();                  // every wave's part has; step s - 1's slot is free
         if (issued < steps) {
-            issue(issued, issued % S);
+            issue(issued, islot);
             ++issued;
+            islot = islot == S - 1 ? 0 : islot + 1;
         }
         const unsigned char *st = smem + slot * stage_bytes;
-        const StepOffsets so = step_offsets(s, G, gb, groups);
+        const StepOffsets so = step_offsets<GT>(s, G, gb, groups);
         // all of the step's LDS operands first, so their latencies overlap
         unsigned hd[WM][2], c[WM][4];
 #pragma unroll
@@ -366,7 +370,7 @@ void *workspace_at_least(size_t bytes) {
     return ws.ptr;
 }
 
-template <int WM, int WN>
+template <int WM, int WN, int GT>
 int launch_tiles(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y, int M, int N, int K, int Kp, int G,
                  int rb, hipStream_t stream) {
     constexpr int BM = 128 * WM, BN = 32 * WN;
@@ -375,12 +379,12 @@ int launch_tiles(const uint8_t *w, const _Float16 *xh, const float *xinv, float 
     const size_t lds = static_cast<size_t>(S) * stage;
     static bool raised = false;
     if (lds > 64 * 1024 && !raised) {
-        TQ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(i4_matmul_mfma<WM, WN>),
+        TQ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(i4_matmul_mfma<WM, WN, GT>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         raised = true;
     }
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
-    hipLaunchKernelGGL((i4_matmul_mfma<WM, WN>), grid, dim3(kThreads), lds, stream, w, xh, xinv, y, M, N, K, Kp, G,
+    hipLaunchKernelGGL((i4_matmul_mfma<WM, WN, GT>), grid, dim3(kThreads), lds, stream, w, xh, xinv, y, M, N, K, Kp, G,
                        rb, S);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
@@ -417,11 +421,15 @@ int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, i
         hipLaunchKernelGGL(x_to_f16_long, dim3(N), dim3(256), 0, stream, x, K, static_cast<int>(Kp), xh, xinv);
     if (hipGetLastError() != hipSuccess) return kLaunchFailed;
     const int ikp = static_cast<int>(Kp), irb = static_cast<int>(rb);
-    switch (pick_wn(N)) {
-        case 1: return launch_tiles<1, 1>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
-        case 2: return launch_tiles<1, 2>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
-        default: return launch_tiles<1, 3>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+    const int wn = pick_wn(N);
+    if (group_size == 64) {
+        if (wn == 1) return launch_tiles<1, 1, 64>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+        if (wn == 2) return launch_tiles<1, 2, 64>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+        return launch_tiles<1, 3, 64>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
     }
+    if (wn == 1) return launch_tiles<1, 1, 0>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+    if (wn == 2) return launch_tiles<1, 2, 0>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+    return launch_tiles<1, 3, 0>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
 }
 
 }  // namespace tqhip
