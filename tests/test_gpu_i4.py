@@ -103,8 +103,14 @@ def test_bad_shapes_return_codes(gpu):
 
 # qkv / pair on device buffers: one launch over all the matrices (the staged
 # kernel) or one per matrix (rows past its window limit, group sizes it does
-# not cover). Each output must equal the single-matrix launch bit for bit (same
-# kernel configuration, fixed reduction order) and meet the bar against the oracle.
+# not cover). Each output must meet the bar against the oracle and equal the
+# single-matrix launch: bit for bit when both run the same kernel (rows under
+# 24 windows of 64 bytes), else within 1e-6 of the output scale (a single long-row
+# matrix with few tiles runs split-K, which adds the same terms in another order).
+def same_as_single(got, single, K, G, gpu):
+    if gpu.i4_row_bytes(K, G) < 24 * 64:
+        return np.array_equal(got, single)
+    return float(np.max(np.abs(got - single))) <= 1e-6 * max(float(np.max(np.abs(single))), 1e-30)
 @pytest.mark.parametrize("q,kv,K,G", [(896, 128, 896, 64), (4096, 1024, 2560, 64), (100, 17, 520, 40),
                                       (64, 16, 4864, 64), (40, 8, 1000, 128), (24, 24, 200, 6)])
 def test_qkv_dev_one_launch_matches_single_and_oracle(gpu, orc, q, kv, K, G):
@@ -118,7 +124,7 @@ def test_qkv_dev_one_launch_matches_single_and_oracle(gpu, orc, q, kv, K, G):
     for i, (w, m) in enumerate(zip(ws, (q, kv, kv))):
         single = gpu.DeviceBuffer(4 * m)
         gpu.matvec_i4_dev(dws[i], dx, single, m, K, G)
-        assert np.array_equal(got[i], single.download(np.float32, m)), f"qkv matrix {i} differs from its own launch"
+        assert same_as_single(got[i], single.download(np.float32, m), K, G, gpu), f"qkv matrix {i} vs its own launch"
         assert_close(got[i], orc.matvec_i4(w, x, m, K, G, threads=16), f"qkv {i}")
 
 
@@ -133,7 +139,7 @@ def test_pair_dev_one_launch_matches_single_and_oracle(gpu, orc, M, K, G):
         single = gpu.DeviceBuffer(4 * M)
         gpu.matvec_i4_dev(dw, dx, single, M, K, G)
         got = dy.download(np.float32, M)
-        assert np.array_equal(got, single.download(np.float32, M))
+        assert same_as_single(got, single.download(np.float32, M), K, G, gpu)
         assert_close(got, orc.matvec_i4(w, x, M, K, G, threads=16), "pair")
 
 
@@ -152,3 +158,37 @@ def test_run_ops_pair_and_qkv_kinds(gpu, orc):
     gpu.synchronize()
     for w, d, m in zip(ws, dys, (q, kv, kv, 4864, 4864)):
         assert_close(d.download(np.float32, m), orc.matvec_i4(w, x, m, K, G, threads=16), "run_ops")
+
+
+# Split-K path (long rows, few tiles; rows a multiple of 16 bytes): several
+# workgroups per 16-row tile, partial sums added by the last one to arrive.
+@pytest.mark.parametrize("M,K,G", [(896, 4864, 64), (2560, 9728, 64), (2560, 4096, 64), (100, 4864, 64),
+                                   (300, 8192, 128), (17, 1792, 64), (64, 3072, 128)])
+def test_split_k_matches_oracle_and_repeats(gpu, orc, M, K, G):
+    w = gpu.synth_i4(M, K, G, seed=M * 7 + K)
+    x = gpu.synth_normal(K, seed=K)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
+    outs = []
+    for _ in range(3):  # the tile counters must come back to zero after every launch
+        gpu.matvec_i4_dev(dw, dx, dy, M, K, G)
+        outs.append(dy.download(np.float32, M))
+    assert all(np.array_equal(outs[0], o) for o in outs[1:]), "split-K result changed between launches"
+    assert_close(outs[0], orc.matvec_i4(w, x, M, K, G, threads=16), f"split {M}x{K} G{G}")
+
+
+def test_split_k_on_two_streams(gpu, orc):
+    """Launches on different streams use different scratch buffers."""
+    M, K, G = 896, 4864, 64
+    ws = [gpu.synth_i4(M, K, G, seed=s) for s in (1, 2)]
+    xs = [gpu.synth_normal(K, seed=s) for s in (3, 4)]
+    dws = [gpu.DeviceBuffer.from_array(w) for w in ws]
+    dxs = [gpu.DeviceBuffer.from_array(x) for x in xs]
+    dys = [gpu.DeviceBuffer(4 * M) for _ in range(2)]
+    streams = [gpu.Stream(), gpu.Stream()]
+    for _ in range(20):
+        for i in range(2):
+            gpu.matvec_i4_dev(dws[i], dxs[i], dys[i], M, K, G, stream=streams[i])
+    for st in streams:
+        st.synchronize()
+    for i in range(2):
+        assert_close(dys[i].download(np.float32, M), orc.matvec_i4(ws[i], xs[i], M, K, G, threads=16), f"stream {i}")

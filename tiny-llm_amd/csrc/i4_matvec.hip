@@ -34,6 +34,8 @@
 #include "tq_common.h"
 
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
 
 namespace tqhip {
 namespace {
@@ -128,6 +130,7 @@ struct Geom {
     int depth;    // DMA ring slots (DMA-staged kernel)
     // DMA-staged kernel: 1..3 matrices sharing x (pair / qkv), their tiles
     // numbered one after the other; tile_end[j] = tiles of matrices 0..j.
+    int ksplit;  // split-K kernel: workgroups (row-window parts) per tile
     int nmat;
     int tile_end[kMaxGroup];
     int mrows[kMaxGroup];
@@ -973,6 +976,134 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     }
 }
 
+// Split-K variant for long rows and few tiles (down projections): the windows
+// of every tile are split into S parts, one workgroup per (tile, part). A
+// workgroup converts only the activations of its part's groups, DMAs only the
+// part's bytes of its 16 rows, reads the group headers straight from global
+// memory, and leaves 16 partial sums in a scratch buffer. The workgroup that
+// arrives last at the tile's counter adds the S partials in part order
+// (deterministic) and resets the counter to zero for the next launch.
+template <int GT, int CPW, int PW, int NWMAX>
+__global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec_split(
+    const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y, Geom gm,
+    float *__restrict__ partial, unsigned *__restrict__ counter) {
+    static_assert(GT == 64 || GT == 128, "one activation block per thread needs a compile-time group size");
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int NW = gm.NW;
+    const int M = gm.M, rb = gm.row_bytes, gb = gm.gb;
+    const int NWP = (NW + 3) & ~3;
+    const int S = gm.ksplit;
+    const int tile = blockIdx.x / S, part = blockIdx.x - tile * S;
+    const int tb = (gm.T * part) / S, te = (gm.T * (part + 1)) / S;  // windows [tb, te)
+    const int Tp = te - tb;
+    const int pitch = kChunk * Tp;  // LDS bytes per row
+    const int byte_lo = kChunk * tb, byte_hi = min(kChunk * te, rb);
+    const int g_lo = byte_lo / gb, g_hi = (byte_hi - 1) / gb + 1;  // groups the part touches
+    const int ng = g_hi - g_lo;
+
+    unsigned char *stage = smem;                                   // [16][pitch]
+    float *part_sum = reinterpret_cast<float *>(smem + gm.tbuf);   // [16][NWP]
+    XPlanes xp;
+    xp.pl = reinterpret_cast<int8_t *>(part_sum + kTile * NWP);
+    xp.stride = ng * GT;
+    xp.pre = reinterpret_cast<int *>(xp.pl + 3 * xp.stride);
+    xp.gexp = reinterpret_cast<float *>(xp.pre + xp.stride / 8);
+    xp.gbase = g_lo;
+    xp.ngroups = ng;
+
+    // 1. the part's bytes of the 16 rows: Tp DMAs of 1 KB, chunk c = 64 j + lane
+    //    -> row c / (4 Tp), 16-byte column c % (4 Tp); surplus slots repeat the last
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(w, M, rb, tile * kTile);
+#pragma unroll
+    for (int s = 0; s < PW; ++s) {
+        const int j = min(wave + s * NW, Tp - 1);
+        const int c = 64 * j + lane;
+        const int r = c / (4 * Tp), col = c - r * (4 * Tp);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(stage + 1024 * j), 16,
+                                                 r * rb + byte_lo + 16 * col, 0, 0, 0);
+    }
+    // 2. this lane's group headers (row bn, group slot kq of each of its windows)
+    const int t0 = min(tb + (Tp * wave) / NW, te - 1);
+    const int nch_raw = tb + (Tp * (wave + 1)) / NW - (tb + (Tp * wave) / NW);  // 0..CPW
+    const int nch = max(nch_raw, 1);  // an idle wave still addresses one valid window
+    const int bn = lane & 15, kq = lane >> 4;
+    unsigned hraw[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int t = t0 + min(c, nch - 1);
+        const int gq = min((kChunk * t) / gb + kq, gm.Gr - 1);
+        hraw[c] = __builtin_amdgcn_raw_buffer_load_b32(rs, bn * rb + gq * gb, 0, 0);
+    }
+    // 3. the part's activations
+    XFirst xf;
+    load_x_first<GT>(xf, x + g_lo * GT, min(gm.K - g_lo * GT, ng * GT), ng * GT);
+    prepare_x<GT, true>(xp, x + g_lo * GT, min(gm.K - g_lo * GT, ng * GT), ng, ng * GT, xf);
+    wait_vmem(0);
+    for (int i = threadIdx.x; i < kTile * NWP; i += blockDim.x)
+        if (i % NWP >= NW) part_sum[i] = 0.f;  // padding slots of the fixed-order sums
+    lds_barrier();
+    v4i A0[CPW], A1[CPW];
+    float E[CPW], C[CPW];
+    int HO[CPW];
+    unsigned HM[CPW];
+    build_operands<GT, CPW, false>(xp, gm, t0, nch, A0, A1, E, C, HO, HM);
+    float a = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int t = t0 + min(c, nch - 1);
+        const v4i d = *reinterpret_cast<const v4i *>(stage + bn * pitch + kChunk * (t - tb) + 16 * kq);
+        a = window_step(a, d, hraw[c] & HM[c], A0[c], A1[c], E[c], C[c]);
+    }
+    if (nch_raw <= 0) a = 0.f;  // a part one window short of the widest leaves a wave idle
+    a += __shfl_xor(a, 16);
+    a += __shfl_xor(a, 32);
+    if (lane < kTile) part_sum[lane * NWP + wave] = a;
+    __syncthreads();
+    // 4. this part's 16 sums -> scratch; the last part of the tile adds them up
+    __shared__ unsigned last;
+    if (threadIdx.x < kTile) {
+        const float4 *pr = reinterpret_cast<const float4 *>(part_sum + threadIdx.x * NWP);
+        float v = 0.f;
+        for (int q = 0; q < NWP / 4; ++q) {
+            const float4 u = pr[q];
+            v += u.x;
+            v += u.y;
+            v += u.z;
+            v += u.w;
+        }
+        // Device-coherent store (sc1: through the XCD's L2, whose contents the
+        // other XCDs do not see), then wait until it is acknowledged. A
+        // device-scope fence would do the same for all memory by writing back
+        // and invalidating the whole L2 in every workgroup, which costs more
+        // than the matvec itself.
+        __hip_atomic_store(&partial[(static_cast<size_t>(tile) * S + part) * kTile + threadIdx.x], v, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the store has completed
+    }
+    __syncthreads();  // every partial of this workgroup has completed before the arrival is counted
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(&counter[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       static_cast<unsigned>(S - 1)
+                   ? 1u
+                   : 0u;
+    __syncthreads();
+    if (last) {
+        asm volatile("" ::: "memory");
+        if (threadIdx.x < kTile) {
+            const int row = tile * kTile + threadIdx.x;
+            float v = 0.f;
+            for (int p = 0; p < S; ++p)
+                v += __hip_atomic_load(&partial[(static_cast<size_t>(tile) * S + p) * kTile + threadIdx.x],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (row < M) y[row] = v;
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(&counter[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ============================================================================================
 // Register-only kernel (rows of 49..96 windows): operands straight from HBM.
 template <int GT, int CPW>
@@ -1170,6 +1301,90 @@ int launch_lds(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX, DEPTH>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, raised);
 }
 
+// Per-stream scratch of the split-K kernel: partial sums and per-tile arrival
+// counters. The counters start at zero and every launch leaves them at zero.
+// Launches on one stream are ordered; launches on different streams get
+// different buffers.
+struct SplitScratch {
+    float *partial = nullptr;
+    unsigned *counter = nullptr;
+    size_t partial_cap = 0, counter_cap = 0;
+};
+std::mutex g_split_mu;
+std::unordered_map<hipStream_t, SplitScratch> g_split;
+
+int split_scratch(hipStream_t stream, size_t npartial, size_t ncounter, float **partial, unsigned **counter) {
+    std::lock_guard<std::mutex> lock(g_split_mu);
+    SplitScratch &sc = g_split[stream];
+    if (sc.partial_cap < npartial || sc.counter_cap < ncounter) {
+        if (hipStreamSynchronize(stream) != hipSuccess) return kLaunchFailed;  // earlier launches may still use them
+        if (sc.partial) (void)hipFree(sc.partial);
+        if (sc.counter) (void)hipFree(sc.counter);
+        sc = SplitScratch{};
+        const size_t np = std::max(npartial, static_cast<size_t>(1) << 16), nc = std::max(ncounter, static_cast<size_t>(4096));
+        if (hipMalloc(&sc.partial, np * sizeof(float)) != hipSuccess) return kLaunchFailed;
+        if (hipMalloc(&sc.counter, nc * sizeof(unsigned)) != hipSuccess) return kLaunchFailed;
+        if (hipMemset(sc.counter, 0, nc * sizeof(unsigned)) != hipSuccess) return kLaunchFailed;
+        sc.partial_cap = np;
+        sc.counter_cap = nc;
+    }
+    *partial = sc.partial;
+    *counter = sc.counter;
+    return kOk;
+}
+
+template <int GT, int CPW, int PW, int NWMAX>
+int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int Tmax, hipStream_t stream) {
+    static bool raised = false;
+    const int tiles = (gm.M + kTile - 1) / kTile;
+    const int NWP = (gm.NW + 3) & ~3;
+    const int ng = (kChunk * Tmax + gm.gb - 1) / gm.gb + 1;  // groups one part can touch
+    const size_t kp = static_cast<size_t>(ng) * GT;
+    if (kp / 8 > static_cast<size_t>(64 * gm.NW)) return kTooLarge;  // one activation block per thread
+    gm.tbuf = kTile * kChunk * Tmax;
+    gm.ksplit = S;
+    const size_t lds = gm.tbuf + static_cast<size_t>(kTile * NWP) * 4 + 3 * kp + kp / 8 * 4 + ng * 4 + 16;
+    if (lds > kLdsBytes) return kTooLarge;
+    float *partial = nullptr;
+    unsigned *counter = nullptr;
+    const int st = split_scratch(stream, static_cast<size_t>(tiles) * S * kTile, tiles, &partial, &counter);
+    if (st != kOk) return st;
+    if (lds > 64 * 1024 && !raised) {
+        TQ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(i4_matvec_split<GT, CPW, PW, NWMAX>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        raised = true;
+    }
+    hipLaunchKernelGGL((i4_matvec_split<GT, CPW, PW, NWMAX>), dim3(tiles * S), dim3(64 * gm.NW), lds, stream, w, x, y,
+                       gm, partial, counter);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+// Split-K when the rows are long and the tiles few: S parts of at least 8
+// windows, enough workgroups for about two per CU.
+template <int GT>
+int launch_split_for(const uint8_t *w, const float *x, float *y, Geom gm, hipStream_t stream) {
+    const int tiles = (gm.M + kTile - 1) / kTile;
+    const int slots = 2 * device_cus();
+    if (gm.T < 24 || 2 * tiles > slots || gm.row_bytes % 16 != 0) return kTooLarge;
+    const int S = std::min({4, slots / tiles, gm.T / 8});
+    if (S < 2) return kTooLarge;
+    const int Tmax = (gm.T + S - 1) / S;
+    if (Tmax <= 8) {
+        gm.NW = Tmax;
+        return launch_split<GT, 1, 1, 8>(w, x, y, gm, S, Tmax, stream);
+    }
+    if (Tmax <= 16) {
+        gm.NW = (Tmax + 1) / 2;
+        return launch_split<GT, 2, 2, 8>(w, x, y, gm, S, Tmax, stream);
+    }
+    if (Tmax <= 24) {
+        gm.NW = (Tmax + 2) / 3;
+        return launch_split<GT, 3, 3, 8>(w, x, y, gm, S, Tmax, stream);
+    }
+    gm.NW = (Tmax + 2) / 3;
+    return launch_split<GT, 3, 3, 16>(w, x, y, gm, S, Tmax, stream);
+}
+
 template <int GT, int CPW>
 int launch_reg(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
     static bool raised = false;
@@ -1270,7 +1485,12 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
         gm.mw[j] = w;
         gm.my[j] = y;
     }
+    gm.ksplit = 1;
     int st;
+    if (TQ_USE_DMA && (group_size == 64 || group_size == 128)) {
+        st = group_size == 64 ? launch_split_for<64>(w, x, y, gm, stream) : launch_split_for<128>(w, x, y, gm, stream);
+        if (st != kTooLarge) return st;
+    }
     if (group_size == 64)
         st = launch_mfma_for<64>(w, x, y, gm, stream);
     else if (group_size == 128)
@@ -1316,6 +1536,7 @@ int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, cons
     gm.tbuf = 0;
     gm.depth = 0;
     gm.nmat = n;
+    gm.ksplit = 1;
     int end = 0;
     for (int j = 0; j < kMaxGroup; ++j) {
         const int jj = std::min(j, n - 1);  // unused slots repeat the last matrix (never selected)
