@@ -165,13 +165,14 @@ def headline(tq, stream, reps=20):
             "rotation": "3 copies, 657 MB"}
 
 
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "i4_matvec_dma_decode_step_traffic.json")
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "i4_matvec_pipe_decode_step_traffic.json")
 
 
 def roofline(tq, work, stream, reps):
-    """The in_dim=896 launches (qkv, o, gate/up pair, lm_head) all run the staged
-    MFMA matvec with 8 windows per row (i4_matvec_dma2<64,1,1,8> for the layer
-    projections, i4_matvec_dma<64,1,1,8> for lm_head). Timed back to back in
+    """The in_dim=896 launches (qkv, o, gate/up pair, lm_head) all run the
+    register-path MFMA matvec with 8 windows per row, one per wave
+    (i4_matvec_pipe<64,1,8,2,true> for the fused qkv and gate/up launches,
+    i4_matvec_pipe<64,1,8,2,false> for o and lm_head). Timed back to back in
     step order with events at both ends; back-to-back launches leave no gaps,
     so the mean per launch is the kernels' mean duration."""
     dom = [i for i, k in enumerate(work.op_in_dim) if k == HIDDEN]
@@ -185,8 +186,8 @@ def roofline(tq, work, stream, reps):
             traffic = json.load(f).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         pass
-    return {"bound": "hbm", "kernel": "i4_matvec_dma2<64,1,1,8> + i4_matvec_dma<64,1,1,8> (every in_dim=896 "
-                                      "launch: qkv, o, gate/up pair, lm_head)",
+    return {"bound": "hbm", "kernel": "i4_matvec_pipe<64,1,8,2,true|false> (every in_dim=896 launch: qkv, o, "
+                                      "gate/up pair, lm_head)",
             "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
             "traffic": traffic, "launches": len(dom), "bytes_per_launch": b_dom // len(dom),
             "avg_launch_us": round(ms * 1e3 / len(dom), 3)}

@@ -65,6 +65,9 @@ constexpr int kDmaWavesPerCu = TQ_DMA_WAVES_PER_CU;
 // Occupancy bound of a DMA-staged instance: three windows per wave need more
 // than the 64 VGPRs that eight waves per SIMD leave.
 constexpr int dma_waves_per_simd(int cpw) { return cpw >= 3 ? std::min(6, kDmaWavesPerCu / 4) : kDmaWavesPerCu / 4; }
+constexpr int kPipeWavesPerSimd = 4;     // register-path kernel: launch bound (VGPR budget 128)
+constexpr int kPipeSlots = 2;            // register-path kernel: tiles loaded ahead of the one computed
+constexpr int kPipeWgsPerCu = 2;         // register-path kernel: workgroups per CU in the grid
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
 constexpr int kMaxDepth = 8;              // DMA ring slots at most
 constexpr int kMaxGroup = 3;              // matrices sharing x in one DMA-staged launch (qkv)
@@ -138,23 +141,54 @@ struct Geom {
     float *my[kMaxGroup];
 };
 
-// Matrix j of the group that holds global tile t, and t's index within it
-// (selects, not indexing: a dynamic index into the kernel argument would put
-// it in scratch memory).
+// Matrix of the group that holds global tile t, and t's index within it.
 struct TileRef {
     const uint8_t *w;
     float *y;
     int M, tile;
 };
-__device__ inline TileRef locate_tile(const Geom &gm, int t) {
-    const bool a = t >= gm.tile_end[0], b = t >= gm.tile_end[1];
-    TileRef r;
-    r.w = b ? gm.mw[2] : a ? gm.mw[1] : gm.mw[0];
-    r.y = b ? gm.my[2] : a ? gm.my[1] : gm.my[0];
-    r.M = b ? gm.mrows[2] : a ? gm.mrows[1] : gm.mrows[0];
-    r.tile = t - (b ? gm.tile_end[1] : a ? gm.tile_end[0] : 0);
-    return r;
-}
+
+// A store of one output through a global-memory pointer. A pointer rebuilt
+// from an integer (TileMap) has lost its address space, and a plain store
+// through it becomes a flat store, which also counts against the LDS wait
+// counter: every later LDS barrier would then wait for the store to complete.
+__device__ inline void store_y(float *p, float v) { *(__attribute__((address_space(1))) float *)p = v; }
+
+// Tile -> matrix lookup for the 1..3 matrices of gm (tiles numbered one
+// matrix after the other): the base values plus differences added under the
+// two comparisons, copied out of the kernel argument once, so a lookup inside
+// a loop is a few scalar selects and adds. (Selects among the fields
+// themselves are turned by the compiler into an indexed load -- from the
+// kernel argument, or from scratch memory for a local copy -- issued and
+// waited for inside the loop.)
+struct TileMap {
+    unsigned long long w0, dw1, dw2, y0, dy1, dy2;
+    int M0, dM1, dM2, end0, end1;
+    __device__ explicit TileMap(const Geom &gm) {
+        const unsigned long long w1 = reinterpret_cast<unsigned long long>(gm.mw[1]);
+        const unsigned long long y1 = reinterpret_cast<unsigned long long>(gm.my[1]);
+        w0 = reinterpret_cast<unsigned long long>(gm.mw[0]);
+        dw1 = w1 - w0;
+        dw2 = reinterpret_cast<unsigned long long>(gm.mw[2]) - w1;
+        y0 = reinterpret_cast<unsigned long long>(gm.my[0]);
+        dy1 = y1 - y0;
+        dy2 = reinterpret_cast<unsigned long long>(gm.my[2]) - y1;
+        M0 = gm.mrows[0];
+        dM1 = gm.mrows[1] - gm.mrows[0];
+        dM2 = gm.mrows[2] - gm.mrows[1];
+        end0 = gm.tile_end[0];
+        end1 = gm.tile_end[1];
+    }
+    __device__ TileRef at(int t) const {
+        const bool a = t >= end0, b = t >= end1;
+        TileRef r;
+        r.w = reinterpret_cast<const uint8_t *>(w0 + (a ? dw1 : 0ull) + (b ? dw2 : 0ull));
+        r.y = reinterpret_cast<float *>(y0 + (a ? dy1 : 0ull) + (b ? dy2 : 0ull));
+        r.M = M0 + (a ? dM1 : 0) + (b ? dM2 : 0);
+        r.tile = t - (a ? end0 : 0) - (b ? end1 - end0 : 0);
+        return r;
+    }
+};
 
 // LDS view of an activation set-up: groups gbase .. gbase+n-1 (the whole
 // vector for a workgroup-wide set-up, or the few groups one wave's windows
@@ -788,8 +822,10 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     load_x_first<GT>(xf, x, gm.K, Kp);
 
     const int tiles = gm.tile_end[gm.nmat - 1];
-    const int ntile = blockIdx.x < static_cast<unsigned>(tiles) ? (tiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-    auto tile_of = [&](int i) { return static_cast<int>(blockIdx.x + static_cast<unsigned>(i) * gridDim.x); };
+    const int wg = blockIdx.x, nwg = gridDim.x;
+    const int ntile = wg < tiles ? (tiles - 1 - wg) / nwg + 1 : 0;
+    auto tile_of = [&](int i) { return wg + i * nwg; };
+    const TileMap map(gm);
     const int last = max(ntile - 1, 0);
 
     // 1 KB pieces of a tile this wave moves (piece j -> wave j % NW). Every
@@ -805,7 +841,7 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
         poff[s] = pdst[s] + 16 * lane;
     }
     auto dma = [&](int i, unsigned char *dst) {
-        const TileRef r = locate_tile(gm, tile_of(i));
+        const TileRef r = map.at(tile_of(i));
         dma_tile(r.w, r.M, rb, r.tile, dst, poff, pdst, PW);
     };
     // the first three tiles go out before the activation set-up (repeats of
@@ -847,9 +883,9 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
                 s += v.z;
                 s += v.w;
             }
-            const TileRef r = locate_tile(gm, tile_of(i));
+            const TileRef r = map.at(tile_of(i));
             const int row = r.tile * kTile + threadIdx.x;
-            if (row < r.M) r.y[row] = s;
+            if (row < r.M) store_y(r.y + row, s);
         }
     };
 
@@ -882,14 +918,20 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     if (ntile > 0) reduce_prev(ntile - 1);
 }
 
-// Small-grid variant of i4_matvec_dma: every workgroup owns at most two tiles
-// (blockIdx.x and blockIdx.x + gridDim.x), as in decode-size projections. The
-// tiles' DMAs go out first, the activation loads after them, and the set-up
-// waits for all of them at once: no ring, no repeated tiles.
-template <int GT, int CPW, int PW, int NWMAX>
-__global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec_dma2(const uint8_t *__restrict__ w,
-                                                                              const float *__restrict__ x,
-                                                                              float *__restrict__ y, Geom gm) {
+// Register-path kernel: every wave loads its own windows of each tile straight
+// into VGPRs (16 rows x 16 bytes per window load, plus the group headers), P
+// tiles ahead of the one it computes. No weight bytes pass through LDS; LDS
+// holds the activation set-up and the per-wave partial sums, reduced in fixed
+// order after one LDS-only barrier per tile. Tiles go round-robin over the
+// workgroups (blockIdx.x + k * gridDim.x) across the 1..3 matrices of gm.
+// Every wave issues the same loads for every tile slot (zero-length loads past
+// its last tile), so the compiler's waits count exactly the loads in flight.
+template <int GT, int CPW, int NWMAX, int P, bool GROUP>
+__global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(const uint8_t *__restrict__ w,
+                                                                         const float *__restrict__ x,
+                                                                         float *__restrict__ y, Geom gm) {
+    // GROUP: 1..3 matrices through gm.mw / gm.my / gm.mrows; else the one
+    // matrix w -> y of gm.M rows (fewer scalar instructions per tile)
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -898,10 +940,7 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     const int G = GT ? GT : gm.G;
     const int Kp = gm.Gr * G;
     const int NWP = (NW + 3) & ~3;
-    const int tbuf = gm.tbuf;
-
-    unsigned char *stage = smem;                               // [2][tbuf]
-    float *part = reinterpret_cast<float *>(smem + 2 * tbuf);  // [2][16][NWP]
+    float *part = reinterpret_cast<float *>(smem);  // [2][16][NWP]
     XPlanes xp;
     xp.pl = reinterpret_cast<int8_t *>(part + 2 * kTile * NWP);
     xp.stride = Kp;
@@ -909,70 +948,97 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
     xp.gbase = 0;
     xp.ngroups = gm.Gr;
-
-    const int tiles = gm.tile_end[gm.nmat - 1];
-    const int t0i = blockIdx.x, t1i = blockIdx.x + gridDim.x;
-    const int ntile = (t0i < tiles ? 1 : 0) + (t1i < tiles ? 1 : 0);
-    if (ntile == 0) return;  // (the host sizes the grid so this does not happen)
-    int poff[PW], pdst[PW];
-#pragma unroll
-    for (int s = 0; s < PW; ++s) {
-        const int j = min(wave + s * NW, gm.pieces - 1);
-        pdst[s] = min(kPiece * j, tbuf - kPiece);
-        poff[s] = pdst[s] + 16 * lane;
-    }
-    {
-        const TileRef r = locate_tile(gm, t0i);
-        dma_tile(r.w, r.M, rb, r.tile, stage, poff, pdst, PW);
-    }
-    if (ntile > 1) {
-        const TileRef r = locate_tile(gm, t1i);
-        dma_tile(r.w, r.M, rb, r.tile, stage + tbuf, poff, pdst, PW);
-    }
     XFirst xf;
     load_x_first<GT>(xf, x, gm.K, Kp);
-    prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
-    wait_vmem(0);   // this wave's tile pieces (the activation loads are already in)
-    for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x)
-        if (i % NWP >= NW) part[i] = 0.f;  // padding slots of the fixed-order sums
-    lds_barrier();  // every wave's pieces and activation planes are in LDS
+
+    const int tiles = gm.tile_end[gm.nmat - 1];
+    const int wg = blockIdx.x, nwg = gridDim.x;  // tile of round k: wg + k * nwg
+    const int ntile = wg < tiles ? (tiles - 1 - wg) / nwg + 1 : 0;
+    const int nround = (ntile + P - 1) / P * P;  // padded to whole rounds of the P register slots
     const int t0 = (gm.T * wave) / NW;
-    const int nch = (gm.T * (wave + 1)) / NW - t0;
+    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
+    const int bn = lane & 15, kq = lane >> 4;
+    int DO[CPW], HOr[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) DO[c] = bn * rb + kChunk * (t0 + min(c, nch - 1)) + 16 * kq;
+
+    // rows of this workgroup's k-th tile; past its last tile: no rows (every load reads 0)
+    const TileMap map(gm);
+    auto tile_of = [&](int t) {
+        if constexpr (GROUP) return map.at(t);
+        TileRef r;
+        r.w = w;
+        r.y = y;
+        r.M = gm.M;
+        r.tile = t;
+        return r;
+    };
+    auto tile_rsrc = [&](int k) {
+        const bool live = k < ntile;
+        const TileRef r = tile_of(live ? wg + k * nwg : 0);
+        return rows_rsrc(r.w, live ? r.M : 0, rb, r.tile * kTile);
+    };
+    v4i d[P][CPW];
+    unsigned h[P][CPW];
+    auto load_d = [&](int k, v4i (&dd)[CPW]) {
+        const __amdgpu_buffer_rsrc_t rs = tile_rsrc(k);
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) dd[c] = __builtin_amdgcn_raw_buffer_load_b128(rs, DO[c], 0, 0);
+    };
+    auto load_h = [&](int k, unsigned (&hh)[CPW]) {
+        const __amdgpu_buffer_rsrc_t rs = tile_rsrc(k);
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) hh[c] = __builtin_amdgcn_raw_buffer_load_b32(rs, HOr[c], 0, 0);
+    };
+    // the first P tiles' code bytes go out before the activation set-up, their
+    // headers once the set-up has located them
+#pragma unroll
+    for (int s = 0; s < P; ++s) load_d(s, d[s]);
+
+    prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
+    lds_barrier();
     v4i A0[CPW], A1[CPW];
     float E[CPW], C[CPW];
     int HO[CPW];
     unsigned HM[CPW];
-    build_operands<GT, CPW, false>(xp, gm, t0, nch, A0, A1, E, C, HO, HM);  // nothing in flight any more
-    const int bn = lane & 15, kq = lane >> 4;
-    for (int i = 0; i < ntile; ++i) {
-        const unsigned char *buf = stage + i * tbuf;
-        float a = 0.f;
+    build_operands<GT, CPW, true>(xp, gm, t0, nch, A0, A1, E, C, HO, HM);
 #pragma unroll
-        for (int c = 0; c < CPW; ++c) {
-            const int t = t0 + min(c, nch - 1);
-            const v4i d = *reinterpret_cast<const v4i *>(buf + bn * rb + kChunk * t + 16 * kq);
-            const unsigned h = *reinterpret_cast<const unsigned *>(buf + bn * rb + HO[c]) & HM[c];
-            a = window_step(a, d, h, A0[c], A1[c], E[c], C[c]);
+    for (int c = 0; c < CPW; ++c) HOr[c] = bn * rb + HO[c];
+#pragma unroll
+    for (int s = 0; s < P; ++s) load_h(s, h[s]);
+    for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x) lds_write_u32(part + i, 0u);  // padding slots stay 0
+    lds_barrier();
+
+    for (int k0 = 0; k0 < nround; k0 += P) {
+#pragma unroll
+        for (int s = 0; s < P; ++s) {
+            const int k = k0 + s;
+            float a = 0.f;
+#pragma unroll
+            for (int c = 0; c < CPW; ++c) a = window_step(a, d[s][c], h[s][c] & HM[c], A0[c], A1[c], E[c], C[c]);
+            load_d(k + P, d[s]);  // this slot's next tile
+            load_h(k + P, h[s]);
+            a += __shfl_xor(a, 16);  // the four group slots of each row
+            a += __shfl_xor(a, 32);
+            float *pb = part + (k & 1) * (kTile * NWP);
+            if (lane < kTile) lds_write_u32(pb + lane * NWP + wave, __builtin_bit_cast(unsigned, a));
+            // every wave's sums of tile k are in; the buffer written next (tile
+            // k + 1) was read before this barrier
+            lds_barrier();
+            if (wave == 0 && lane < kTile && k < ntile) {
+                float sum = 0.f;
+                for (int q = 0; q < NWP / 4; ++q) {  // fixed order; padding slots hold 0
+                    const float4 v = lds_read_f4(pb + lane * NWP + 4 * q);
+                    sum += v.x;
+                    sum += v.y;
+                    sum += v.z;
+                    sum += v.w;
+                }
+                const TileRef r = tile_of(wg + k * nwg);
+                const int row = r.tile * kTile + lane;
+                if (row < r.M) store_y(r.y + row, sum);
+            }
         }
-        a += __shfl_xor(a, 16);
-        a += __shfl_xor(a, 32);
-        if (lane < kTile) part[i * (kTile * NWP) + lane * NWP + wave] = a;
-    }
-    __syncthreads();
-    if (threadIdx.x < kTile * ntile) {
-        const int i = threadIdx.x / kTile, rr = threadIdx.x % kTile;
-        const float4 *pr = reinterpret_cast<const float4 *>(part + i * (kTile * NWP) + rr * NWP);
-        float s = 0.f;
-        for (int q = 0; q < NWP / 4; ++q) {  // fixed order
-            const float4 v = pr[q];
-            s += v.x;
-            s += v.y;
-            s += v.z;
-            s += v.w;
-        }
-        const TileRef r = locate_tile(gm, i == 0 ? t0i : t1i);
-        const int row = r.tile * kTile + rr;
-        if (row < r.M) r.y[row] = s;
     }
 }
 
@@ -1219,6 +1285,22 @@ int device_cus() {
     return cus;
 }
 
+// Lets `fn` take `lds` bytes of dynamic LDS. Above the default 64 KB the
+// limit is raised once per kernel, to what the CU's 160 KB leaves beside the
+// kernel's static LDS; `limit` caches that figure (0: not raised yet).
+int fit_dynamic_lds(const void *fn, size_t lds, size_t &limit) {
+    if (lds <= 64 * 1024) return kOk;
+    if (limit == 0) {
+        hipFuncAttributes attr{};
+        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
+        if (attr.sharedSizeBytes >= static_cast<size_t>(kLdsBytes)) return kTooLarge;
+        const size_t cap = kLdsBytes - attr.sharedSizeBytes;
+        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(cap)));
+        limit = cap;
+    }
+    return lds <= limit ? kOk : kTooLarge;
+}
+
 size_t xplanes_bytes(const Geom &gm) {
     const size_t Kp = static_cast<size_t>(gm.Gr) * gm.G;
     return 3 * Kp + (Kp / 8) * 4 + static_cast<size_t>(gm.Gr) * 4;
@@ -1226,20 +1308,32 @@ size_t xplanes_bytes(const Geom &gm) {
 
 template <typename KernelT>
 int launch_with_lds(KernelT kernel, int grid, int threads, size_t lds, const uint8_t *w, const float *x, float *y,
-                    const Geom &gm, hipStream_t stream, bool &raised) {
-    if (lds > 160 * 1024) return kTooLarge;
-    if (lds > 64 * 1024 && !raised) {
-        TQ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        raised = true;
-    }
+                    const Geom &gm, hipStream_t stream, size_t &limit) {
+    const int fit = fit_dynamic_lds(reinterpret_cast<const void *>(kernel), lds, limit);
+    if (fit != kOk) return fit;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), lds, stream, w, x, y, gm);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
+template <int GT, int CPW, int NWMAX>
+int launch_pipe(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
+    static size_t limit = 0;
+    const int tiles = gm.tile_end[gm.nmat - 1];
+    const int NWP = (gm.NW + 3) & ~3;
+    const size_t lds = static_cast<size_t>(2 * kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
+    const int grid = std::max(1, std::min(tiles, device_cus() * kPipeWgsPerCu));
+    if (gm.nmat > 1) {
+        static size_t limit_group = 0;
+        return launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, kPipeSlots, true>, grid, 64 * gm.NW, lds, w, x, y, gm,
+                               stream, limit_group);
+    }
+    return launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, kPipeSlots, false>, grid, 64 * gm.NW, lds, w, x, y, gm, stream,
+                           limit);
+}
+
 template <int GT, int CPW, int PW, int NWMAX>
 int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
-    static bool raised = false;
+    static size_t limit = 0;
     const int tiles = gm.tile_end[gm.nmat - 1];
     const int NWP = (gm.NW + 3) & ~3;
     Geom g2 = gm;
@@ -1253,20 +1347,14 @@ int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
         return kTooLarge;  // the activation set-up assumes one 8-element block per thread
     int wgs = std::max(1, std::min(4, 4 * dma_waves_per_simd(CPW) / gm.NW));
     {
-        // at most two tiles per workgroup: the small-grid kernel, one wave of workgroups
-        static bool raised2 = false;
+        // The DMA ring pays off only for long rows over many tiles: one window
+        // per wave, or at most two tiles per workgroup slot, run faster on the
+        // register path.
         const size_t lds2 = 2 * tbuf + fixed;
         int wgs2 = wgs;
         while (wgs2 > 1 && static_cast<size_t>(wgs2) * lds2 > kLdsBytes) --wgs2;
         const int slots = device_cus() * wgs2;
-        if (lds2 <= kLdsBytes && tiles <= 2 * slots) {
-            Geom g2 = gm;
-            g2.tbuf = static_cast<int>(tbuf);
-            g2.depth = 2;
-            const int grid2 = tiles <= slots ? tiles : (tiles + 1) / 2;
-            return launch_with_lds(i4_matvec_dma2<GT, CPW, PW, NWMAX>, grid2, 64 * gm.NW, lds2, w, x, y, g2, stream,
-                                   raised2);
-        }
+        if (CPW == 1 || tiles <= 2 * slots) return launch_pipe<GT, CPW, NWMAX>(w, x, y, gm, stream);
     }
     while (wgs > 1 && static_cast<size_t>(wgs) * (3 * tbuf + fixed) > kLdsBytes) --wgs;
     if (3 * tbuf + fixed > kLdsBytes) return kTooLarge;
@@ -1279,13 +1367,13 @@ int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     g2.tbuf = static_cast<int>(tbuf);
     g2.depth = depth;
     const size_t lds = depth * tbuf + fixed;
-    return launch_with_lds(i4_matvec_dma<GT, CPW, PW, NWMAX>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, raised);
+    return launch_with_lds(i4_matvec_dma<GT, CPW, PW, NWMAX>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, limit);
 }
 
 template <int GT, int CPW, int PW, int NWMAX, int DEPTH = TQ_LDS_DEPTH>
 int launch_lds(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
     if (TQ_USE_DMA) return launch_dma<GT, CPW, PW, NWMAX>(w, x, y, gm, stream);
-    static bool raised = false;
+    static size_t limit = 0;
     const int tiles = (gm.M + kTile - 1) / kTile;
     const int NWP = (gm.NW + 3) & ~3;
     const size_t tbuf = static_cast<size_t>(kTile) * gm.rbp + kChunk;
@@ -1298,7 +1386,7 @@ int launch_lds(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     const int by_waves = std::max(1, kWavesPerCu / NWMAX);
     const int by_lds = std::max(1, static_cast<int>((160 * 1024) / lds));
     const int grid = std::max(1, std::min(tiles, device_cus() * std::min(by_waves, by_lds)));
-    return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX, DEPTH>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, raised);
+    return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX, DEPTH>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, limit);
 }
 
 // Per-stream scratch of the split-K kernel: partial sums and per-tile arrival
@@ -1335,7 +1423,7 @@ int split_scratch(hipStream_t stream, size_t npartial, size_t ncounter, float **
 
 template <int GT, int CPW, int PW, int NWMAX>
 int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int Tmax, hipStream_t stream) {
-    static bool raised = false;
+    static size_t limit = 0;
     const int tiles = (gm.M + kTile - 1) / kTile;
     const int NWP = (gm.NW + 3) & ~3;
     const int ng = (kChunk * Tmax + gm.gb - 1) / gm.gb + 1;  // groups one part can touch
@@ -1349,11 +1437,8 @@ int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int
     unsigned *counter = nullptr;
     const int st = split_scratch(stream, static_cast<size_t>(tiles) * S * kTile, tiles, &partial, &counter);
     if (st != kOk) return st;
-    if (lds > 64 * 1024 && !raised) {
-        TQ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(i4_matvec_split<GT, CPW, PW, NWMAX>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        raised = true;
-    }
+    const int fit = fit_dynamic_lds(reinterpret_cast<const void *>(i4_matvec_split<GT, CPW, PW, NWMAX>), lds, limit);
+    if (fit != kOk) return fit;
     hipLaunchKernelGGL((i4_matvec_split<GT, CPW, PW, NWMAX>), dim3(tiles * S), dim3(64 * gm.NW), lds, stream, w, x, y,
                        gm, partial, counter);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
@@ -1387,12 +1472,12 @@ int launch_split_for(const uint8_t *w, const float *x, float *y, Geom gm, hipStr
 
 template <int GT, int CPW>
 int launch_reg(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
-    static bool raised = false;
+    static size_t limit = 0;
     const int tiles = (gm.M + kTile - 1) / kTile;
     const int NWP = (gm.NW + 3) & ~3;
     const size_t lds = static_cast<size_t>(kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
     const int grid = std::max(1, std::min(tiles, device_cus()));
-    return launch_with_lds(i4_matvec_reg<GT, CPW>, grid, 64 * gm.NW, lds, w, x, y, gm, stream, raised);
+    return launch_with_lds(i4_matvec_reg<GT, CPW>, grid, 64 * gm.NW, lds, w, x, y, gm, stream, limit);
 }
 
 // Picks windows-per-wave, pieces-per-wave and waves for a row of T 64-byte windows.
