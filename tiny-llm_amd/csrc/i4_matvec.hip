@@ -457,6 +457,25 @@ __device__ inline void load_x_wave(XFirst &xf, const float *__restrict__ x, int 
 // windows t0 .. t0+nch-1 (CPW slots; unused slots get a zero operand).
 // HIDDEN: read LDS through lds_read_* (needed where global->LDS transfers are
 // in flight, which the compiler would otherwise wait for before every read).
+// Header offset (within its row) and mask of the group slot each lane reads
+// for each of this wave's windows: the same values build_operands produces,
+// from the geometry alone, so the header loads can go out before the
+// activation set-up.
+template <int GT, int CPW>
+__device__ inline void header_slots(const Geom &gm, int t0, int nch, int (&HO)[CPW], unsigned (&HM)[CPW]) {
+    const int gb = GT ? kI4Header + GT / 2 : gm.gb;
+    const int kq = (threadIdx.x & 63) >> 4;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int t = t0 + min(c, nch - 1);
+        const int gq = (kChunk * t) / gb + kq;
+        const int wend = min(kChunk * (t + 1), gm.row_bytes);
+        const bool valid = c < nch && gq < gm.Gr && gq * gb < wend;
+        HO[c] = valid ? gq * gb : 0;
+        HM[c] = valid ? 0xFFFFFFFFu : 0u;
+    }
+}
+
 template <int GT, int CPW, bool HIDDEN = false>
 __device__ void build_operands(const XPlanes &xp, const Geom &gm, int t0, int nch, v4i (&A0)[CPW], v4i (&A1)[CPW],
                                float (&E)[CPW], float (&C)[CPW], int (&HO)[CPW], unsigned (&HM)[CPW]) {
@@ -954,7 +973,6 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
     const int tiles = gm.tile_end[gm.nmat - 1];
     const int wg = blockIdx.x, nwg = gridDim.x;  // tile of round k: wg + k * nwg
     const int ntile = wg < tiles ? (tiles - 1 - wg) / nwg + 1 : 0;
-    const int nround = (ntile + P - 1) / P * P;  // padded to whole rounds of the P register slots
     const int t0 = (gm.T * wave) / NW;
     const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
     const int bn = lane & 15, kq = lane >> 4;
@@ -990,25 +1008,38 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
 #pragma unroll
         for (int c = 0; c < CPW; ++c) hh[c] = __builtin_amdgcn_raw_buffer_load_b32(rs, HOr[c], 0, 0);
     };
-    // the first P tiles' code bytes go out before the activation set-up, their
-    // headers once the set-up has located them
+    // The first P tiles' codes go out before the activation set-up. With one
+    // window per wave their headers go with them (their offsets depend on the
+    // geometry only); with more, after the set-up (measured faster there).
+    int HO[CPW];
+    unsigned HM[CPW];
+    header_slots<GT, CPW>(gm, t0, nch, HO, HM);
 #pragma unroll
-    for (int s = 0; s < P; ++s) load_d(s, d[s]);
+    for (int c = 0; c < CPW; ++c) HOr[c] = bn * rb + HO[c];
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+        load_d(s, d[s]);
+        if constexpr (CPW == 1) load_h(s, h[s]);
+    }
 
     prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
     lds_barrier();
     v4i A0[CPW], A1[CPW];
     float E[CPW], C[CPW];
-    int HO[CPW];
-    unsigned HM[CPW];
-    build_operands<GT, CPW, true>(xp, gm, t0, nch, A0, A1, E, C, HO, HM);
+    int HO2[CPW];
+    unsigned HM2[CPW];
+    build_operands<GT, CPW, true>(xp, gm, t0, nch, A0, A1, E, C, HO2, HM2);  // (the same header slots)
+    if constexpr (CPW > 1) {
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) HOr[c] = bn * rb + HO[c];
-#pragma unroll
-    for (int s = 0; s < P; ++s) load_h(s, h[s]);
+        for (int s = 0; s < P; ++s) load_h(s, h[s]);
+    }
     for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x) lds_write_u32(part + i, 0u);  // padding slots stay 0
     lds_barrier();
 
+    // Whole rounds of the P register slots: every slot is loaded and computed
+    // the same way in every round (zero-length loads past the last tile),
+    // which keeps the compiler's waits exact.
+    const int nround = (ntile + P - 1) / P * P;
     for (int k0 = 0; k0 < nround; k0 += P) {
 #pragma unroll
         for (int s = 0; s < P; ++s) {
@@ -1040,6 +1071,7 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
             }
         }
     }
+    wait_vmem(0);  // the loads issued past the last tile have returned before the wave ends
 }
 
 // Split-K variant for long rows and few tiles (down projections): the windows
