@@ -11,11 +11,12 @@
 //      overflow and gives every token the full 11-bit significand; 2^-e_n is
 //      applied exactly in the epilogue.
 //   2. i4_matmul_mfma: workgroup tiles of BM weight rows x BN tokens, 64 K
-//      elements per step. Each step the workgroup loads its W slice
-//      (group header + 16 code bytes per thread-unit) and the fp16 X slice
-//      into registers one step ahead, dequantizes W as q * scale - zero * scale
-//      with one rounding to fp16 (v_fma_mix) into LDS, and contracts with
-//      v_mfma_f32_32x32x16_f16 (fp32 accumulation).
+//      elements per step. Global -> LDS DMA brings each step's raw W slice
+//      (group headers + packed codes) and fp16 X slice into a ring of 2-4
+//      stages, issued stages - 1 steps ahead. Each wave dequantizes its W
+//      operands from the raw codes in LDS straight into registers as
+//      q * scale - zero * scale with one rounding to fp16 (v_fma_mix), and
+//      contracts with v_mfma_f32_32x32x16_f16 (fp32 accumulation).
 //      fp16 and bf16 MFMA run at the same rate on gfx950; fp16 keeps 8x
 //      finer rounding of both operands.
 // Other group sizes: one i4 matvec per token column.
