@@ -1349,18 +1349,25 @@ int launch_with_lds(KernelT kernel, int grid, int threads, size_t lds, const uin
 
 template <int GT, int CPW, int NWMAX>
 int launch_pipe(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
-    static size_t limit = 0;
     const int tiles = gm.tile_end[gm.nmat - 1];
     const int NWP = (gm.NW + 3) & ~3;
     const size_t lds = static_cast<size_t>(2 * kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
     const int grid = std::max(1, std::min(tiles, device_cus() * kPipeWgsPerCu));
+    // one tile per workgroup: nothing to load ahead (a second register slot
+    // would only add a round of zero-length loads and an idle iteration)
+    const bool one = tiles <= grid;
     if (gm.nmat > 1) {
-        static size_t limit_group = 0;
-        return launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, kPipeSlots, true>, grid, 64 * gm.NW, lds, w, x, y, gm,
-                               stream, limit_group);
+        static size_t limit_g1 = 0, limit_g = 0;
+        return one ? launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, 1, true>, grid, 64 * gm.NW, lds, w, x, y, gm,
+                                     stream, limit_g1)
+                   : launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, kPipeSlots, true>, grid, 64 * gm.NW, lds, w, x, y,
+                                     gm, stream, limit_g);
     }
-    return launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, kPipeSlots, false>, grid, 64 * gm.NW, lds, w, x, y, gm, stream,
-                           limit);
+    static size_t limit_1 = 0, limit = 0;
+    return one ? launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, 1, false>, grid, 64 * gm.NW, lds, w, x, y, gm, stream,
+                                 limit_1)
+               : launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, kPipeSlots, false>, grid, 64 * gm.NW, lds, w, x, y, gm,
+                                 stream, limit);
 }
 
 template <int GT, int CPW, int PW, int NWMAX>
