@@ -33,7 +33,11 @@ def test_matmul_vq2_golden_decomposes(gpu):
     assert_close(gpu.matmul_vq2(f["w"], f["x"], M, K, N), f["y"], 1e-5, "matmul_vq2")
 
 
-@pytest.mark.parametrize("M,K", [(3072, 1024), (1, 4), (513, 896), (4864, 896), (100, 52), (77, 1000), (16384, 2048)])
+# aligned index rows (in_dim % 16 == 0): conflict-free kernel with one chunk per
+# row, several, a partial last chunk and many tiles per wave; the rest: the
+# byte-load kernel
+@pytest.mark.parametrize("M,K", [(3072, 1024), (1, 4), (513, 896), (4864, 896), (100, 52), (77, 1000), (16384, 2048),
+                                 (2001, 3056), (151936, 896), (3, 16)])
 def test_vq2_device_api_matches_oracle(gpu, orc, M, K):
     w = gpu.synth_vq2(M, K, seed=M + K)
     x = gpu.synth_normal(K, seed=K)

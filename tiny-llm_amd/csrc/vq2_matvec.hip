@@ -4,12 +4,17 @@
 // reference's matvec_vq2_ref (kernels/matvec/matvec_vq2_ref.cpp:52-81), on the
 // layout [codebook 256 x 4 fp16 = 2048 B][out_dim x in_dim/4 uint8 indices].
 //
-// Design: the codebook is decoded once per workgroup into LDS as fp32 rows of
-// 16 bytes (one ds_read_b128 per index). A wave owns a tile of kRows rows and
-// sweeps the row in steps of 64 lanes x 4 indices; each lane keeps the 16
-// activations of its 4 indices in VGPRs and reuses them for all kRows rows, so
-// x is read once per tile. Partial sums are reduced across the wave at the end
-// of the tile. fp32 accumulation.
+// Two kernels:
+// - vq2_matvec_copies (index rows dword-aligned, in_dim % 16 == 0): 16 bank-
+//   interleaved fp32 copies of the codebook in LDS make every lookup
+//   conflict-free; tiles of 4 rows per wave, the next tile's index dwords in
+//   flight during the current tile's lookups, and a short halving reduction
+//   over the wave (see its comment).
+// - vq2_matvec_kernel (any other in_dim): one fp32 codebook copy in LDS, one
+//   byte load per index. A wave owns a tile of kRows rows and sweeps the row in
+//   steps of 64 lanes x 4 indices; each lane keeps the 16 activations of its 4
+//   indices in VGPRs and reuses them for all kRows rows.
+// Both accumulate in fp32.
 
 #include "tq_common.h"
 
@@ -26,9 +31,7 @@ __device__ inline float half_bits(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xFFFFu)));
 }
 
-// ALIGNED: the index rows start on 4-byte boundaries (in_dim % 16 == 0), so a
-// lane's 4 indices are one dword load; otherwise bytes are loaded one by one.
-template <bool ALIGNED>
+// Index rows at any byte alignment: one byte load per index.
 __global__ __launch_bounds__(256) void vq2_matvec_kernel(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                                          float *__restrict__ y, int M, int K) {
     __shared__ float4 cb[kVq2Entries];
@@ -65,15 +68,10 @@ __global__ __launch_bounds__(256) void vq2_matvec_kernel(const uint8_t *__restri
             }
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
-                unsigned q;
-                if (ALIGNED) {
-                    q = __builtin_amdgcn_raw_buffer_load_b32(rs, r * nb + b, 0, 0);
-                } else {
-                    q = 0;
+                unsigned q = 0;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (b + j < nb) q |= static_cast<unsigned>(__builtin_amdgcn_raw_buffer_load_b8(rs, r * nb + b + j, 0, 0)) << (8 * j);
-                }
+                for (int j = 0; j < 4; ++j)
+                    if (b + j < nb) q |= static_cast<unsigned>(__builtin_amdgcn_raw_buffer_load_b8(rs, r * nb + b + j, 0, 0)) << (8 * j);
                 float a = acc[r];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -96,6 +94,146 @@ __global__ __launch_bounds__(256) void vq2_matvec_kernel(const uint8_t *__restri
     }
 }
 
+// ---- Bank-conflict-free variant (index rows dword-aligned).
+// A lookup reads a random codebook entry per lane, so with one codebook copy
+// the lanes of an LDS pass collide on banks. Here LDS holds 16 interleaved
+// fp32 copies: copy c of entry e is float4 number 16 e + c, and lane l reads
+// copy l % 16. Entry rows are 256 bytes apart (a whole number of bank sweeps),
+// so a lane's banks are 4 (l % 16) .. +3 whatever entry it reads: the 16 lanes
+// served together never share a bank. 16 copies x 256 entries x 16 B = 64 KB.
+//
+// A wave owns tiles of R rows and covers a row chunk of 256 index bytes with
+// 64 lanes x 4 indices (one dword per lane per row). The next tile's index
+// dwords are loaded while the current tile is computed. The R per-lane sums
+// are reduced over the wave by halving exchanges (R - 1 + log2(64 / R)
+// shuffles instead of 6 R).
+constexpr int kCopies = 16;
+constexpr int kVq2Waves = 16;  // waves per workgroup (the 64 KB codebook is shared by all of them)
+constexpr int kVq2Rows = 4;    // rows per wave tile
+
+template <int R>
+__device__ inline void vq2_load_rows(const __amdgpu_buffer_rsrc_t &rs, int nb, int off, unsigned (&q)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) q[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, r * nb + off, 0, 0);
+}
+
+template <int R, bool ONE_CHUNK>
+__global__ __launch_bounds__(64 * kVq2Waves) void vq2_matvec_copies(const uint8_t *__restrict__ w,
+                                                                    const float *__restrict__ x,
+                                                                    float *__restrict__ y, int M, int K) {
+    __shared__ float4 cb[kVq2Entries * kCopies];
+    for (int i = threadIdx.x; i < kVq2Entries * kCopies; i += blockDim.x) {
+        const uint16_t *h = reinterpret_cast<const uint16_t *>(w) + kVq2Dim * (i / kCopies);
+        cb[i] = make_float4(half_bits(h[0]), half_bits(h[1]), half_bits(h[2]), half_bits(h[3]));
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const int nb = K / kVq2Dim;           // index bytes per row (a multiple of 4)
+    const int nchunk = ONE_CHUNK ? 1 : (nb + 255) / 256;  // 256-byte chunks of a row (ONE_CHUNK: nb <= 256)
+    const uint8_t *idx = w + kVq2CodebookBytes;
+    const int tiles = (M + R - 1) / R;
+    const int gw = blockIdx.x * kVq2Waves + wave;
+    const int nw = gridDim.x * kVq2Waves;
+    const int ntile = gw < tiles ? (tiles - 1 - gw) / nw + 1 : 0;  // this wave's tiles
+    const int nstep = ntile * nchunk;                                // (tile, chunk) steps
+    const float4 *cbl = cb + (lane & (kCopies - 1));  // this lane's copy: entry e at cbl[16 e]
+
+    // indices of step s: tile gw + (s / nchunk) nw, chunk s % nchunk; this
+    // lane's dword is bytes 256 chunk + 4 lane .. +3 of each of the R rows.
+    // Steps past the last and bytes past the row end read 0.
+    auto load_step = [&](int s, unsigned (&q)[R]) {
+        const int t = s / nchunk, ch = s - t * nchunk;
+        const int tile = gw + t * nw;
+        const int row0 = tile * R;
+        const size_t rem = s < nstep ? static_cast<size_t>(M - row0) * nb : 0;
+        const int nrec = rem > 0xFFFFFFFFull ? -1 : static_cast<int>(static_cast<unsigned>(rem));
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(idx) + static_cast<size_t>(s < nstep ? row0 : 0) * nb, static_cast<short>(0), nrec,
+            kBufferFlags);
+        const int b = 256 * ch + 4 * lane;
+        const int off = b < nb ? b : 0x40000000;
+#pragma unroll
+        for (int r = 0; r < R; ++r) q[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, r * nb + off, 0, 0);
+    };
+    // activations of this lane's 4 indices of a chunk (0 past the row end)
+    auto xvals = [&](int ch, float4 (&xv)[4]) {
+        const int b = 256 * ch + 4 * lane;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float *xp = x + 4 * (b + j);
+            xv[j] = (b + j < nb) ? make_float4(xp[0], xp[1], xp[2], xp[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+
+    float4 xv[4];
+    xvals(0, xv);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    // one step: lookups of q, and at a tile's last chunk the reduction and store
+    auto step = [&](int s, const unsigned (&q)[R]) {
+        const int t = s / nchunk, ch = s - t * nchunk;
+        if constexpr (!ONE_CHUNK) xvals(ch, xv);  // (with one chunk, loaded once before the loop)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float a = acc[r];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 c = cbl[kCopies * ((q[r] >> (8 * j)) & 0xFFu)];
+                a = fmaf(c.x, xv[j].x, a);
+                a = fmaf(c.y, xv[j].y, a);
+                a = fmaf(c.z, xv[j].z, a);
+                a = fmaf(c.w, xv[j].w, a);
+            }
+            acc[r] = a;
+        }
+        if (ch + 1 < nchunk) return;
+        // halving exchanges: after the exchange over lane bit `bit`, half the
+        // rows remain, each summed over both lanes of the pair
+        float v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = acc[r];
+        constexpr int kSteps = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;  // log2 R
+        int row = 0;
+#pragma unroll
+        for (int st = 0; st < kSteps; ++st) {  // (unrolled: every index below is a constant)
+            const int h = (R >> st) / 2, bit = 32 >> st;
+            const bool upper = (lane & bit) != 0;
+#pragma unroll
+            for (int r = 0; r < h; ++r) {
+                // both halves summed over the pair, then the lane keeps its
+                // half (a select of two sums: a select of two array elements
+                // is compiled as a run-time index into the array)
+                const float lo = v[r] + __shfl_xor(v[r], bit);
+                const float hi = v[r + h] + __shfl_xor(v[r + h], bit);
+                v[r] = upper ? hi : lo;
+            }
+            row += upper ? h : 0;
+        }
+        float sum = v[0];
+#pragma unroll
+        for (int bit = 32 / R; bit > 0; bit /= 2) sum += __shfl_xor(sum, bit);
+        const int r0 = (gw + t * nw) * R;
+        if ((lane & (64 / R - 1)) == 0 && r0 + row < M) y[r0 + row] = sum;
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    };
+
+    // two register sets, alternating: the next step's indices are in flight
+    // during every step's lookups
+    unsigned qa[R], qb[R];
+    load_step(0, qa);
+    for (int s = 0; s < nstep; s += 2) {
+        load_step(s + 1, qb);
+        step(s, qa);
+        if (s + 1 >= nstep) break;
+        load_step(s + 2, qa);
+        step(s + 1, qb);
+    }
+}
+
 int device_cus_vq2() {
     static int cus = 0;
     if (cus == 0) {
@@ -111,15 +249,22 @@ int device_cus_vq2() {
 
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream) {
     if (out_dim < 1 || in_dim < kVq2Dim || in_dim % kVq2Dim) return kBadShape;
+    const int cus = device_cus_vq2();
+    if ((in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0) {
+        // index rows dword-aligned: the conflict-free kernel (16 waves x 4-row
+        // tiles measured fastest at 3072..16384 rows, within 4% of the best at
+        // 151936 rows)
+        const bool one = in_dim <= 1024;  // one 256-byte chunk of indices per row
+        const int tiles = (out_dim + kVq2Rows - 1) / kVq2Rows;
+        const int g = std::max(1, std::min((tiles + kVq2Waves - 1) / kVq2Waves, 2 * cus));
+        auto kernel = one ? vq2_matvec_copies<kVq2Rows, true> : vq2_matvec_copies<kVq2Rows, false>;
+        hipLaunchKernelGGL(kernel, dim3(g), dim3(64 * kVq2Waves), 0, stream, w, x, y, out_dim, in_dim);
+        return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+    }
     const int tiles = (out_dim + kRows - 1) / kRows;
-    const int grid = std::max(1, std::min((tiles + kWavesPerBlock - 1) / kWavesPerBlock, device_cus_vq2() * 8));
-    const bool aligned = (in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0;
-    if (aligned)
-        hipLaunchKernelGGL(vq2_matvec_kernel<true>, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream, w, x, y,
-                           out_dim, in_dim);
-    else
-        hipLaunchKernelGGL(vq2_matvec_kernel<false>, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream, w, x, y,
-                           out_dim, in_dim);
+    const int grid = std::max(1, std::min((tiles + kWavesPerBlock - 1) / kWavesPerBlock, cus * 8));
+    hipLaunchKernelGGL(vq2_matvec_kernel, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream, w, x, y, out_dim,
+                       in_dim);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
