@@ -378,12 +378,16 @@ int launch_tiles(const uint8_t *w, const _Float16 *xh, const float *xinv, float 
     constexpr int stage = kWStage1 * WM + BN * 128;
     const int S = std::max(2, std::min(4, (80 * 1024) / stage));  // ring depth within 80 KB of LDS
     const size_t lds = static_cast<size_t>(S) * stage;
-    static bool raised = false;
-    if (lds > 64 * 1024 && !raised) {
-        TQ_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(i4_matmul_mfma<WM, WN, GT>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        raised = true;
+    static size_t limit = 0;  // dynamic LDS the kernel may take (0: not raised from the default 64 KB yet)
+    if (lds > 64 * 1024 && limit == 0) {
+        // what the CU's 160 KB leaves beside the kernel's static LDS
+        hipFuncAttributes attr{};
+        const void *fn = reinterpret_cast<const void *>(i4_matmul_mfma<WM, WN, GT>);
+        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
+        limit = 160 * 1024 - attr.sharedSizeBytes;
+        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(limit)));
     }
+    if (lds > 64 * 1024 && lds > limit) return kTooLarge;
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
     hipLaunchKernelGGL((i4_matmul_mfma<WM, WN, GT>), grid, dim3(kThreads), lds, stream, w, xh, xinv, y, M, N, K, Kp, G,
                        rb, S);
