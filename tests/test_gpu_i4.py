@@ -48,9 +48,10 @@ SHAPES = [
     (4864, 896, 64), (896, 4864, 64), (300, 2560, 64), (2560, 9728, 64), (333, 200, 64),
     (257, 1024, 128), (100, 520, 40), (64, 4096, 256), (50, 100, 32), (7, 70, 6), (41, 1000, 48),
     # register-path kernel over many tiles per workgroup (one, two and three
-    # windows per wave, run-time group size) and the DMA ring (three windows,
-    # more tiles than two per workgroup slot)
+    # windows per wave, run-time group size); the wave-private DMA ring (three
+    # windows: one and two workgroups per CU, rows of more than 24 windows)
     (151936, 896, 64), (16384, 1536, 64), (20000, 2560, 64), (40000, 520, 40), (60000, 2560, 64),
+    (20000, 4096, 64),
 ]
 
 

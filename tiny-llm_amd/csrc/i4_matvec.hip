@@ -1074,6 +1074,147 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
     wait_vmem(0);  // the loads issued past the last tile have returned before the wave ends
 }
 
+// Wave-private DMA ring: no workgroup barrier per tile. Each wave moves only
+// the bytes its own windows read: of every row of a 16-row tile, the segment
+// from the first group header its windows need to the end of its last window
+// (nc 16-byte chunks per row, 16 * nc chunks = at most PD DMAs of 64 lanes;
+// element e of the tile segment lands at 16 e of the wave's ring slot). The
+// wave's ring holds D tiles; it waits only for its own transfers. Row sums
+// of every tile go to LDS per (tile, row, wave) and are added in fixed wave
+// order after the loop, so waves never wait for each other inside it.
+template <int GT, int CPW, int PD, int NWMAX>
+__global__ __launch_bounds__(64 * NWMAX, 2) void i4_matvec_seg(const uint8_t *__restrict__ w,
+                                                             const float *__restrict__ x, float *__restrict__ y,
+                                                             Geom gm) {
+    (void)w;
+    (void)y;  // (w, y, gm.M: see the tile map)
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int NW = gm.NW;
+    const int rb = gm.row_bytes;
+    const int G = GT ? GT : gm.G;
+    const int Kp = gm.Gr * G;
+    const int NWP = (NW + 3) & ~3;
+    const int D = gm.depth;
+    const int tiles = gm.tile_end[gm.nmat - 1];
+    const int wg = blockIdx.x, nwg = gridDim.x;
+    const int ntile = wg < tiles ? (tiles - 1 - wg) / nwg + 1 : 0;
+
+    // LDS: [NW waves][D slots][PD KB] rings, then the activation set-up, which
+    // the per-tile sums [ntile][16][NWP] overlay once the operands are built
+    unsigned char *ring = smem + static_cast<size_t>(wave) * D * (PD * kPiece);
+    unsigned char *shared_area = smem + static_cast<size_t>(NW) * D * (PD * kPiece);
+    float *part = reinterpret_cast<float *>(shared_area);
+    XPlanes xp;
+    xp.pl = reinterpret_cast<int8_t *>(shared_area);
+    xp.stride = Kp;
+    xp.pre = reinterpret_cast<int *>(xp.pl + 3 * Kp);
+    xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
+    xp.gbase = 0;
+    xp.ngroups = gm.Gr;
+    XFirst xf;
+    load_x_first<GT>(xf, x, gm.K, Kp);
+
+    const int t0 = (gm.T * wave) / NW;
+    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
+    int HO[CPW];
+    unsigned HM[CPW];
+    header_slots<GT, CPW>(gm, t0, nch, HO, HM);
+    // this wave's segment of a row: [sb, sb + 16 nc), sb 16-aligned, covering
+    // its windows and the headers they use (masked headers read offset 0 and
+    // are never used)
+    int lo = kChunk * t0;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+        if (HM[c]) lo = min(lo, HO[c]);
+    const int sb = __builtin_amdgcn_readfirstlane(lo & ~15);
+    const int nc = __builtin_amdgcn_readfirstlane((kChunk * (t0 + nch) - sb + 15) / 16);  // <= 64 PD / 16 on the host
+    const TileMap map(gm);
+
+    // DMA sources of this lane: element e = 64 i + lane of the tile segment,
+    // row e / nc, chunk e % nc (elements past 16 nc repeat the last one; they
+    // land in the slot's unused tail)
+    int poff[PD], pdst[PD];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) {
+        const int e = min(64 * i + lane, 16 * nc - 1);
+        const int row = e / nc, ch = e - row * nc;
+        poff[i] = row * rb + sb + 16 * ch;
+        pdst[i] = kPiece * i;
+    }
+    auto dma = [&](int k, unsigned char *dst) {  // the wave's segment of its k-th tile (no rows past the last tile)
+        const bool live = k < ntile;
+        const TileRef r = map.at(live ? wg + k * nwg : 0);
+        dma_tile(r.w, live ? r.M : 0, rb, r.tile, dst, poff, pdst, PD);
+    };
+    // the first two tiles go out before the activation set-up (a fixed count,
+    // so the compiler's wait for the activation loads stays exact), the rest
+    // of the ring after it
+    dma(0, ring);
+    dma(1, ring + PD * kPiece);
+    prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
+    for (int k = 2; k < D; ++k) dma(k, ring + k * (PD * kPiece));
+    lds_barrier();
+    v4i A0[CPW], A1[CPW];
+    float E[CPW], C[CPW];
+    int HO2[CPW];
+    unsigned HM2[CPW];
+    build_operands<GT, CPW, true>(xp, gm, t0, nch, A0, A1, E, C, HO2, HM2);
+    lds_barrier();  // every wave is done with the set-up: the sums may overlay it
+    for (int i = threadIdx.x; i < ntile * kTile * NWP; i += blockDim.x) lds_write_u32(part + i, 0u);  // padding stays 0
+    lds_barrier();
+
+    const int bn = lane & 15, kq = lane >> 4;
+    int RO[CPW], RH[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+        const int t = t0 + min(c, nch - 1);
+        RO[c] = 16 * (bn * nc) + kChunk * t + 16 * kq - sb;
+        RH[c] = 16 * (bn * nc) + (HM[c] ? HO[c] - sb : 0);
+    }
+    int issued = D;  // tiles whose DMAs are out (past ntile: zero-length)
+    int b = 0;
+    for (int k = 0; k < ntile; ++k) {
+        wait_vmem((issued - k - 1) * PD);  // this wave's transfers of tile k have landed
+        const unsigned char *buf = ring + b * (PD * kPiece);
+        float a = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPW; ++c) {
+            const v4i d = *reinterpret_cast<const v4i *>(buf + RO[c]);
+            const unsigned h = *reinterpret_cast<const unsigned *>(buf + RH[c]) & HM[c];
+            a = window_step(a, d, h, A0[c], A1[c], E[c], C[c]);
+        }
+        // the slot's reads are complete (their values are used above): refill it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (issued < ntile) {
+            dma(issued, ring + b * (PD * kPiece));
+            ++issued;
+        }
+        a += __shfl_xor(a, 16);  // the four group slots of each row
+        a += __shfl_xor(a, 32);
+        if (lane < kTile) lds_write_u32(part + (k * kTile + lane) * NWP + wave, __builtin_bit_cast(unsigned, a));
+        b = b == D - 1 ? 0 : b + 1;
+    }
+    wait_vmem(0);  // no transfer may still be writing this workgroup's LDS
+    __syncthreads();
+    for (int i = threadIdx.x; i < ntile * kTile; i += blockDim.x) {
+        const int k = i / kTile, row_in = i - k * kTile;
+        const float *pr = part + i * NWP;
+        float sum = 0.f;
+        for (int q = 0; q < NWP / 4; ++q) {  // fixed order; padding slots hold 0
+            const float4 v = lds_read_f4(pr + 4 * q);
+            sum += v.x;
+            sum += v.y;
+            sum += v.z;
+            sum += v.w;
+        }
+        const TileRef r = map.at(wg + k * nwg);
+        const int row = r.tile * kTile + row_in;
+        if (row < r.M) store_y(r.y + row, sum);
+    }
+}
+
 // Split-K variant for long rows and few tiles (down projections): the windows
 // of every tile are split into S parts, one workgroup per (tile, part). A
 // workgroup converts only the activations of its part's groups, DMAs only the
@@ -1370,6 +1511,32 @@ int launch_pipe(const uint8_t *w, const float *x, float *y, const Geom &gm, hipS
                                  stream, limit);
 }
 
+// Wave-private ring for three windows per wave. Measured against the
+// workgroup ring (i4_matvec_dma): faster for rows of more than 24 windows and
+// for fewer than 32 tiles per CU (-7% to -17%); as fast or slower at 37 tiles
+// per CU with 23 windows (the 151936x2560 lm_head), and slower for two windows
+// per wave. One workgroup per CU with a three-tile ring up to 8 tiles per CU,
+// else two with two-tile rings.
+template <int GT, int CPW, int NWMAX>
+int launch_seg(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
+    constexpr int PD = 4;  // DMAs per wave per tile: a row segment of at most 64 B of header lead-in + 3 windows
+    static_assert(kChunk * CPW + 48 <= 16 * PD * 4, "segment fits the slot");
+    const int tiles = gm.tile_end[gm.nmat - 1];
+    const int NWP = (gm.NW + 3) & ~3;
+    const int cus = device_cus();
+    const int wgs = tiles <= 8 * cus ? 1 : 2, depth = wgs == 1 ? 3 : 2;
+    const int grid = std::max(1, std::min(tiles, cus * wgs));
+    const int per_wg = (tiles + grid - 1) / grid;
+    const size_t rings = static_cast<size_t>(gm.NW) * depth * PD * kPiece;
+    const size_t shared_area = std::max(xplanes_bytes(gm), static_cast<size_t>(per_wg) * kTile * NWP * 4);
+    const size_t lds = rings + shared_area + 16;
+    if (lds > kLdsBytes) return kTooLarge;
+    Geom g2 = gm;
+    g2.depth = depth;
+    static size_t limit = 0;
+    return launch_with_lds(i4_matvec_seg<GT, CPW, PD, NWMAX>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, limit);
+}
+
 template <int GT, int CPW, int PW, int NWMAX>
 int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
     static size_t limit = 0;
@@ -1394,6 +1561,12 @@ int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
         while (wgs2 > 1 && static_cast<size_t>(wgs2) * lds2 > kLdsBytes) --wgs2;
         const int slots = device_cus() * wgs2;
         if (CPW == 1 || tiles <= 2 * slots) return launch_pipe<GT, CPW, NWMAX>(w, x, y, gm, stream);
+    }
+    if constexpr (CPW == 3) {
+        if (gm.T > 24 || tiles < 32 * device_cus()) {
+            const int st = launch_seg<GT, CPW, NWMAX>(w, x, y, gm, stream);
+            if (st != kTooLarge) return st;
+        }
     }
     while (wgs > 1 && static_cast<size_t>(wgs) * (3 * tbuf + fixed) > kLdsBytes) --wgs;
     if (3 * tbuf + fixed > kLdsBytes) return kTooLarge;
