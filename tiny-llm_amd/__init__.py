@@ -88,6 +88,9 @@ _SIGS = {
     "tqhip_event_elapsed_ms": (_i, [_vp, _vp, _f32p]),
     "tqhip_run_ops": (_i, [ctypes.POINTER(Op), _i, _i, _vp]),
     "tqhip_run_ops_timed": (_i, [ctypes.POINTER(Op), _i, _i, _vp, _f32p]),
+    "tqhip_ops_graph_create": (_i, [ctypes.POINTER(Op), _i, _vp, ctypes.POINTER(_vp)]),
+    "tqhip_ops_graph_launch": (_i, [_vp, _vp]),
+    "tqhip_ops_graph_destroy": (_i, [_vp]),
     # synthetic inputs
     "tq_synth_seed": (ctypes.c_uint64, [ctypes.c_uint64, _i, ctypes.c_char_p]),
     "tq_synth_i4": (None, [_vp, _i, _i, _i, ctypes.c_uint64, ctypes.c_float, ctypes.c_float,
@@ -381,6 +384,33 @@ class Event:
 def run_ops(ops: list, repeats: int, stream: "Stream | None" = None) -> None:
     arr = (Op * len(ops))(*ops)
     _check(lib().tqhip_run_ops(arr, len(ops), repeats, _stream(stream)), "tqhip_run_ops")
+
+
+class OpsGraph:
+    """An op list captured into a HIP graph (tqhip_ops_graph_create) on a created
+    stream, replayed with launch() on that stream."""
+
+    def __init__(self, ops: list, stream: "Stream"):
+        self._arr = (Op * len(ops))(*ops)
+        self._stream = stream
+        h = _vp()
+        _check(lib().tqhip_ops_graph_create(self._arr, len(ops), _stream(stream), ctypes.byref(h)),
+               "tqhip_ops_graph_create")
+        self._h = h
+
+    def launch(self) -> None:
+        _check(lib().tqhip_ops_graph_launch(self._h, _stream(self._stream)), "tqhip_ops_graph_launch")
+
+    def close(self) -> None:
+        if self._h:
+            _check(lib().tqhip_ops_graph_destroy(self._h), "tqhip_ops_graph_destroy")
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def run_ops_timed(ops: list, repeats: int, stream: "Stream | None" = None) -> np.ndarray:

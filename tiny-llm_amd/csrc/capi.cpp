@@ -380,6 +380,60 @@ int tqhip_run_ops_timed(const tqhip_op *ops, int n_ops, int repeats, void *strea
     return st;
 }
 
+// An op list captured once into a HIP graph and replayed: a device-resident
+// decode loop issues the same calls every token with the same buffers, and a
+// replay costs the GPU about 1.6 us per kernel instead of about 2.8 us for
+// separate launches (measured on MI355X).
+struct tqhip_ops_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int tqhip_ops_graph_create(const tqhip_op *ops, int n_ops, void *stream, void **graph_out) {
+    if (!graph_out || n_ops < 1 || !stream) return kBadShape;  // (the null stream cannot be captured)
+    *graph_out = nullptr;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // One eager pass first: it allocates the per-stream scratch and sets kernel
+    // attributes, neither of which may happen inside a capture.
+    int st = tqhip_run_ops(ops, n_ops, 1, stream);
+    if (st != kOk) return st;
+    if (hipStreamSynchronize(s) != hipSuccess) return kLaunchFailed;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return kLaunchFailed;
+    for (int i = 0; i < n_ops && st == kOk; ++i) st = launch_op(ops[i], s);
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(s, &g);
+    if (st != kOk || end != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return st != kOk ? st : kLaunchFailed;
+    }
+    hipGraphExec_t exec = nullptr;
+    if (hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return kLaunchFailed;
+    }
+    auto *h = new tqhip_ops_graph;
+    h->graph = g;
+    h->exec = exec;
+    *graph_out = h;
+    return kOk;
+}
+
+int tqhip_ops_graph_launch(void *graph, void *stream) {
+    if (!graph || !stream) return kBadShape;
+    auto *h = static_cast<tqhip_ops_graph *>(graph);
+    return hipGraphLaunch(h->exec, static_cast<hipStream_t>(stream)) == hipSuccess ? kOk : kLaunchFailed;
+}
+
+int tqhip_ops_graph_destroy(void *graph) {
+    if (!graph) return kOk;
+    auto *h = static_cast<tqhip_ops_graph *>(graph);
+    int st = kOk;
+    if (h->exec && hipGraphExecDestroy(h->exec) != hipSuccess) st = kLaunchFailed;
+    if (h->graph && hipGraphDestroy(h->graph) != hipSuccess) st = kLaunchFailed;
+    delete h;
+    return st;
+}
+
 }  // extern "C"
 
 // Self-registration as the "hip" variants (kernels/dispatch.h:459-474 idiom).
