@@ -7,17 +7,22 @@ seeded weights, each q 896x896, k 128x896, v 128x896, o 896x896, gate 4864x896,
 up 4864x896, down 896x4864, plus lm_head 151936x896 -- issued the way the
 reference runtime calls them (qwen_forward_token: mv_qkv, mv o, mv_pair
 gate/up, mv down; lm_head matvec_i4): 97 launches on one stream, inputs
-resident in HBM.
+resident in HBM, issued eagerly (one host call per launch, as the reference
+runtime issues them). The same 97 launches captured once into a HIP graph and
+replayed are reported under "graph" (--no-graph skips that part).
 
 Printed (one JSON line on stdout):
   value        algorithmic GB/s of the whole step; bytes per matvec are the
                reference's own definition weight_bytes + 4*(M+K)
                (benchmarks/bench_kernels.cpp:487): 280,664,064 B per step
   us_per_layer_set  time of one layer's 7 matvecs (the 24-layer part / 24)
+  graph        the same step captured into one HIP graph (tqhip_ops_graph_create)
+               and replayed --steps times: ms, GB/s, layer set
   roofline     the kernel with the largest share of the step's time (the
-               staged i4 MFMA matvec, every in_dim=896 launch): algorithmic
-               bytes of its launches / their time, those launches timed back
-               to back in step order with HIP events on the launch stream,
+               register-path i4 MFMA matvec, every in_dim=896 launch):
+               algorithmic bytes of its launches / their time, those launches
+               timed back to back in step order with HIP events on the launch
+               stream,
                against 8 TB/s. traffic = HBM bytes per launch from the committed
                rocprofv3 FETCH_SIZE/WRITE_SIZE summary, when present
   headline     BASELINE configs[2] lm_head 151936x2560 alone, rotated over
@@ -147,6 +152,30 @@ def time_ops(tq, ops, reps, warmup, stream, batches=1):
     return float(np.median(out))
 
 
+def time_graph(tq, ops, reps, warmup, stream, batches=1):
+    """ms per pass over `ops` captured once into a HIP graph (tq.OpsGraph) and
+    replayed: HIP events around `reps` back-to-back replays on `stream`; with
+    batches > 1, the median over that many such measurements. Every kernel of
+    the list runs in every replay; the graph only removes the per-launch host
+    and dispatch cost."""
+    graph = tq.OpsGraph(ops, stream)
+    try:
+        for _ in range(warmup):
+            graph.launch()
+        stream.synchronize()
+        out = []
+        for _ in range(batches):
+            e0, e1 = tq.Event(), tq.Event()
+            e0.record(stream)
+            for _ in range(reps):
+                graph.launch()
+            e1.record(stream)
+            out.append(e0.elapsed_ms(e1) / reps)
+        return float(np.median(out))
+    finally:
+        graph.close()
+
+
 def headline(tq, stream, reps=20):
     """configs[2] lm_head 151936x2560, 3 rotated copies (657 MB): median of 7
     batches of 20 rotations (60 launches each)."""
@@ -173,8 +202,8 @@ def roofline(tq, work, stream, reps):
     register-path MFMA matvec with 8 windows per row, one per wave
     (i4_matvec_pipe<64,1,8,2,true> for the fused qkv and gate/up launches,
     i4_matvec_pipe<64,1,8,2,false> for o and lm_head). Timed back to back in
-    step order with events at both ends; back-to-back launches leave no gaps,
-    so the mean per launch is the kernels' mean duration."""
+    step order with events at both ends, so the mean per launch is the
+    kernels' mean duration plus the inter-kernel dispatch gap."""
     dom = [i for i, k in enumerate(work.op_in_dim) if k == HIDDEN]
     ops = [work.ops[i] for i in dom]
     ms = time_ops(tq, ops, reps, 2, stream, batches=5)
@@ -322,6 +351,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill dequant-GEMM timings")
     ap.add_argument("--no-host-call", action="store_true", help="skip the host-pointer (PCIe-inclusive) timing")
     ap.add_argument("--no-vq2", action="store_true", help="skip the VQ2 matvec timings")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first run one device-to-device copy of MB MiB (a known-size kernel for counter runs)")
     args = ap.parse_args()
@@ -355,9 +385,15 @@ def main():
     log(f"[bench] step: {ms_step * 1e3:.1f} us, {value:.1f} GB/s")
     # the 24 layers alone
     layer_ops = work.ops[:-1]
-    ms_layers = time_ops(tq, layer_ops, args.steps, 2, stream)
-    us_layer = ms_layers * 1e3 / N_LAYERS
+    us_layer = time_ops(tq, layer_ops, args.steps, 2, stream) * 1e3 / N_LAYERS
     log(f"[bench] layer set: {us_layer:.2f} us per layer ({len(layer_ops) // N_LAYERS} launches)")
+    graph = None
+    if not args.no_graph:  # the same step captured into one HIP graph and replayed --steps times
+        ms_graph = time_graph(tq, work.ops, args.steps, args.warmup, stream)
+        graph = {"ms_per_step": round(ms_graph, 4), "value": round(work.bytes / (ms_graph * 1e-3) / 1e9, 1),
+                 "us_per_layer_set": round(time_graph(tq, layer_ops, args.steps, 2, stream) * 1e3 / N_LAYERS, 2)}
+        log(f"[bench] step as a HIP graph replay: {graph['ms_per_step'] * 1e3:.1f} us, {graph['value']} GB/s, "
+            f"layer set {graph['us_per_layer_set']} us")
     roof = roofline(tq, work, stream, args.steps)
     log(f"[bench] dominant kernel: {roof['launches']} launches/step, {roof['avg_launch_us']} us avg, "
         f"{roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of 8 TB/s)")
@@ -392,6 +428,7 @@ def main():
         "data": "synthetic (BASELINE distributions, seeded)",
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "us_per_layer_set": round(us_layer, 2),
+        "graph": graph,
         "config": {"workload": "BASELINE configs[1]: Qwen2.5-0.5B-shaped i4 HQQ@64 decode matvec set, batch=1, "
                                "24 layers x (qkv 896/128/128x896, o 896x896, gate/up pair 4864x896, "
                                "down 896x4864) + lm_head 151936x896, independent seeded weights",

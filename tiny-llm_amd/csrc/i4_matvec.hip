@@ -47,6 +47,7 @@ constexpr int kTile = 16;      // weight rows per MFMA tile
 constexpr int kPiece = 1024;   // bytes one wave streams per 16-byte-per-lane load
 constexpr unsigned kNibbles = 0x0F0F0F0Fu;
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family word 3)
+constexpr int kCachePolicyStream = 2;     // buffer-load cache-policy bits: nt (non-temporal)
 #ifndef TQ_LDS_DEPTH
 #define TQ_LDS_DEPTH 1  // tiles in flight per workgroup beyond the one in LDS
 #endif
@@ -86,6 +87,24 @@ __device__ inline float half_bits(uint32_t h) {
 __device__ inline float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
+}
+
+// a[l] + a[l^16], then + the same of lane l^32: the four 16-lane rows of the
+// wave summed in every lane, in the order of two xor-shuffle steps (16, then
+// 32). gfx950's row swaps move the values in registers, where a shuffle is an
+// LDS permute round trip. v_permlane16_swap(d, s) exchanges the odd rows of d
+// with the even rows of s, so with d = s = a the two results hold rows
+// (0,0,2,2) and (1,1,3,3) and their sum is a[l] + a[l^16] in every lane (fp
+// addition commutes); v_permlane32_swap does the same for the wave halves.
+__device__ __forceinline__ float sum_rows4(float a) {
+    const unsigned u = __builtin_bit_cast(unsigned, a);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float b = __builtin_bit_cast(float, static_cast<unsigned>(p[0])) +
+                    __builtin_bit_cast(float, static_cast<unsigned>(p[1]));
+    const unsigned v = __builtin_bit_cast(unsigned, b);
+    const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __builtin_bit_cast(float, static_cast<unsigned>(q[0])) +
+           __builtin_bit_cast(float, static_cast<unsigned>(q[1]));
 }
 
 __device__ inline float wave_sum(float v) {
@@ -727,8 +746,7 @@ __global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_lds(con
             const unsigned h = *reinterpret_cast<const unsigned *>(buf + RH[c]) & HM[c];
             a = window_step(a, d, h, A0[c], A1[c], E[c], C[c]);
         }
-        a += __shfl_xor(a, 16);  // the four group slots of each row
-        a += __shfl_xor(a, 32);
+        a = sum_rows4(a);  // the four group slots of each row
         float *pb = part + (i & 1) * (kTile * NWP);
         if (lane < kTile) pb[lane * NWP + wave] = a;
     };
@@ -802,6 +820,20 @@ __device__ __forceinline__ void dma_tile(const uint8_t *w, int M, int rb, int ti
                                                  poff[s], 0, 0, 0);
 }
 
+// dma_tile with the non-temporal hint: the DMA ring reads every tile once, in
+// 1 KB pieces of one contiguous 16-row block, so no line is read twice and the
+// caches need not keep any. Measured on the lm_head-sized stream: 8% faster
+// than the default policy. The kernels whose waves read parts of lines that
+// other waves also read (row segments, windows) lose with it.
+__device__ __forceinline__ void dma_tile_stream(const uint8_t *w, int M, int rb, int tile, unsigned char *dst,
+                                                const int *poff, const int *pdst, int pw) {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(w, M, rb, tile * kTile);
+#pragma unroll
+    for (int s = 0; s < pw; ++s)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(dst + pdst[s]), 16,
+                                                 poff[s], 0, 0, kCachePolicyStream);
+}
+
 // Workgroup barrier for LDS traffic that leaves weight DMAs in flight: waits
 // for this wave's own LDS operations only (a __syncthreads() here would also
 // wait for every pending global->LDS transfer). The empty asm statements keep
@@ -861,7 +893,7 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     }
     auto dma = [&](int i, unsigned char *dst) {
         const TileRef r = map.at(tile_of(i));
-        dma_tile(r.w, r.M, rb, r.tile, dst, poff, pdst, PW);
+        dma_tile_stream(r.w, r.M, rb, r.tile, dst, poff, pdst, PW);
     };
     // the first three tiles go out before the activation set-up (repeats of
     // the last tile when the workgroup has fewer; they are never read) ...
@@ -926,8 +958,7 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
             const unsigned h = *reinterpret_cast<const unsigned *>(buf + RH[c]) & HM[c];
             a = window_step(a, d, h, A0[c], A1[c], E[c], C[c]);
         }
-        a += __shfl_xor(a, 16);  // the four group slots of each row
-        a += __shfl_xor(a, 32);
+        a = sum_rows4(a);  // the four group slots of each row
         if (lane < kTile) lds_write_u32(part + (i & 1) * (kTile * NWP) + lane * NWP + wave, __builtin_bit_cast(unsigned, a));
         if (i > 0) reduce_prev(i - 1);
         b = b == D - 1 ? 0 : b + 1;
@@ -1049,8 +1080,7 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
             for (int c = 0; c < CPW; ++c) a = window_step(a, d[s][c], h[s][c] & HM[c], A0[c], A1[c], E[c], C[c]);
             load_d(k + P, d[s]);  // this slot's next tile
             load_h(k + P, h[s]);
-            a += __shfl_xor(a, 16);  // the four group slots of each row
-            a += __shfl_xor(a, 32);
+            a = sum_rows4(a);  // the four group slots of each row
             float *pb = part + (k & 1) * (kTile * NWP);
             if (lane < kTile) lds_write_u32(pb + lane * NWP + wave, __builtin_bit_cast(unsigned, a));
             // every wave's sums of tile k are in; the buffer written next (tile
@@ -1191,8 +1221,7 @@ __global__ __launch_bounds__(64 * NWMAX, 2) void i4_matvec_seg(const uint8_t *__
             dma(issued, ring + b * (PD * kPiece));
             ++issued;
         }
-        a += __shfl_xor(a, 16);  // the four group slots of each row
-        a += __shfl_xor(a, 32);
+        a = sum_rows4(a);  // the four group slots of each row
         if (lane < kTile) lds_write_u32(part + (k * kTile + lane) * NWP + wave, __builtin_bit_cast(unsigned, a));
         b = b == D - 1 ? 0 : b + 1;
     }
@@ -1296,8 +1325,7 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
         a = window_step(a, d, hraw[c] & HM[c], A0[c], A1[c], E[c], C[c]);
     }
     if (nch_raw <= 0) a = 0.f;  // a part one window short of the widest leaves a wave idle
-    a += __shfl_xor(a, 16);
-    a += __shfl_xor(a, 32);
+    a = sum_rows4(a);
     if (lane < kTile) part_sum[lane * NWP + wave] = a;
     __syncthreads();
     // 4. this part's 16 sums -> scratch; the last part of the tile adds them up
@@ -1398,8 +1426,7 @@ __global__ __launch_bounds__(1024, 4) void i4_matvec_reg(const uint8_t *__restri
         float a = 0.f;
 #pragma unroll
         for (int c = 0; c < CPW; ++c) a = window_step(a, d[c], h[c] & HM[c], A0[c], A1[c], E[c], C[c]);
-        a += __shfl_xor(a, 16);
-        a += __shfl_xor(a, 32);
+        a = sum_rows4(a);
         if (lane < kTile) part[lane * NWP + wave] = a;
         __syncthreads();
         if (threadIdx.x < kTile) {
