@@ -1244,17 +1244,38 @@ __global__ __launch_bounds__(64 * NWMAX, 2) void i4_matvec_seg(const uint8_t *__
     }
 }
 
+// One meeting of two partial sums of a row in a split-K tile: a 64-bit slot
+// that is 0 when empty and (1 << 32 | float bits) when it holds the first
+// arrival's value. Each side swaps its own value in; the side that gets a
+// full slot back arrives second, adds the two in fixed order (first + second
+// operand of the tree, whatever the arrival order) and empties the slot for
+// the next launch. The value travels inside the atomic itself, so no other
+// store has to be made visible first: one round trip to the device-coherent
+// level per meeting.
+__device__ inline bool meet_partial(unsigned long long *slot, bool second_operand, float &v) {
+    const unsigned long long mine = (1ull << 32) | __builtin_bit_cast(unsigned, v);
+    const unsigned long long old = __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old >> 32) == 0) return false;  // first arrival: the other side carries on
+    const float o = __builtin_bit_cast(float, static_cast<unsigned>(old));
+    v = second_operand ? o + v : v + o;
+    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 // Split-K variant for long rows and few tiles (down projections): the windows
-// of every tile are split into S parts, one workgroup per (tile, part). A
+// of every tile are split into S <= 4 parts, one workgroup per (tile, part). A
 // workgroup converts only the activations of its part's groups, DMAs only the
-// part's bytes of its 16 rows, reads the group headers straight from global
-// memory, and leaves 16 partial sums in a scratch buffer. The workgroup that
-// arrives last at the tile's counter adds the S partials in part order
-// (deterministic) and resets the counter to zero for the next launch.
+// part's bytes of its 16 rows and reads the group headers straight from
+// global memory. The S row sums meet in a binary tree of 64-bit exchange
+// slots (meet_partial): parts 2j and 2j+1 meet first, then the winners of
+// the two pairs (a part without a sibling goes straight up), so the sums are
+// added as (p0 + p1) + (p2 + p3) whatever the arrival order (deterministic),
+// and the last arrival stores the row. Slots: [tile][3][16], level-one pair
+// slots 0 and 1, level-two slot 2; every launch leaves them empty.
 template <int GT, int CPW, int PW, int NWMAX>
 __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec_split(
     const uint8_t *__restrict__ w, const float *__restrict__ x, float *__restrict__ y, Geom gm,
-    float *__restrict__ partial, unsigned *__restrict__ counter) {
+    unsigned long long *__restrict__ slots) {
     static_assert(GT == 64 || GT == 128, "one activation block per thread needs a compile-time group size");
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
@@ -1328,8 +1349,7 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     a = sum_rows4(a);
     if (lane < kTile) part_sum[lane * NWP + wave] = a;
     __syncthreads();
-    // 4. this part's 16 sums -> scratch; the last part of the tile adds them up
-    __shared__ unsigned last;
+    // 4. this part's 16 row sums climb the exchange tree; the last arrival stores
     if (threadIdx.x < kTile) {
         const float4 *pr = reinterpret_cast<const float4 *>(part_sum + threadIdx.x * NWP);
         float v = 0.f;
@@ -1340,34 +1360,13 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
             v += u.z;
             v += u.w;
         }
-        // Device-coherent store (sc1: through the XCD's L2, whose contents the
-        // other XCDs do not see), then wait until it is acknowledged. A
-        // device-scope fence would do the same for all memory by writing back
-        // and invalidating the whole L2 in every workgroup, which costs more
-        // than the matvec itself.
-        __hip_atomic_store(&partial[(static_cast<size_t>(tile) * S + part) * kTile + threadIdx.x], v, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the store has completed
-    }
-    __syncthreads();  // every partial of this workgroup has completed before the arrival is counted
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(&counter[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                       static_cast<unsigned>(S - 1)
-                   ? 1u
-                   : 0u;
-    __syncthreads();
-    if (last) {
-        asm volatile("" ::: "memory");
-        if (threadIdx.x < kTile) {
-            const int row = tile * kTile + threadIdx.x;
-            float v = 0.f;
-            for (int p = 0; p < S; ++p)
-                v += __hip_atomic_load(&partial[(static_cast<size_t>(tile) * S + p) * kTile + threadIdx.x],
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (row < M) y[row] = v;
-        }
-        if (threadIdx.x == 0) __hip_atomic_store(&counter[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned long long *ts = slots + static_cast<size_t>(tile) * (3 * kTile) + threadIdx.x;
+        bool alive = true;
+        if ((part ^ 1) < S) alive = meet_partial(ts + (part >> 1) * kTile, part & 1, v);
+        const int node = part >> 1, nodes = (S + 1) >> 1;
+        if (alive && (node ^ 1) < nodes) alive = meet_partial(ts + 2 * kTile, node & 1, v);
+        const int row = tile * kTile + threadIdx.x;
+        if (alive && row < M) store_y(y + row, v);
     }
 }
 
@@ -1628,35 +1627,29 @@ int launch_lds(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX, DEPTH>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, limit);
 }
 
-// Per-stream scratch of the split-K kernel: partial sums and per-tile arrival
-// counters. The counters start at zero and every launch leaves them at zero.
-// Launches on one stream are ordered; launches on different streams get
-// different buffers.
+// Per-stream scratch of the split-K kernel: the exchange slots of every tile,
+// empty (zero) between launches. Launches on one stream are ordered; launches
+// on different streams get different buffers.
 struct SplitScratch {
-    float *partial = nullptr;
-    unsigned *counter = nullptr;
-    size_t partial_cap = 0, counter_cap = 0;
+    unsigned long long *slots = nullptr;
+    size_t cap = 0;
 };
 std::mutex g_split_mu;
 std::unordered_map<hipStream_t, SplitScratch> g_split;
 
-int split_scratch(hipStream_t stream, size_t npartial, size_t ncounter, float **partial, unsigned **counter) {
+int split_scratch(hipStream_t stream, size_t nslots, unsigned long long **slots) {
     std::lock_guard<std::mutex> lock(g_split_mu);
     SplitScratch &sc = g_split[stream];
-    if (sc.partial_cap < npartial || sc.counter_cap < ncounter) {
-        if (hipStreamSynchronize(stream) != hipSuccess) return kLaunchFailed;  // earlier launches may still use them
-        if (sc.partial) (void)hipFree(sc.partial);
-        if (sc.counter) (void)hipFree(sc.counter);
+    if (sc.cap < nslots) {
+        if (hipStreamSynchronize(stream) != hipSuccess) return kLaunchFailed;  // earlier launches may still use it
+        if (sc.slots) (void)hipFree(sc.slots);
         sc = SplitScratch{};
-        const size_t np = std::max(npartial, static_cast<size_t>(1) << 16), nc = std::max(ncounter, static_cast<size_t>(4096));
-        if (hipMalloc(&sc.partial, np * sizeof(float)) != hipSuccess) return kLaunchFailed;
-        if (hipMalloc(&sc.counter, nc * sizeof(unsigned)) != hipSuccess) return kLaunchFailed;
-        if (hipMemset(sc.counter, 0, nc * sizeof(unsigned)) != hipSuccess) return kLaunchFailed;
-        sc.partial_cap = np;
-        sc.counter_cap = nc;
+        const size_t n = std::max(nslots, static_cast<size_t>(1) << 14);
+        if (hipMalloc(&sc.slots, n * sizeof(unsigned long long)) != hipSuccess) return kLaunchFailed;
+        if (hipMemset(sc.slots, 0, n * sizeof(unsigned long long)) != hipSuccess) return kLaunchFailed;
+        sc.cap = n;
     }
-    *partial = sc.partial;
-    *counter = sc.counter;
+    *slots = sc.slots;
     return kOk;
 }
 
@@ -1672,14 +1665,14 @@ int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int
     gm.ksplit = S;
     const size_t lds = gm.tbuf + static_cast<size_t>(kTile * NWP) * 4 + 3 * kp + kp / 8 * 4 + ng * 4 + 16;
     if (lds > kLdsBytes) return kTooLarge;
-    float *partial = nullptr;
-    unsigned *counter = nullptr;
-    const int st = split_scratch(stream, static_cast<size_t>(tiles) * S * kTile, tiles, &partial, &counter);
+    if (S < 2 || S > 4) return kTooLarge;  // the exchange tree has two levels
+    unsigned long long *slots = nullptr;
+    const int st = split_scratch(stream, static_cast<size_t>(tiles) * 3 * kTile, &slots);
     if (st != kOk) return st;
     const int fit = fit_dynamic_lds(reinterpret_cast<const void *>(i4_matvec_split<GT, CPW, PW, NWMAX>), lds, limit);
     if (fit != kOk) return fit;
     hipLaunchKernelGGL((i4_matvec_split<GT, CPW, PW, NWMAX>), dim3(tiles * S), dim3(64 * gm.NW), lds, stream, w, x, y,
-                       gm, partial, counter);
+                       gm, slots);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
