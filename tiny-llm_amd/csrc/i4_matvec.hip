@@ -991,6 +991,8 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
     const int Kp = gm.Gr * G;
     const int NWP = (NW + 3) & ~3;
     float *part = reinterpret_cast<float *>(smem);  // [2][16][NWP]
+    const int t0 = (gm.T * wave) / NW;
+    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
     XPlanes xp;
     xp.pl = reinterpret_cast<int8_t *>(part + 2 * kTile * NWP);
     xp.stride = Kp;
@@ -1004,8 +1006,6 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
     const int tiles = gm.tile_end[gm.nmat - 1];
     const int wg = blockIdx.x, nwg = gridDim.x;  // tile of round k: wg + k * nwg
     const int ntile = wg < tiles ? (tiles - 1 - wg) / nwg + 1 : 0;
-    const int t0 = (gm.T * wave) / NW;
-    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
     const int bn = lane & 15, kq = lane >> 4;
     int DO[CPW], HOr[CPW];
 #pragma unroll
@@ -1053,6 +1053,9 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
         if constexpr (CPW == 1) load_h(s, h[s]);
     }
 
+    // (A wave-local set-up -- each wave converting only the groups its
+    // windows touch, with no barrier -- measured slower here: eight waves
+    // fetching x instead of one workgroup.)
     prepare_x<GT, true>(xp, x, gm.K, gm.Gr, Kp, xf);
     lds_barrier();
     v4i A0[CPW], A1[CPW];
@@ -1064,8 +1067,6 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
 #pragma unroll
         for (int s = 0; s < P; ++s) load_h(s, h[s]);
     }
-    for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x) lds_write_u32(part + i, 0u);  // padding slots stay 0
-    lds_barrier();
 
     // Whole rounds of the P register slots: every slot is loaded and computed
     // the same way in every round (zero-length loads past the last tile),
@@ -1078,11 +1079,16 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
             float a = 0.f;
 #pragma unroll
             for (int c = 0; c < CPW; ++c) a = window_step(a, d[s][c], h[s][c] & HM[c], A0[c], A1[c], E[c], C[c]);
-            load_d(k + P, d[s]);  // this slot's next tile
-            load_h(k + P, h[s]);
+            if constexpr (P > 1) {  // (one tile per workgroup: nothing follows)
+                load_d(k + P, d[s]);  // this slot's next tile
+                load_h(k + P, h[s]);
+            }
             a = sum_rows4(a);  // the four group slots of each row
             float *pb = part + (k & 1) * (kTile * NWP);
-            if (lane < kTile) lds_write_u32(pb + lane * NWP + wave, __builtin_bit_cast(unsigned, a));
+            if (lane < kTile) {
+                lds_write_u32(pb + lane * NWP + wave, __builtin_bit_cast(unsigned, a));
+                for (int q = NW + wave; q < NWP; q += NW) lds_write_u32(pb + lane * NWP + q, 0u);  // padding slots
+            }
             // every wave's sums of tile k are in; the buffer written next (tile
             // k + 1) was read before this barrier
             lds_barrier();
@@ -1101,7 +1107,7 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
             }
         }
     }
-    wait_vmem(0);  // the loads issued past the last tile have returned before the wave ends
+    if constexpr (P > 1) wait_vmem(0);  // the loads issued past the last tile have returned before the wave ends
 }
 
 // Wave-private DMA ring: no workgroup barrier per tile. Each wave moves only
