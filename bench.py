@@ -27,6 +27,8 @@ Printed (one JSON line on stdout):
                rocprofv3 FETCH_SIZE/WRITE_SIZE summary, when present
   headline     BASELINE configs[2] lm_head 151936x2560 alone, rotated over
                3 copies (657 MB > 2x the 256 MB MALL) so reads come from HBM
+  configs2     BASELINE configs[2] gate/up 9728x2560, down 2560x9728, attention
+               4096x2560 and 2560x4096, each rotated over > 512 MB of copies
   prefill      BASELINE configs[4] dequant-GEMM 9728x2560 at 32/128/512
                tokens: us, TFLOP/s and fraction of the dense fp16 MFMA peak
   vq2          BASELINE configs[3] VQ2 matvec 3072x1024 and VQ2 151936x896,
@@ -177,20 +179,29 @@ def time_graph(tq, ops, reps, warmup, stream, batches=1):
 
 
 def headline(tq, stream, reps=20):
-    """configs[2] lm_head 151936x2560, 3 rotated copies (657 MB): median of 7
-    batches of 20 rotations (60 launches each)."""
+    """configs[2] lm_head 151936x2560, 3 rotated copies (657 MB): median of 15
+    batches of 20 rotations (60 launches each). Batch medians drift by up to
+    15% over a run on the same box (kernel traces show stretches of slower
+    launches that recover), so many batches are taken; the fastest and
+    slowest batch are reported beside the median."""
     M, K = VOCAB, 2560
     w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -1, "lm_head_2560"))
     x = tq.synth_normal(K, seed=tq.synth_seed(0, -1, "x_2560"))
     copies = [tq.DeviceBuffer.from_array(w) for _ in range(3)]
     dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
     ops = [tq.Op(tq.OP_I4_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, G) for c in copies]
-    ms = time_ops(tq, ops, reps, 5, stream, batches=7) / len(ops)
+    tq.run_ops(ops, 5, stream)
+    stream.synchronize()
+    per = []
+    for _ in range(15):
+        per.append(time_ops(tq, ops, reps, 0, stream) / len(ops))
+    ms = float(np.median(per))
     gbs = algo_bytes(M, K) / (ms * 1e-3) / 1e9
     for c in copies:
         c.free()
     return {"shape": "151936x2560 G64 (BASELINE configs[2] lm_head)", "us": round(ms * 1e3, 2),
             "gbs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4), "bytes": algo_bytes(M, K),
+            "us_batch_min": round(min(per) * 1e3, 2), "us_batch_max": round(max(per) * 1e3, 2),
             "rotation": "3 copies, 657 MB"}
 
 
@@ -200,8 +211,9 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "i4_matvec_pipe_decode_step_traffi
 def roofline(tq, work, stream, reps):
     """The in_dim=896 launches (qkv, o, gate/up pair, lm_head) all run the
     register-path MFMA matvec with 8 windows per row, one per wave
-    (i4_matvec_pipe<64,1,8,2,true> for the fused qkv and gate/up launches,
-    i4_matvec_pipe<64,1,8,2,false> for o and lm_head). Timed back to back in
+    (i4_matvec_pipe<64,1,8,P,true> for the fused qkv and gate/up launches,
+    i4_matvec_pipe<64,1,8,P,false> for o and lm_head; P = 1 register slot when
+    every workgroup has one tile: qkv and o). Timed back to back in
     step order with events at both ends, so the mean per launch is the
     kernels' mean duration plus the inter-kernel dispatch gap."""
     dom = [i for i, k in enumerate(work.op_in_dim) if k == HIDDEN]
@@ -215,7 +227,7 @@ def roofline(tq, work, stream, reps):
             traffic = json.load(f).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         pass
-    return {"bound": "hbm", "kernel": "i4_matvec_pipe<64,1,8,2,true|false> (every in_dim=896 launch: qkv, o, "
+    return {"bound": "hbm", "kernel": "i4_matvec_pipe<64,1,8,1|2,true|false> (every in_dim=896 launch: qkv, o, "
                                       "gate/up pair, lm_head)",
             "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
             "traffic": traffic, "launches": len(dom), "bytes_per_launch": b_dom // len(dom),
@@ -243,6 +255,34 @@ def prefill(tq, stream, reps=30):
     dw.free()
     return {"shape": "W 9728x2560 G64, X 2560 x tokens (BASELINE configs[4])",
             "mfma": "v_mfma_f32_32x32x16_f16, fp32 accumulate", "tokens": rows}
+
+
+CONFIGS2 = ((9728, 2560, "gate/up"), (2560, 9728, "down"), (4096, 2560, "attn in"), (2560, 4096, "attn out"))
+
+
+def configs2(tq, stream):
+    """BASELINE configs[2] (Qwen3.5-4B scale) matvecs other than the lm_head:
+    gate/up 9728x2560, down 2560x9728, attention 4096x2560 and 2560x4096, each
+    rotated over enough copies to exceed 2x the 256 MB MALL (cold reads);
+    median of 7 batches of at least 60 launches."""
+    rows = []
+    for M, K, role in CONFIGS2:
+        w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -4, f"c2_{M}x{K}"))
+        x = tq.synth_normal(K, seed=tq.synth_seed(0, -4, f"c2x_{K}"))
+        b = algo_bytes(M, K)
+        ncopy = (512 << 20) // (M * ((K + G - 1) // G) * (4 + G // 2)) + 1
+        copies = [tq.DeviceBuffer.from_array(w) for _ in range(ncopy)]
+        dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
+        ops = [tq.Op(tq.OP_I4_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, G) for c in copies]
+        ms = time_ops(tq, ops, max(1, 60 // ncopy), 1, stream, batches=7) / len(ops)
+        rows.append({"shape": f"{M}x{K}", "role": role, "us": round(ms * 1e3, 2),
+                     "gbs": round(b / (ms * 1e-3) / 1e9, 1), "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                     "bytes": b, "copies": ncopy})
+        for c in copies:
+            c.free()
+        dx.free()
+        dy.free()
+    return rows
 
 
 def vq2(tq, stream, reps=20):
@@ -352,6 +392,7 @@ def main():
     ap.add_argument("--no-host-call", action="store_true", help="skip the host-pointer (PCIe-inclusive) timing")
     ap.add_argument("--no-vq2", action="store_true", help="skip the VQ2 matvec timings")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
+    ap.add_argument("--no-configs2", action="store_true", help="skip the configs[2] gate/up, down and attention matvecs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first run one device-to-device copy of MB MiB (a known-size kernel for counter runs)")
     args = ap.parse_args()
@@ -401,6 +442,9 @@ def main():
     head = None if args.no_headline else headline(tq, stream)
     if head:
         log(f"[bench] headline 151936x2560: {head['us']} us, {head['gbs']} GB/s ({100 * head['frac']:.1f}% of 8 TB/s)")
+    c2 = None if args.no_configs2 else configs2(tq, stream)
+    if c2:
+        log("[bench] configs[2] matvecs: " + ", ".join(f"{r['shape']} {r['us']} us {r['gbs']} GB/s" for r in c2))
     pre = None if args.no_prefill else prefill(tq, stream)
     if pre:
         for r in pre["tokens"]:
@@ -436,6 +480,7 @@ def main():
                    "launches_per_step": len(work.ops), "group_size": G},
         "roofline": roof,
         "headline": head,
+        "configs2": c2,
         "prefill": pre,
         "vq2": v,
         "host_call": host,
