@@ -49,9 +49,11 @@ SHAPES = [
     (257, 1024, 128), (100, 520, 40), (64, 4096, 256), (50, 100, 32), (7, 70, 6), (41, 1000, 48),
     # register-path kernel over many tiles per workgroup (one, two and three
     # windows per wave, run-time group size); the wave-private DMA ring (three
-    # windows: one and two workgroups per CU, rows of more than 24 windows)
+    # windows: one and two workgroups per CU, rows of more than 24 windows,
+    # more tiles than the register path has workgroups); the register path
+    # with one three-window tile per workgroup
     (151936, 896, 64), (16384, 1536, 64), (20000, 2560, 64), (40000, 520, 40), (60000, 2560, 64),
-    (20000, 4096, 64),
+    (20000, 4096, 64), (9728, 2560, 64), (4096, 2560, 64),
 ]
 
 

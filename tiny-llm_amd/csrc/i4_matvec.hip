@@ -1587,12 +1587,15 @@ int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     {
         // The DMA ring pays off only for long rows over many tiles: one window
         // per wave, or at most two tiles per workgroup slot, run faster on the
-        // register path.
+        // register path -- except three windows per wave over more tiles than
+        // the register path has workgroups (9728x2560: 7.6 us on the
+        // wave-private ring below, 9.7 us on the register path).
         const size_t lds2 = 2 * tbuf + fixed;
         int wgs2 = wgs;
         while (wgs2 > 1 && static_cast<size_t>(wgs2) * lds2 > kLdsBytes) --wgs2;
         const int slots = device_cus() * wgs2;
-        if (CPW == 1 || tiles <= 2 * slots) return launch_pipe<GT, CPW, NWMAX>(w, x, y, gm, stream);
+        const bool pipe_one_round = CPW != 3 || tiles <= device_cus() * kPipeWgsPerCu;
+        if (CPW == 1 || (tiles <= 2 * slots && pipe_one_round)) return launch_pipe<GT, CPW, NWMAX>(w, x, y, gm, stream);
     }
     if constexpr (CPW == 3) {
         if (gm.T > 24 || tiles < 32 * device_cus()) {
