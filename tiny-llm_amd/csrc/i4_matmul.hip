@@ -344,6 +344,169 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma(const uint8_t *__rest
     }
 }
 
+// ---- 3. MFMA tile kernel, slot-major staging
+//   The same tile, dequantization and MFMA as i4_matmul_mfma, with the per-step
+//   overhead taken out of the loop:
+//   - W is staged slot-major, [10 slots][128 rows] dwords (slot 0/1: group
+//     header of half 0/1 of the step; slot 2 + 4t + i: code dword i of half t).
+//     One DMA instruction moves one slot of 64 rows: its per-lane source is
+//     row * row_bytes, fixed for the whole loop, and the step enters only
+//     through the scalar offset of the slot (SALU), so no per-lane selects.
+//     Reading a slot back, 32 consecutive lanes read 32 consecutive dwords.
+//   - X rows are 128 B; 16-byte chunk c of token row r is stored at position
+//     c ^ ((r >> 1) & 7). A ds_read_b128 is served 16 lanes at a time, one
+//     256-byte bank sweep: the 16 rows a group reads differ in (r & 1, chunk),
+//     so they cover the sweep once (no bank conflicts).
+//   - Every step issues the same DMAs, also past the last step (reads past a
+//     row or the end of the buffer land in a slot that is never consumed), so
+//     the wait before each step is one constant s_waitcnt.
+constexpr int kWSlots = 10;
+constexpr int kBM = 128;
+
+// Byte offset within a row of the step-s dword of W slot `slot` (scalar).
+template <int GT>
+__device__ __forceinline__ int w_slot_offset(int slot, int s, int G, int gb, int groups) {
+    const int t = slot < 2 ? slot : (slot - 2) >> 2;
+    const int k = s * kStepK + 32 * t;
+    const int g = min(k / (GT ? GT : G), groups - 1);  // past the last group: in-row bytes, masked later
+    const int base = g * gb;
+    return slot < 2 ? base : base + 4 + (k - g * (GT ? GT : G)) / 2 + 4 * ((slot - 2) & 3);
+}
+
+// One step's DMAs of one wave: 5 W slot DMAs (instruction i = 5 * wave + q:
+// slot i >> 1, rows 64 (i & 1) + lane) and nx X DMAs of 16 bytes per lane.
+// (Not a template and not a lambda: the DMA builtin exists for the device only.)
+__device__ __forceinline__ void issue_step2(__amdgpu_buffer_rsrc_t wr, __amdgpu_buffer_rsrc_t xr, unsigned char *st,
+                                            const int *wvo, const int *wso, const int *xvo, int nx, int xso,
+                                            int wstage, int wave) {
+#pragma unroll
+    for (int q = 0; q < 5; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wr, (__attribute__((address_space(3))) void *)(st + 256 * (5 * wave + q)), 4, wvo[q], wso[q], 0, 0);
+#pragma unroll
+    for (int q = 0; q < nx; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (__attribute__((address_space(3))) void *)(st + wstage + 1024 * (nx * wave + q)), 16, xvo[q], xso, 0,
+            0);
+}
+
+template <int WN, int GT, int S>
+__global__ __launch_bounds__(kThreads) void i4_matmul_mfma2(const uint8_t *__restrict__ w,
+                                                            const _Float16 *__restrict__ xh,
+                                                            const float *__restrict__ xinv, float *__restrict__ y,
+                                                            int M, int N, int K, int Kp, int G, int row_bytes) {
+    constexpr int BN = 32 * WN;
+    constexpr int WStage = kWSlots * kBM * 4;
+    constexpr int StageBytes = WStage + BN * 128;
+    constexpr int P = 5 + WN;  // DMAs per wave per step
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * BN;
+    if constexpr (GT != 0) G = GT;
+    const int gb = 4 + G / 2;
+    const int groups = (K + G - 1) / G;
+    const int steps = Kp / kStepK;
+
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + static_cast<size_t>(m0) * row_bytes,
+                                                static_cast<size_t>(M - m0) * row_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh + static_cast<size_t>(n0) * Kp,
+                                                static_cast<size_t>(N - n0) * Kp * 2);
+    int wvo[5], wslot[5];
+#pragma unroll
+    for (int q = 0; q < 5; ++q) {
+        const int i = 5 * wave + q;
+        wslot[q] = i >> 1;
+        wvo[q] = (64 * (i & 1) + lane) * row_bytes;
+    }
+    int xvo[WN];
+#pragma unroll
+    for (int q = 0; q < WN; ++q) {
+        const int p = 64 * (WN * wave + q) + lane;
+        const int r = p >> 3, c = (p & 7) ^ ((r >> 1) & 7);
+        xvo[q] = r * Kp * 2 + 16 * c;
+    }
+    // G = 64: both halves of step s lie in group s, so a slot's offset is
+    // 36 * s plus a constant of the slot
+    int wconst[5];
+#pragma unroll
+    for (int q = 0; q < 5; ++q) wconst[q] = w_slot_offset<GT>(wslot[q], 0, G, gb, groups);
+    auto issue = [&](int s) {
+        int wso[5];
+        if constexpr (GT == 64) {
+            const int base = gb * min(s, groups - 1);
+#pragma unroll
+            for (int q = 0; q < 5; ++q) wso[q] = base + wconst[q];
+        } else {
+#pragma unroll
+            for (int q = 0; q < 5; ++q) wso[q] = w_slot_offset<GT>(wslot[q], s, G, gb, groups);
+        }
+        issue_step2(wr, xr, smem + (s % S) * StageBytes, wvo, wso, xvo, WN, s * kStepK * 2, WStage, wave);
+    };
+
+    f16x acc[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[j] = f16x{};
+    const int li = lane & 31, kq = lane >> 5;
+    const int row = 32 * wave + li;
+    // LDS read offsets within a stage (bytes)
+    int xro[4][WN];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int r = 32 * j + li;
+            xro[kk][j] = WStage + 16 * (8 * r + ((2 * kk + kq) ^ ((r >> 1) & 7)));
+        }
+
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) issue(s);
+    for (int s = 0; s < steps; ++s) {
+        wait_vm((S - 2) * P);  // this wave's part of step s has landed
+        lds_barrier();         // every wave's part has; step s - 1's slot is free
+        issue(s + S - 1);      // (past the last step: never consumed)
+        const unsigned char *st = smem + (s % S) * StageBytes;
+        const unsigned *ws = reinterpret_cast<const unsigned *>(st);
+        const unsigned hd0 = ws[row], hd1 = ws[kBM + row];
+        unsigned c[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) c[kk] = ws[(2 + 4 * (kk >> 1) + 2 * (kk & 1) + kq) * kBM + row];
+        h8 b[4][WN];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) b[kk][j] = *reinterpret_cast<const h8 *>(st + xro[kk][j]);
+        const bool v0 = (s * kStepK) / G < groups, v1 = (s * kStepK + 32) / G < groups;
+        const float s0 = v0 ? half_bits_f(hd0) : 0.f;
+        const float s1 = v1 ? half_bits_f(hd1) : 0.f;
+        const float z0 = v0 ? -(half_bits_f(hd0 >> 16) * s0) : 0.f;
+        const float z1 = v1 ? -(half_bits_f(hd1 >> 16) * s1) : 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const h8 a = kk < 2 ? dequant8(c[kk], s0, z0) : dequant8(c[kk], s1, z1);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[kk][j], acc[j], 0, 0, 0);
+        }
+    }
+    wait_vm(0);
+
+    // epilogue: lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        const int n = n0 + 32 * j + li;
+        if (n >= N) continue;
+        const float sc = xinv[n];
+        float *yc = y + static_cast<size_t>(n) * M;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int m = m0 + 32 * wave + 8 * r4 + 4 * kq;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (m + q < M) yc[m + q] = acc[j][4 * r4 + q] * sc;
+        }
+    }
+}
+
 // Grow-only device workspace for the fp16 copy of X (one per process; the
 // launches that use it are ordered on their streams by the caller).
 struct Workspace {
@@ -394,6 +557,28 @@ int launch_tiles(const uint8_t *w, const _Float16 *xh, const float *xinv, float 
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
+template <int WN, int GT, int S>
+int launch_tiles2(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y, int M, int N, int K, int Kp, int G,
+                  int rb, hipStream_t stream) {
+    constexpr int BN = 32 * WN;
+    const size_t lds = static_cast<size_t>(S) * (kWSlots * kBM * 4 + BN * 128);
+    static size_t limit = 0;
+    if (lds > 64 * 1024 && limit == 0) {
+        hipFuncAttributes attr{};
+        const void *fn = reinterpret_cast<const void *>(i4_matmul_mfma2<WN, GT, S>);
+        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
+        limit = 160 * 1024 - attr.sharedSizeBytes;
+        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(limit)));
+    }
+    if (lds > 64 * 1024 && lds > limit) return kTooLarge;
+    // row offsets of the 128 staged rows and token-row offsets must fit the 32-bit DMA offsets
+    if (static_cast<size_t>(kBM) * rb + static_cast<size_t>(Kp) * 2 >= (1ull << 31)) return kTooLarge;
+    const dim3 grid((M + kBM - 1) / kBM, (N + BN - 1) / BN);
+    hipLaunchKernelGGL((i4_matmul_mfma2<WN, GT, S>), grid, dim3(kThreads), lds, stream, w, xh, xinv, y, M, N, K, Kp, G,
+                       rb);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
 // Token blocks of 32 per wave (WN). Measured on MI355X at 9728x2560: one
 // block for <= 32 tokens, two for <= 64, three above (128-token tiles and two
 // row blocks per wave were slower: fewer workgroups, more registers).
@@ -427,6 +612,17 @@ int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, i
     if (hipGetLastError() != hipSuccess) return kLaunchFailed;
     const int ikp = static_cast<int>(Kp), irb = static_cast<int>(rb);
     const int wn = pick_wn(N);
+    int st;
+    if (group_size == 64) {
+        st = wn == 1   ? launch_tiles2<1, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
+             : wn == 2 ? launch_tiles2<2, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
+                       : launch_tiles2<3, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+    } else {
+        st = wn == 1   ? launch_tiles2<1, 0, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
+             : wn == 2 ? launch_tiles2<2, 0, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
+                       : launch_tiles2<3, 0, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+    }
+    if (st != kTooLarge) return st;
     if (group_size == 64) {
         if (wn == 1) return launch_tiles<1, 1, 64>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
         if (wn == 2) return launch_tiles<1, 2, 64>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
