@@ -24,6 +24,7 @@
 #include "tq_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 
 namespace tqhip {
@@ -507,6 +508,132 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma2(const uint8_t *__res
     }
 }
 
+// ---- 4. G = 64: W straight into registers
+//   At G = 64 a step's 64 elements of a row are one group: 36 contiguous bytes
+//   [scale | zero | 32 code bytes] at 36 s. Each lane loads its row's record
+//   with three loads (16 + 16 + 4 bytes) into VGPRs, S - 1 steps ahead, so W
+//   never passes through LDS (measured: the dword-granular W staging of
+//   i4_matmul_mfma2 was 40% of its time). X is staged as in i4_matmul_mfma2.
+//   The loop is unrolled by S so that every register slot index is a
+//   constant; steps past the last are loaded (never consumed) and not
+//   computed, which keeps every wait one constant s_waitcnt.
+__device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char *st, const int *xvo, int nx, int xso,
+                                        int wave) {
+#pragma unroll
+    for (int q = 0; q < nx; ++q)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (__attribute__((address_space(3))) void *)(st + 1024 * (nx * wave + q)), 16, xvo[q], xso, 0, 0);
+}
+
+template <int WN, int S>
+__global__ __launch_bounds__(kThreads) void i4_matmul_g64(const uint8_t *__restrict__ w,
+                                                          const _Float16 *__restrict__ xh,
+                                                          const float *__restrict__ xinv, float *__restrict__ y, int M,
+                                                          int N, int K, int Kp, int row_bytes) {
+    constexpr int BN = 32 * WN;
+    constexpr int XStage = BN * 128;
+    constexpr int P = 3 + WN;  // loads per wave per step: W 16 + 16 + 4 bytes, WN X DMAs
+    constexpr int kGroupBytes = 36;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * BN;
+    const int groups = (K + 63) / 64;
+    const int steps = Kp / kStepK;  // = groups
+
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + static_cast<size_t>(m0) * row_bytes,
+                                                static_cast<size_t>(M - m0) * row_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh + static_cast<size_t>(n0) * Kp,
+                                                static_cast<size_t>(N - n0) * Kp * 2);
+    const int li = lane & 31, kq = lane >> 5;
+    const int wvo = (32 * wave + li) * row_bytes;
+    int xvo[WN];
+#pragma unroll
+    for (int q = 0; q < WN; ++q) {
+        const int p = 64 * (WN * wave + q) + lane;
+        const int r = p >> 3, c = (p & 7) ^ ((r >> 1) & 7);
+        xvo[q] = r * Kp * 2 + 16 * c;
+    }
+    int xro[4][WN];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int r = 32 * j + li;
+            xro[kk][j] = 16 * (8 * r + ((2 * kk + kq) ^ ((r >> 1) & 7)));
+        }
+
+    u4v wa[S], wb[S];
+    unsigned wc[S];
+    auto issue = [&](auto uc, int s) {  // step s into register slot and X stage u = s % S
+        constexpr int u = decltype(uc)::value;
+        const int so = kGroupBytes * min(s, groups - 1);  // (past the last step: in-row bytes, never used)
+        wa[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo, so, 0));
+        wb[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo + 16, so, 0));
+        wc[u] = __builtin_amdgcn_raw_buffer_load_b32(wr, wvo + 32, so, 0);
+        issue_x(xr, smem + u * XStage, xvo, WN, s * kStepK * 2, wave);
+    };
+    f16x acc[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[j] = f16x{};
+    auto compute = [&](auto uc) {
+        constexpr int u = decltype(uc)::value;
+        const unsigned char *st = smem + u * XStage;
+        h8 b[4][WN];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) b[kk][j] = *reinterpret_cast<const h8 *>(st + xro[kk][j]);
+        // code dword i of the group: 0..2 in wa.yzw, 3..6 in wb, 7 in wc; lane half kq takes i = 2 kk' + kq
+        const unsigned c[4] = {kq ? wa[u].z : wa[u].y, kq ? wb[u].x : wa[u].w, kq ? wb[u].z : wb[u].y,
+                               kq ? wc[u] : wb[u].w};
+        const unsigned hd = wa[u].x;
+        const float sc = half_bits_f(hd);
+        const float zs = -(half_bits_f(hd >> 16) * sc);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const h8 a = dequant8(c[kk], sc, zs);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[kk][j], acc[j], 0, 0, 0);
+        }
+    };
+    auto round_step = [&](auto uc, int s) {
+        constexpr int u = decltype(uc)::value;
+        wait_vm((S - 2) * P);  // this wave's loads of step s have landed
+        lds_barrier();         // every wave's X part has; step s - 1's stage is free
+        issue(std::integral_constant<int, (u + S - 1) % S>{}, s + S - 1);
+        if (s < steps) compute(uc);
+    };
+
+    issue(std::integral_constant<int, 0>{}, 0);
+    if constexpr (S > 2) issue(std::integral_constant<int, 1>{}, 1);
+    if constexpr (S > 3) issue(std::integral_constant<int, 2>{}, 2);
+    static_assert(S >= 2 && S <= 4, "register slots 0..3");
+    for (int s0 = 0; s0 < steps; s0 += S) {
+        round_step(std::integral_constant<int, 0>{}, s0);
+        round_step(std::integral_constant<int, 1>{}, s0 + 1);
+        if constexpr (S > 2) round_step(std::integral_constant<int, 2>{}, s0 + 2);
+        if constexpr (S > 3) round_step(std::integral_constant<int, 3>{}, s0 + 3);
+    }
+    wait_vm(0);
+
+    // epilogue: lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+        const int n = n0 + 32 * j + li;
+        if (n >= N) continue;
+        const float sc = xinv[n];
+        float *yc = y + static_cast<size_t>(n) * M;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int m = m0 + 32 * wave + 8 * r4 + 4 * kq;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (m + q < M) yc[m + q] = acc[j][4 * r4 + q] * sc;
+        }
+    }
+}
+
 // Grow-only device workspace for the fp16 copy of X (one per process; the
 // launches that use it are ordered on their streams by the caller).
 struct Workspace {
@@ -579,6 +706,26 @@ int launch_tiles2(const uint8_t *w, const _Float16 *xh, const float *xinv, float
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
+template <int WN, int S>
+int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y, int M, int N, int K, int Kp, int rb,
+               hipStream_t stream) {
+    constexpr int BN = 32 * WN;
+    const size_t lds = static_cast<size_t>(S) * BN * 128;
+    static size_t limit = 0;
+    if (lds > 64 * 1024 && limit == 0) {
+        hipFuncAttributes attr{};
+        const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WN, S>);
+        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
+        limit = 160 * 1024 - attr.sharedSizeBytes;
+        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(limit)));
+    }
+    if (lds > 64 * 1024 && lds > limit) return kTooLarge;
+    if (static_cast<size_t>(kBM) * rb + static_cast<size_t>(Kp) * 2 * BN >= (1ull << 31)) return kTooLarge;
+    const dim3 grid((M + kBM - 1) / kBM, (N + BN - 1) / BN);
+    hipLaunchKernelGGL((i4_matmul_g64<WN, S>), grid, dim3(kThreads), lds, stream, w, xh, xinv, y, M, N, K, Kp, rb);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
 // Token blocks of 32 per wave (WN). Measured on MI355X at 9728x2560: one
 // block for <= 32 tokens, two for <= 64, three above (128-token tiles and two
 // row blocks per wave were slower: fewer workgroups, more registers).
@@ -614,6 +761,10 @@ int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, i
     const int wn = pick_wn(N);
     int st;
     if (group_size == 64) {
+        st = wn == 1   ? launch_g64<1, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+             : wn == 2 ? launch_g64<2, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+                       : launch_g64<3, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
+        if (st != kTooLarge) return st;
         st = wn == 1   ? launch_tiles2<1, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
              : wn == 2 ? launch_tiles2<2, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
                        : launch_tiles2<3, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
