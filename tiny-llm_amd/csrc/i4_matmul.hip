@@ -525,19 +525,22 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char
             xr, (__attribute__((address_space(3))) void *)(st + 1024 * (nx * wave + q)), 16, xvo[q], xso, 0, 0);
 }
 
-template <int WN, int S>
-__global__ __launch_bounds__(kThreads) void i4_matmul_g64(const uint8_t *__restrict__ w,
+template <int WN, int S, int NWV>
+__global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restrict__ w,
                                                           const _Float16 *__restrict__ xh,
                                                           const float *__restrict__ xinv, float *__restrict__ y, int M,
                                                           int N, int K, int Kp, int row_bytes) {
     constexpr int BN = 32 * WN;
+    constexpr int BM = 32 * NWV;
     constexpr int XStage = BN * 128;
-    constexpr int P = 3 + WN;  // loads per wave per step: W 16 + 16 + 4 bytes, WN X DMAs
+    constexpr int XD = 4 * WN / NWV;  // X DMAs per wave per step
+    constexpr int P = 3 + XD;         // loads per wave per step: W 16 + 16 + 4 bytes, the X DMAs
+    static_assert(4 * WN % NWV == 0, "X DMAs split evenly over the waves");
     constexpr int kGroupBytes = 36;
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * BN;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int groups = (K + 63) / 64;
     const int steps = Kp / kStepK;  // = groups
 
@@ -547,10 +550,10 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_g64(const uint8_t *__restr
                                                 static_cast<size_t>(N - n0) * Kp * 2);
     const int li = lane & 31, kq = lane >> 5;
     const int wvo = (32 * wave + li) * row_bytes;
-    int xvo[WN];
+    int xvo[XD];
 #pragma unroll
-    for (int q = 0; q < WN; ++q) {
-        const int p = 64 * (WN * wave + q) + lane;
+    for (int q = 0; q < XD; ++q) {
+        const int p = 64 * (XD * wave + q) + lane;
         const int r = p >> 3, c = (p & 7) ^ ((r >> 1) & 7);
         xvo[q] = r * Kp * 2 + 16 * c;
     }
@@ -571,7 +574,7 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_g64(const uint8_t *__restr
         wa[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo, so, 0));
         wb[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo + 16, so, 0));
         wc[u] = __builtin_amdgcn_raw_buffer_load_b32(wr, wvo + 32, so, 0);
-        issue_x(xr, smem + u * XStage, xvo, WN, s * kStepK * 2, wave);
+        issue_x(xr, smem + u * XStage, xvo, XD, s * kStepK * 2, wave);
     };
     f16x acc[WN];
 #pragma unroll
@@ -706,30 +709,32 @@ int launch_tiles2(const uint8_t *w, const _Float16 *xh, const float *xinv, float
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
-template <int WN, int S>
+template <int WN, int S, int NWV>
 int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y, int M, int N, int K, int Kp, int rb,
                hipStream_t stream) {
-    constexpr int BN = 32 * WN;
+    constexpr int BN = 32 * WN, BM = 32 * NWV;
     const size_t lds = static_cast<size_t>(S) * BN * 128;
     static size_t limit = 0;
     if (lds > 64 * 1024 && limit == 0) {
         hipFuncAttributes attr{};
-        const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WN, S>);
+        const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WN, S, NWV>);
         TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
         limit = 160 * 1024 - attr.sharedSizeBytes;
         TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(limit)));
     }
     if (lds > 64 * 1024 && lds > limit) return kTooLarge;
-    if (static_cast<size_t>(kBM) * rb + static_cast<size_t>(Kp) * 2 * BN >= (1ull << 31)) return kTooLarge;
-    const dim3 grid((M + kBM - 1) / kBM, (N + BN - 1) / BN);
-    hipLaunchKernelGGL((i4_matmul_g64<WN, S>), grid, dim3(kThreads), lds, stream, w, xh, xinv, y, M, N, K, Kp, rb);
+    if (static_cast<size_t>(BM) * rb + static_cast<size_t>(Kp) * 2 * BN >= (1ull << 31)) return kTooLarge;
+    const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
+    hipLaunchKernelGGL((i4_matmul_g64<WN, S, NWV>), grid, dim3(64 * NWV), lds, stream, w, xh, xinv, y, M, N, K, Kp,
+                       rb);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
 // Token blocks of 32 per wave (WN). Measured on MI355X at 9728x2560: one
-// block for <= 32 tokens, two for <= 64, three above (128-token tiles and two
-// row blocks per wave were slower: fewer workgroups, more registers).
-int pick_wn(int N) { return N <= 32 ? 1 : N <= 64 ? 2 : 3; }
+// block for <= 32 tokens, two for <= 128 (30.6 vs 38.2 us at 128 tokens),
+// three above (128-token tiles and two row blocks per wave were slower: fewer
+// workgroups, more registers).
+int pick_wn(int N) { return N <= 32 ? 1 : N <= 128 ? 2 : 3; }
 
 }  // namespace
 
@@ -761,9 +766,11 @@ int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, i
     const int wn = pick_wn(N);
     int st;
     if (group_size == 64) {
-        st = wn == 1   ? launch_g64<1, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-             : wn == 2 ? launch_g64<2, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-                       : launch_g64<3, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
+        // one-wave workgroups of 32 rows for a single token block: four times
+        // the workgroups (304 at 9728 rows), each with a wave-private X ring
+        st = wn == 1   ? launch_g64<1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+             : wn == 2 ? launch_g64<2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+                       : launch_g64<3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
         if (st != kTooLarge) return st;
         st = wn == 1   ? launch_tiles2<1, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
              : wn == 2 ? launch_tiles2<2, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
