@@ -54,6 +54,10 @@ SHAPES = [
     # with one three-window tile per workgroup
     (151936, 896, 64), (16384, 1536, 64), (20000, 2560, 64), (40000, 520, 40), (60000, 2560, 64),
     (20000, 4096, 64), (9728, 2560, 64), (4096, 2560, 64),
+    # the fp32 lane kernel (G = 64, K % 4 == 0, K <= 1024): every lane of a
+    # half-wave live (K = 1024), a partial last group (K = 964), rows shorter
+    # than a group, one and two rows per half-wave (up to 4 tiles per CU)
+    (40, 1024, 64), (3000, 964, 64), (9, 36, 64), (16000, 512, 64),
 ]
 
 
@@ -108,6 +112,20 @@ def test_bad_shapes_return_codes(gpu):
     assert lib.tqhip_matmul_i4_dev(None, None, None, 4, 64, 0, 64, None) == gpu.EBADSHAPE
 
 
+def test_misaligned_activations_take_another_kernel(gpu, orc):
+    """x 4 bytes past a 16-byte boundary: the lane kernel needs 16-byte aligned
+    activations, so this launch goes to the register path; same results as
+    the oracle either way."""
+    M, K, G = 896, 896, 64
+    w = gpu.synth_i4(M, K, G, seed=77)
+    x = gpu.synth_normal(K + 4, seed=78)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
+    st = gpu.lib().tqhip_matvec_i4_dev(dw.ptr, dx.ptr + 4, dy.ptr, M, K, G, None)
+    assert st == 0
+    gpu.synchronize()
+    assert_close(dy.download(np.float32, M), orc.matvec_i4(w, x[1:K + 1], M, K, G, threads=16), "misaligned x")
+
+
 # qkv / pair on device buffers: one launch over all the matrices (the staged
 # kernel) or one per matrix (rows past its window limit, group sizes it does
 # not cover). Each output must meet the bar against the oracle and equal the
@@ -118,6 +136,8 @@ def same_as_single(got, single, K, G, gpu):
     if gpu.i4_row_bytes(K, G) < 24 * 64:
         return np.array_equal(got, single)
     return float(np.max(np.abs(got - single))) <= 1e-6 * max(float(np.max(np.abs(single))), 1e-30)
+
+
 @pytest.mark.parametrize("q,kv,K,G", [(896, 128, 896, 64), (4096, 1024, 2560, 64), (100, 17, 520, 40),
                                       (64, 16, 4864, 64), (40, 8, 1000, 128), (24, 24, 200, 6)])
 def test_qkv_dev_one_launch_matches_single_and_oracle(gpu, orc, q, kv, K, G):

@@ -1377,6 +1377,138 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
 }
 
 // ============================================================================================
+// Lane kernel (G = 64, K % 4 == 0, rows of at most 32 half-groups: K <= 1024) for grids of
+// up to four 16-row tiles per CU (the decode-size launches): fp32 VALU, no LDS, no barrier.
+// Each wave owns 2 * R rows, one per half-wave and round; lane u of a half-wave takes
+// half-group u of the row (32 weights: 16 code bytes plus the group's header) and the 32
+// activations it multiplies, which stay in VGPRs for all R rows. Per half-group,
+// scale * (sum(q * x) - zero * sum(x)) in fp32; the 32 lanes of a half-wave are added with
+// DPP and one gfx950 row swap in a fixed order. One load round trip, about 100 VALU and
+// the reduction lie between the launch and the store, where the MFMA path also converts
+// the activations, builds operands and synchronises its waves twice through LDS.
+constexpr int kLaneWaves = 4;  // waves per workgroup
+constexpr int kDppMirror = 0x140;
+
+template <int B>
+__device__ inline float ubyte_float(unsigned v) {
+    float f;
+    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
+    if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
+    if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
+    if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
+    return f;
+}
+
+template <int R, bool GROUP>
+__global__ __launch_bounds__(64 * kLaneWaves) void i4_matvec_lane(const uint8_t *__restrict__ w,
+                                                                  const float *__restrict__ x,
+                                                                  float *__restrict__ y, Geom gm) {
+    const int lane = threadIdx.x & 63;
+    const int half = lane >> 5, u = lane & 31;
+    const int job = blockIdx.x * kLaneWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (job >= gm.tile_end[gm.nmat - 1]) return;  // (whole waves)
+    TileRef r;
+    if constexpr (GROUP) {
+        r = TileMap(gm).at(job);
+    } else {
+        r.w = w;
+        r.y = y;
+        r.M = gm.M;
+        r.tile = job;
+    }
+    const int rb = gm.row_bytes;
+    const bool live = u < 2 * gm.Gr;
+    const int row0 = r.tile * (2 * R);
+    const __amdgpu_buffer_rsrc_t wr = rows_rsrc(r.w, r.M, rb, row0);  // rows past the matrix read 0
+    unsigned hd[R];
+    v4i cd[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int off = (2 * i + half) * rb + (kI4Header + 32) * (u >> 1);
+        hd[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
+        cd[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + kI4Header + 16 * (u & 1), 0, 0);
+    }
+    // the 32 activations of half-group u (zeros past K; K % 4 == 0 and x is
+    // 16-byte aligned, so a float4 lies wholly inside or outside x), and their
+    // sum. (Plain loads: with a buffer load of 16 bytes whose elements are used
+    // as floats, this compiler shrank the load to its first dword and reused
+    // that dword for the other three elements.)
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float xv[32];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int e = 32 * u + 4 * q;
+        const float4 v = e < gm.K ? x4[e >> 2] : make_float4(0.f, 0.f, 0.f, 0.f);
+        xv[4 * q] = v.x;
+        xv[4 * q + 1] = v.y;
+        xv[4 * q + 2] = v.z;
+        xv[4 * q + 3] = v.w;
+    }
+    float sx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) sx += xv[e];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned d = static_cast<unsigned>(cd[i][j]);
+            const unsigned lo = d & kNibbles, hi = (d >> 4) & kNibbles;  // elements 8j + 2b and 8j + 2b + 1 in byte b
+            acc = fmaf(ubyte_float<0>(lo), xv[8 * j], acc);
+            acc = fmaf(ubyte_float<0>(hi), xv[8 * j + 1], acc);
+            acc = fmaf(ubyte_float<1>(lo), xv[8 * j + 2], acc);
+            acc = fmaf(ubyte_float<1>(hi), xv[8 * j + 3], acc);
+            acc = fmaf(ubyte_float<2>(lo), xv[8 * j + 4], acc);
+            acc = fmaf(ubyte_float<2>(hi), xv[8 * j + 5], acc);
+            acc = fmaf(ubyte_float<3>(lo), xv[8 * j + 6], acc);
+            acc = fmaf(ubyte_float<3>(hi), xv[8 * j + 7], acc);
+        }
+        const float sc = half_bits(hd[i]), z = half_bits(hd[i] >> 16);
+        float p = live ? sc * fmaf(-z, sx, acc) : 0.f;
+        p += dpp_f<kDppXor1>(p);
+        p += dpp_f<kDppXor2>(p);
+        p += dpp_f<kDppHalfMirror>(p);
+        p += dpp_f<kDppMirror>(p);
+        const unsigned pu = __builtin_bit_cast(unsigned, p);
+        const auto sw = __builtin_amdgcn_permlane16_swap(pu, pu, false, false);  // rows (0,0,2,2) and (1,1,3,3)
+        p = __builtin_bit_cast(float, static_cast<unsigned>(sw[0])) + __builtin_bit_cast(float, static_cast<unsigned>(sw[1]));
+        const int row = row0 + 2 * i + half;
+        if (u == 0 && row < r.M) store_y(r.y + row, p);
+    }
+}
+
+template <int R>
+int launch_lane(const uint8_t *w, const float *x, float *y, Geom gm, const int *rows, hipStream_t stream) {
+    int end = 0;
+    for (int j = 0; j < kMaxGroup; ++j) {
+        if (j < gm.nmat) end += (rows[j] + 2 * R - 1) / (2 * R);
+        gm.tile_end[j] = end;  // jobs (2 R rows) of matrices 0..j
+    }
+    const int grid = (end + kLaneWaves - 1) / kLaneWaves;
+    if (gm.nmat > 1)
+        hipLaunchKernelGGL((i4_matvec_lane<R, true>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
+    else
+        hipLaunchKernelGGL((i4_matvec_lane<R, false>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+int device_cus();
+
+// The lane kernel runs for short rows on grids of at most kLaneMaxTilesPerCu
+// 16-row tiles per CU (everything at K = 896 but lm_head): G = 64, K % 4 == 0
+// and x 16-byte aligned (whole float4 activation loads), K <= 1024.
+constexpr int kLaneMaxTilesPerCu = 4;
+inline bool lane_fits(const float *x, int K, int G, int tiles) {
+    return G == 64 && K % 4 == 0 && K <= 1024 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+           tiles <= kLaneMaxTilesPerCu * device_cus();
+}
+// Rows per half-wave: one while the grid is at most one tile per CU (more
+// waves, shorter chains: 896x896 2.99 vs 3.18 us), two above (the activations
+// reused over twice the rows: the 2x4864x896 gate/up pair 5.52 us, against
+// 5.84 on the register path).
+inline int lane_rows(int tiles) { return tiles <= device_cus() ? 1 : 2; }
+
+// ============================================================================================
 // Register-only kernel (rows of 49..96 windows): operands straight from HBM.
 template <int GT, int CPW>
 __global__ __launch_bounds__(1024, 4) void i4_matvec_reg(const uint8_t *__restrict__ w, const float *__restrict__ x,
@@ -1813,6 +1945,9 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
     }
     gm.ksplit = 1;
     int st;
+    if (lane_fits(x, in_dim, group_size, gm.tile_end[0]))
+        return lane_rows(gm.tile_end[0]) == 1 ? launch_lane<1>(w, x, y, gm, &out_dim, stream)
+                                              : launch_lane<2>(w, x, y, gm, &out_dim, stream);
     if (TQ_USE_DMA && (group_size == 64 || group_size == 128)) {
         st = group_size == 64 ? launch_split_for<64>(w, x, y, gm, stream) : launch_split_for<128>(w, x, y, gm, stream);
         if (st != kTooLarge) return st;
@@ -1872,6 +2007,9 @@ int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, cons
         gm.mw[j] = w[jj];
         gm.my[j] = y[jj];
     }
+    if (lane_fits(x, in_dim, group_size, end))
+        return lane_rows(end) == 1 ? launch_lane<1>(w[0], x, y[0], gm, out_dim, stream)
+                                   : launch_lane<2>(w[0], x, y[0], gm, out_dim, stream);
     const int st = group_size == 64    ? launch_mfma_for<64>(w[0], x, y[0], gm, stream)
                    : group_size == 128 ? launch_mfma_for<128>(w[0], x, y[0], gm, stream)
                                        : launch_mfma_for<0>(w[0], x, y[0], gm, stream);
