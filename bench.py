@@ -18,8 +18,8 @@ Printed (one JSON line on stdout):
   us_per_layer_set  time of one layer's 7 matvecs (the 24-layer part / 24)
   graph        the same step captured into one HIP graph (tqhip_ops_graph_create)
                and replayed --steps times: ms, GB/s, layer set
-  roofline     the kernel with the largest share of the step's time (the
-               register-path i4 MFMA matvec, every in_dim=896 launch):
+  roofline     the kernel with the largest share of the step's time (the fp32
+               lane matvec of every layer's qkv, o and gate/up launch):
                algorithmic bytes of its launches / their time, those launches
                timed back to back in step order with HIP events on the launch
                stream,
@@ -205,18 +205,17 @@ def headline(tq, stream, reps=20):
             "rotation": "3 copies, 657 MB"}
 
 
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "i4_matvec_pipe_decode_step_traffic.json")
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "i4_matvec_lane_decode_step_traffic.json")
 
 
 def roofline(tq, work, stream, reps):
-    """The in_dim=896 launches (qkv, o, gate/up pair, lm_head) all run the
-    register-path MFMA matvec with 8 windows per row, one per wave
-    (i4_matvec_pipe<64,1,8,P,true> for the fused qkv and gate/up launches,
-    i4_matvec_pipe<64,1,8,P,false> for o and lm_head; P = 1 register slot when
-    every workgroup has one tile: qkv and o). Timed back to back in
-    step order with events at both ends, so the mean per launch is the
-    kernels' mean duration plus the inter-kernel dispatch gap."""
-    dom = [i for i, k in enumerate(work.op_in_dim) if k == HIDDEN]
+    """The kernel with the largest share of the step: the fp32 lane matvec
+    (i4_matvec_lane<R, GROUP>) of every layer's qkv, o and gate/up pair launch
+    (72 launches: one row per half-wave for qkv and o, two for the pair; the
+    lm_head launch runs the register-path MFMA kernel and is not counted).
+    Timed back to back in step order with events at both ends, so the mean per
+    launch is the kernels' mean duration plus the inter-kernel dispatch gap."""
+    dom = [i for i, k in enumerate(work.op_in_dim) if k == HIDDEN and work.ops[i].out_dim != VOCAB]
     ops = [work.ops[i] for i in dom]
     ms = time_ops(tq, ops, reps, 2, stream, batches=5)
     b_dom = sum(work.op_bytes[i] for i in dom)
@@ -227,8 +226,8 @@ def roofline(tq, work, stream, reps):
             traffic = json.load(f).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         pass
-    return {"bound": "hbm", "kernel": "i4_matvec_pipe<64,1,8,1|2,true|false> (every in_dim=896 launch: qkv, o, "
-                                      "gate/up pair, lm_head)",
+    return {"bound": "hbm", "kernel": "i4_matvec_lane<1|2,true|false> (every layer's qkv, o and gate/up pair "
+                                      "launch)",
             "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_GBS, 4),
             "traffic": traffic, "launches": len(dom), "bytes_per_launch": b_dom // len(dom),
             "avg_launch_us": round(ms * 1e3 / len(dom), 3)}
