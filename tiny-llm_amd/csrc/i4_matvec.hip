@@ -1477,6 +1477,93 @@ __global__ __launch_bounds__(64 * kLaneWaves) void i4_matvec_lane(const uint8_t 
     }
 }
 
+// Long rows (32 < half-groups <= 64 S): the same arithmetic with one wave per
+// row; lane u takes half-groups u, u + 64, ..., and the 64 lanes are added
+// with DPP and the two gfx950 row swaps (sum_rows4).
+template <int S, bool GROUP>
+__global__ __launch_bounds__(64 * kLaneWaves) void i4_matvec_lanew(const uint8_t *__restrict__ w,
+                                                                   const float *__restrict__ x,
+                                                                   float *__restrict__ y, Geom gm) {
+    const int u = threadIdx.x & 63;
+    const int job = blockIdx.x * kLaneWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (job >= gm.tile_end[gm.nmat - 1]) return;  // (whole waves)
+    TileRef r;
+    if constexpr (GROUP) {
+        r = TileMap(gm).at(job);
+    } else {
+        r.w = w;
+        r.y = y;
+        r.M = gm.M;
+        r.tile = job;
+    }
+    const int rb = gm.row_bytes, U = 2 * gm.Gr;
+    const __amdgpu_buffer_rsrc_t wr = rows_rsrc(r.w, r.M, rb, r.tile);  // one row; past the matrix: reads 0
+    unsigned hd[S];
+    v4i cd[S];
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) {
+        const int unit = u + 64 * sl;
+        const int off = (kI4Header + 32) * (unit >> 1);
+        hd[sl] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
+        cd[sl] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + kI4Header + 16 * (unit & 1), 0, 0);
+    }
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float p = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl) {
+        const int unit = u + 64 * sl;
+        float xv[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int e = 32 * unit + 4 * q;
+            const float4 v = e < gm.K ? x4[e >> 2] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[4 * q] = v.x;
+            xv[4 * q + 1] = v.y;
+            xv[4 * q + 2] = v.z;
+            xv[4 * q + 3] = v.w;
+        }
+        float sx = 0.f, acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) sx += xv[e];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const unsigned d = static_cast<unsigned>(cd[sl][j]);
+            const unsigned lo = d & kNibbles, hi = (d >> 4) & kNibbles;
+            acc = fmaf(ubyte_float<0>(lo), xv[8 * j], acc);
+            acc = fmaf(ubyte_float<0>(hi), xv[8 * j + 1], acc);
+            acc = fmaf(ubyte_float<1>(lo), xv[8 * j + 2], acc);
+            acc = fmaf(ubyte_float<1>(hi), xv[8 * j + 3], acc);
+            acc = fmaf(ubyte_float<2>(lo), xv[8 * j + 4], acc);
+            acc = fmaf(ubyte_float<2>(hi), xv[8 * j + 5], acc);
+            acc = fmaf(ubyte_float<3>(lo), xv[8 * j + 6], acc);
+            acc = fmaf(ubyte_float<3>(hi), xv[8 * j + 7], acc);
+        }
+        const float sc = half_bits(hd[sl]), z = half_bits(hd[sl] >> 16);
+        if (unit < U) p += sc * fmaf(-z, sx, acc);
+    }
+    p += dpp_f<kDppXor1>(p);
+    p += dpp_f<kDppXor2>(p);
+    p += dpp_f<kDppHalfMirror>(p);
+    p += dpp_f<kDppMirror>(p);
+    p = sum_rows4(p);
+    if (u == 0 && r.tile < r.M) store_y(r.y + r.tile, p);
+}
+
+template <int S>
+int launch_lanew(const uint8_t *w, const float *x, float *y, Geom gm, const int *rows, hipStream_t stream) {
+    int end = 0;
+    for (int j = 0; j < kMaxGroup; ++j) {
+        if (j < gm.nmat) end += rows[j];
+        gm.tile_end[j] = end;  // jobs (rows) of matrices 0..j
+    }
+    const int grid = (end + kLaneWaves - 1) / kLaneWaves;
+    if (gm.nmat > 1)
+        hipLaunchKernelGGL((i4_matvec_lanew<S, true>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
+    else
+        hipLaunchKernelGGL((i4_matvec_lanew<S, false>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
 template <int R>
 int launch_lane(const uint8_t *w, const float *x, float *y, Geom gm, const int *rows, hipStream_t stream) {
     int end = 0;
@@ -1507,6 +1594,23 @@ inline bool lane_fits(const float *x, int K, int G, int tiles) {
 // reused over twice the rows: the 2x4864x896 gate/up pair 5.52 us, against
 // 5.84 on the register path).
 inline int lane_rows(int tiles) { return tiles <= device_cus() ? 1 : 2; }
+
+// Long rows (1024 < K <= 64 * 3 * 32) on grids of at most one 16-row tile per
+// four CUs (one wave per row): 896x4864 4.8 vs 5.6 us on split-K, 300x2560 3.6
+// vs 5.3 us; at 160 and 256 tiles the MFMA kernels win (8.2 vs 7.6 us at
+// 2560x4096, 8.0 vs 5.4 us at 4096x2560).
+inline int lanew_slots(const float *x, int K, int G, int tiles) {
+    if (G != 64 || K % 4 != 0 || K <= 1024 || K > 3 * 64 * 32 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 ||
+        4 * tiles > device_cus())
+        return 0;
+    return (K + 64 * 32 - 1) / (64 * 32);  // 64-half-group slots per lane: 1..3
+}
+int launch_lanew_for(const uint8_t *w, const float *x, float *y, const Geom &gm, const int *rows, int slots,
+                     hipStream_t stream) {
+    return slots == 1 ? launch_lanew<1>(w, x, y, gm, rows, stream)
+           : slots == 2 ? launch_lanew<2>(w, x, y, gm, rows, stream)
+                        : launch_lanew<3>(w, x, y, gm, rows, stream);
+}
 
 // ============================================================================================
 // Register-only kernel (rows of 49..96 windows): operands straight from HBM.
@@ -1948,6 +2052,8 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
     if (lane_fits(x, in_dim, group_size, gm.tile_end[0]))
         return lane_rows(gm.tile_end[0]) == 1 ? launch_lane<1>(w, x, y, gm, &out_dim, stream)
                                               : launch_lane<2>(w, x, y, gm, &out_dim, stream);
+    if (const int sl = lanew_slots(x, in_dim, group_size, gm.tile_end[0]))
+        return launch_lanew_for(w, x, y, gm, &out_dim, sl, stream);
     if (TQ_USE_DMA && (group_size == 64 || group_size == 128)) {
         st = group_size == 64 ? launch_split_for<64>(w, x, y, gm, stream) : launch_split_for<128>(w, x, y, gm, stream);
         if (st != kTooLarge) return st;
@@ -2010,6 +2116,8 @@ int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, cons
     if (lane_fits(x, in_dim, group_size, end))
         return lane_rows(end) == 1 ? launch_lane<1>(w[0], x, y[0], gm, out_dim, stream)
                                    : launch_lane<2>(w[0], x, y[0], gm, out_dim, stream);
+    if (const int sl = lanew_slots(x, in_dim, group_size, end))
+        return launch_lanew_for(w[0], x, y[0], gm, out_dim, sl, stream);
     const int st = group_size == 64    ? launch_mfma_for<64>(w[0], x, y[0], gm, stream)
                    : group_size == 128 ? launch_mfma_for<128>(w[0], x, y[0], gm, stream)
                                        : launch_mfma_for<0>(w[0], x, y[0], gm, stream);
