@@ -61,6 +61,13 @@ void tqhip_matvec_vq2(const uint8_t *w, const float *x, float *y, int out_dim, i
 /* MatmulI4Fn, kernels/dispatch.h:249-250; replaces matmul_i4_ref (kernels/matvec/matmul_i4_ref.cpp:53). */
 void tqhip_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size);
 
+/* BiipRotateFn, kernels/dispatch.h:226-227; replaces biip_rotate_activation_ref
+ * (kernels/biip/biip_rotate.cpp:37-68): y = blockHadamard((x / scale) * sign),
+ * scale == NULL skipping the division, block_size a power of two dividing dim;
+ * y may alias x. scale and sign are cached in HBM like weights (by host pointer,
+ * size and fingerprint). Bit-identical to the reference's scalar rotation. */
+void tqhip_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size);
+
 /* Drops every cached device copy of host weights (not in the reference: its
  * CUDA variants keep their cache until exit). */
 void tqhip_release_weights(void);
@@ -78,6 +85,9 @@ int tqhip_matvec_qkv_i4_dev(const uint8_t *wq, const uint8_t *wk, const uint8_t 
                             float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size, void *stream);
 int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                         void *stream);
+/* The BiIP rotation on device buffers (y may alias x). */
+int tqhip_biip_rotate_dev(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,
+                          void *stream);
 /* The portable fp32 one-wave-per-row i4 kernel, used by the fast path for
  * group sizes it does not cover; exported for cross-checks. */
 int tqhip_matvec_i4_generic_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim,
@@ -92,6 +102,13 @@ int tqhip_set_matvec_vq2_impl_by_name(const char *name);
 const char *tqhip_matvec_vq2_impl_name(void);
 const char *tqhip_available_matvec_vq2_impls(void);
 int tqhip_set_matmul_i4_impl_by_name(const char *name);
+/* The ops registry's BiIP member (set_ops_impl_by_name / ops_impl_name /
+ * biip_rotate_activation, kernels/dispatch.h:229-230, 320-321). Unlike the
+ * reference, "ref" is rejected: this library has no CPU path. */
+int tqhip_set_ops_impl_by_name(const char *name);
+const char *tqhip_ops_impl_name(void);
+void tqhip_biip_rotate_activation(const float *x, float *y, int dim, const float *scale, const float *sign,
+                                  int block_size);
 void tqhip_dispatch_matvec_i4(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size);
 void tqhip_dispatch_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2,
                                    int out_dim, int in_dim, int group_size);
@@ -133,7 +150,7 @@ typedef struct tqhip_op {
     const float *x;
     float *y;
     int out_dim, in_dim, n, group_size;
-    const void *w2, *w3;      /* PAIR: w2 / y2; QKV: k = (w2, y2), v = (w3, y3) */
+    const void *w2, *w3;      /* PAIR: w2 / y2; QKV: k = (w2, y2), v = (w3, y3); BIIP: scale, sign */
     float *y2, *y3;
     int out_dim2;             /* QKV: kv_dim (out_dim is q_dim) */
 } tqhip_op;
@@ -142,6 +159,7 @@ typedef struct tqhip_op {
 #define TQHIP_OP_I4_MATMUL 3
 #define TQHIP_OP_I4_PAIR 4
 #define TQHIP_OP_I4_QKV 5
+#define TQHIP_OP_BIIP_ROTATE 6   /* x -> y, in_dim = dim, group_size = block_size, w2 = scale (or NULL), w3 = sign */
 int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream);
 /* As tqhip_run_ops, with a HIP event pair around every call; op_ms[i] gets the
  * mean event-to-event time of call i over the repeats (kernel duration as the

@@ -13,6 +13,7 @@ Functions and the reference code they restate:
   matvec_vq2     kernels/matvec/matvec_vq2_ref.cpp:52-81
   matmul_i4      kernels/matvec/matmul_i4_ref.cpp:53-114
   dequant_i4_row kernels/ref_ops.h:183-205
+  biip_rotate    kernels/biip/biip_rotate.cpp:37-68
   half_to_float / float_to_half   kernels/ref_ops.h:51-105
   i4_row_bytes / vq2_tensor_bytes runtime/tiny_format.h:73-78, 100-103
   quantized_size quantization/quant.cpp:94-118
@@ -45,6 +46,7 @@ _SIGS = {
     "orc_matmul_i4": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "orc_matmul_i4_mt": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _i]),
     "orc_dequant_i4_row": (None, [_vp, _i, _i, _i, _vp]),
+    "orc_biip_rotate": (None, [_vp, _vp, _i, _vp, _vp, _i]),
 }
 _REF_SIGS = {
     "tqref_matvec_i4": (None, [_vp, _vp, _vp, _i, _i, _i]),
@@ -59,6 +61,7 @@ _REF_SIGS = {
     "tqref_half_to_float_n": (None, [_vp, _vp, ctypes.c_longlong]),
     "tqref_float_to_half_n": (None, [_vp, _vp, ctypes.c_longlong]),
     "tqref_unknown_i4_name_rejected": (_i, []),
+    "tqref_biip_rotate": (None, [_vp, _vp, _i, _vp, _vp, _i]),
 }
 
 _LIB = None
@@ -170,6 +173,16 @@ def dequant_i4_row(embed, row, dim, group_size) -> np.ndarray:
     out = np.zeros(dim, dtype=np.float32)
     lib().orc_dequant_i4_row(_p(embed), row, dim, group_size, _p(out))
     return out
+
+
+def biip_rotate(x, scale, sign, block_size) -> np.ndarray:
+    """BiIP activation rotation; scale None = the reference's nullptr (no division)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    sc = None if scale is None else np.ascontiguousarray(scale, dtype=np.float32)
+    sg = np.ascontiguousarray(sign, dtype=np.float32)
+    lib().orc_biip_rotate(_p(x), _p(y), x.size, None if sc is None else _p(sc), _p(sg), block_size)
+    return y
 
 
 def dequant_i4_matrix_f64(w: np.ndarray, out_dim: int, in_dim: int, group_size: int) -> np.ndarray:

@@ -275,4 +275,25 @@ void orc_dequant_i4_row(const uint8_t *embed, int row, int dim, int group_size, 
     }
 }
 
+// BiIP activation rotation (kernels/biip/biip_rotate.cpp:37-68):
+// y = blockHadamard((x / scale) * sign), scale == nullptr skipping the division;
+// per block of block_size (a power of two) an unnormalised butterfly, stage h
+// = 1, 2, 4, ... replacing (a, c) at (j, j + h) by (a + c, a - c), then every
+// element times 1 / sqrt(block_size) (computed in float). y may alias x.
+void orc_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size) {
+    for (int j = 0; j < dim; ++j) y[j] = scale ? (x[j] / scale[j]) * sign[j] : x[j] * sign[j];
+    const float inv_sqrt = 1.0f / std::sqrt(static_cast<float>(block_size));
+    for (int b = 0; b < dim / block_size; ++b) {
+        float *blk = y + static_cast<size_t>(b) * block_size;
+        for (int h = 1; h < block_size; h <<= 1)
+            for (int i = 0; i < block_size; i += 2 * h)
+                for (int j = i; j < i + h; ++j) {
+                    const float a = blk[j], c = blk[j + h];
+                    blk[j] = a + c;
+                    blk[j + h] = a - c;
+                }
+        for (int j = 0; j < block_size; ++j) blk[j] *= inv_sqrt;
+    }
+}
+
 }  // extern "C"

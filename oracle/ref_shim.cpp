@@ -2,7 +2,7 @@
 //
 // TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile (target `ref`) together
 // with the reference's unmodified sources, read in place from the reference
-// tree: kernels/dispatch.cpp and kernels/*/*_ref.cpp. The result,
+// tree: kernels/dispatch.cpp, kernels/*/*_ref.cpp and kernels/biip/biip_rotate.cpp. The result,
 // oracle/_ref/libtqref.so, is the compiled reference `ref` path; tests and
 // tests/golden/make_golden.py use it to pin the restatement in oracle.cpp.
 //
@@ -78,6 +78,13 @@ uint16_t tqref_float_to_half(float f) { return tinyqwen::float_to_half(f); }
 
 int tqref_unknown_i4_name_rejected(void) {
     return tinyqwen::set_matvec_i4_impl_by_name("no_such_impl") ? 0 : 1;
+}
+
+// The reference's generic BiIP entry with its ops registry on "ref"
+// (dispatch.cpp:880-889 falls back to biip_rotate_activation_ref).
+void tqref_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size) {
+    if (!tinyqwen::set_ops_impl_by_name("ref")) std::abort();
+    tinyqwen::biip_rotate_activation(x, y, dim, scale, sign, block_size);
 }
 
 }  // extern "C"

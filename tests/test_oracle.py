@@ -248,3 +248,60 @@ def test_oracle_equals_compiled_reference_on_random_inputs(tqa, orc, seed):
         r.tqref_matvec_vq2(v.ctypes.data, x.ctypes.data, y_ref.ctypes.data, M, K)
         assert np.array_equal(bits(orc.matvec_vq2(v, x, M, K)), bits(y_ref))
     assert r.tqref_unknown_i4_name_rejected() == 1
+
+
+# ---------------------------------------------------------------- BiIP activation rotation
+
+BIIP_CASES = [(896, 128, True), (896, 128, False), (4864, 256, True), (256, 64, True), (128, 128, True),
+              (256, 4, True), (256, 2, True), (1024, 256, False), (3072, 256, True), (7, 1, True)]
+
+
+def biip_inputs(dim, with_scale, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(dim) * 3.0).astype(np.float32)
+    scale = rng.uniform(0.25, 4.0, dim).astype(np.float32) if with_scale else None
+    sign = np.where(rng.random(dim) < 0.5, -1.0, 1.0).astype(np.float32)
+    return x, scale, sign
+
+
+def sylvester(n):
+    h = np.ones((1, 1))
+    while h.shape[0] < n:
+        h = np.block([[h, h], [h, -h]])
+    return h
+
+
+@pytest.mark.parametrize("dim,bs,with_scale", BIIP_CASES)
+def test_biip_rotate_equals_compiled_reference(orc, dim, bs, with_scale):
+    r = orc.ref_lib()
+    if r is None:
+        pytest.skip("oracle/_ref not built here (it needs the reference tree)")
+    x, scale, sign = biip_inputs(dim, with_scale, dim + bs)
+    want = np.empty(dim, np.float32)
+    r.tqref_biip_rotate(x.ctypes.data, want.ctypes.data, dim, None if scale is None else scale.ctypes.data,
+                        sign.ctypes.data, bs)
+    assert np.array_equal(bits(orc.biip_rotate(x, scale, sign, bs)), bits(want))
+
+
+@pytest.mark.parametrize("dim,bs,with_scale", BIIP_CASES)
+def test_biip_rotate_equals_dense_hadamard(orc, dim, bs, with_scale):
+    """blockHadamard((x / scale) * sign) with the Sylvester matrix H / sqrt(bs) in float64
+    (the mathematics the butterfly computes; tests/test_biip_rotate.cpp:40-62 checks the
+    same against a naive Hadamard)."""
+    x, scale, sign = biip_inputs(dim, with_scale, 3 * dim + bs)
+    v = x.astype(np.float64) * sign
+    if scale is not None:
+        v = x.astype(np.float64) / scale * sign
+    H = sylvester(bs) / np.sqrt(bs)
+    want = (v.reshape(-1, bs) @ H.T).reshape(-1)
+    got = orc.biip_rotate(x, scale, sign, bs).astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 1e-5 * max(np.max(np.abs(want)), 1.0)
+
+
+def test_biip_rotate_is_orthogonal_and_in_place_safe(orc):
+    x, _, sign = biip_inputs(2048, False, 5)
+    y = orc.biip_rotate(x, None, sign, 256)
+    assert abs(np.linalg.norm(y.astype(np.float64)) / np.linalg.norm(x.astype(np.float64)) - 1.0) < 1e-6
+    z = x.copy()
+    orc.lib().orc_biip_rotate(z.ctypes.data, z.ctypes.data, z.size, None, sign.ctypes.data, 256)
+    assert np.array_equal(bits(z), bits(y))

@@ -21,7 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtqhip.so")
 
 OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH = 0, -1, -2, -3, -4
-OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV = 1, 2, 3, 4, 5
+OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV, OP_BIIP_ROTATE = 1, 2, 3, 4, 5, 6
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -44,6 +44,7 @@ _SIGS = {
     "tqhip_matvec_qkv_i4": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i]),
     "tqhip_matvec_vq2": (None, [_vp, _vp, _vp, _i, _i]),
     "tqhip_matmul_i4": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "tqhip_biip_rotate": (None, [_vp, _vp, _i, _vp, _vp, _i]),
     "tqhip_release_weights": (None, []),
     # device-pointer entry points
     "tqhip_matvec_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
@@ -52,7 +53,11 @@ _SIGS = {
     "tqhip_matvec_pair_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "tqhip_matvec_qkv_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matmul_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "tqhip_biip_rotate_dev": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp]),
     # registry
+    "tqhip_set_ops_impl_by_name": (_i, [ctypes.c_char_p]),
+    "tqhip_ops_impl_name": (ctypes.c_char_p, []),
+    "tqhip_biip_rotate_activation": (None, [_vp, _vp, _i, _vp, _vp, _i]),
     "tqhip_set_matvec_i4_impl_by_name": (_i, [ctypes.c_char_p]),
     "tqhip_matvec_i4_impl_name": (ctypes.c_char_p, []),
     "tqhip_available_matvec_i4_impls": (ctypes.c_char_p, []),
@@ -221,6 +226,22 @@ def matmul_i4(w: np.ndarray, x: np.ndarray, M: int, K: int, N: int, group_size: 
     y = np.empty(M * N, dtype=np.float32)
     lib().tqhip_dispatch_matmul_i4(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size)
     return y
+
+
+def biip_rotate(x: np.ndarray, scale, sign: np.ndarray, block_size: int) -> np.ndarray:
+    """BiIP activation rotation through the ops registry (host pointers); scale None = no division."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    sc = None if scale is None else np.ascontiguousarray(scale, dtype=np.float32)
+    sg = np.ascontiguousarray(sign, dtype=np.float32)
+    lib().tqhip_biip_rotate_activation(_ptr(x), _ptr(y), x.size, None if sc is None else _ptr(sc), _ptr(sg),
+                                       block_size)
+    return y
+
+
+def biip_rotate_dev(x, y, dim: int, scale, sign, block_size: int, stream: "Stream | None" = None) -> None:
+    _check(lib().tqhip_biip_rotate_dev(_ptr(x), _ptr(y), dim, None if scale is None else _ptr(scale), _ptr(sign),
+                                       block_size, _stream(stream)), "tqhip_biip_rotate_dev")
 
 
 def matmul_vq2(w: np.ndarray, x: np.ndarray, M: int, K: int, N: int) -> np.ndarray:

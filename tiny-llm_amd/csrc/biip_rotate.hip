@@ -1,0 +1,71 @@
+// biip_rotate.hip -- BiIP activation rotation for gfx950.
+//
+// y = blockHadamard((x / scale) * sign), the contract of the reference's
+// biip_rotate_activation (kernels/dispatch.h:220-231; scalar reference
+// kernels/biip/biip_rotate.cpp:37-68): scale == nullptr skips the division;
+// every block of block_size elements (a power of two) goes through the
+// unnormalised Walsh-Hadamard butterfly, stage h = 1, 2, 4, ... replacing
+// (a, c) at (j, j + h) by (a + c, a - c), and is then scaled by
+// 1 / sqrt(block_size). It runs ahead of every matvec of a rotated model.
+//
+// One workgroup takes a chunk of whole blocks (up to 2048 elements) into LDS,
+// runs the butterfly stages there with one barrier per stage, and writes the
+// scaled result. Every element goes through the same fp32 operations in the
+// same order as the scalar reference (one correctly rounded division, the
+// sign product, the adds and subtracts of each stage, the final product), so
+// the result is bit-identical to it. y may alias x: a workgroup reads its
+// whole chunk before it writes any of it, and chunks are disjoint.
+
+#include "tq_common.h"
+
+#include <cmath>
+
+namespace tqhip {
+namespace {
+
+constexpr int kBiipThreads = 256;
+constexpr int kBiipChunk = 2048;  // elements per workgroup: whole blocks (block_size divides it)
+
+__global__ __launch_bounds__(kBiipThreads) void biip_rotate_kernel(const float *x, float *y, int dim,
+                                                                   const float *__restrict__ scale,
+                                                                   const float *__restrict__ sign, int lg_bs,
+                                                                   float inv_sqrt) {
+    __shared__ float v[kBiipChunk];
+    const int base = blockIdx.x * kBiipChunk;
+    const int n = min(kBiipChunk, dim - base);  // a whole number of blocks
+    for (int i = threadIdx.x; i < n; i += kBiipThreads) {
+        const int j = base + i;
+        v[i] = scale ? (x[j] / scale[j]) * sign[j] : x[j] * sign[j];
+    }
+    for (int lg = 0; lg < lg_bs; ++lg) {  // stage h = 2^lg
+        __syncthreads();
+        const int h = 1 << lg;
+        for (int p = threadIdx.x; p < n / 2; p += kBiipThreads) {
+            const int j = ((p >> lg) << (lg + 1)) + (p & (h - 1));  // pair (j, j + h) within its block
+            const float a = v[j], c = v[j + h];
+            v[j] = a + c;
+            v[j + h] = a - c;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kBiipThreads) y[base + i] = v[i] * inv_sqrt;
+}
+
+}  // namespace
+
+int launch_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,
+                       hipStream_t stream) {
+    if (dim < 1 || block_size < 1 || (block_size & (block_size - 1)) || block_size > kBiipChunk ||
+        dim % block_size)
+        return kBadShape;
+    int lg = 0;
+    while ((1 << lg) < block_size) ++lg;
+    // computed on the host exactly as the reference does (float sqrt, then 1.0f / it)
+    const float inv_sqrt = 1.0f / std::sqrt(static_cast<float>(block_size));
+    const int grid = (dim + kBiipChunk - 1) / kBiipChunk;
+    hipLaunchKernelGGL(biip_rotate_kernel, dim3(grid), dim3(kBiipThreads), 0, stream, x, y, dim, scale, sign, lg,
+                       inv_sqrt);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+}  // namespace tqhip

@@ -205,6 +205,23 @@ void tqhip_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, i
     TQ_HIP_CHECK(hipStreamSynchronize(s));
 }
 
+void tqhip_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size) {
+    if (dim < 1 || block_size < 1 || (block_size & (block_size - 1)) || dim % block_size)
+        check_status(kBadShape, "tqhip_biip_rotate");
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    hipStream_t s = hb.get_stream();
+    // scale and sign are per-layer model constants: cached in HBM like weights
+    const float *dscale =
+        scale ? reinterpret_cast<const float *>(hb.resident(scale, static_cast<size_t>(dim) * sizeof(float))) : nullptr;
+    const float *dsign = reinterpret_cast<const float *>(hb.resident(sign, static_cast<size_t>(dim) * sizeof(float)));
+    float *dx = hb.ensure(hb.dx, hb.x_cap, dim);
+    upload(dx, x, dim, s);
+    check_status(launch_biip_rotate(dx, dx, dim, dscale, dsign, block_size, s), "tqhip_biip_rotate");
+    download(y, dx, dim, s);
+    TQ_HIP_CHECK(hipStreamSynchronize(s));
+}
+
 void tqhip_release_weights(void) {
     HostBoundary &hb = boundary();
     std::lock_guard<std::mutex> lock(hb.mu);
@@ -234,6 +251,10 @@ int tqhip_matvec_i4_generic_dev(const uint8_t *w, const float *x, float *y, int 
                                 void *stream) {
     return launch_i4_matvec_generic(w, x, y, out_dim, in_dim, group_size, static_cast<hipStream_t>(stream));
 }
+int tqhip_biip_rotate_dev(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,
+                          void *stream) {
+    return launch_biip_rotate(x, y, dim, scale, sign, block_size, static_cast<hipStream_t>(stream));
+}
 int tqhip_matvec_vq2_dev(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, void *stream) {
     return launch_vq2_matvec(w, x, y, out_dim, in_dim, static_cast<hipStream_t>(stream));
 }
@@ -251,6 +272,12 @@ int tqhip_set_matvec_vq2_impl_by_name(const char *name) {
 const char *tqhip_matvec_vq2_impl_name(void) { return tinyqwen::matvec_vq2_impl_name(); }
 const char *tqhip_available_matvec_vq2_impls(void) { return tinyqwen::available_matvec_vq2_impls(); }
 int tqhip_set_matmul_i4_impl_by_name(const char *name) { return tinyqwen::set_matmul_i4_impl_by_name(name) ? 1 : 0; }
+int tqhip_set_ops_impl_by_name(const char *name) { return tinyqwen::set_ops_impl_by_name(name) ? 1 : 0; }
+const char *tqhip_ops_impl_name(void) { return tinyqwen::ops_impl_name(); }
+void tqhip_biip_rotate_activation(const float *x, float *y, int dim, const float *scale, const float *sign,
+                                  int block_size) {
+    tinyqwen::biip_rotate_activation(x, y, dim, scale, sign, block_size);
+}
 void tqhip_dispatch_matvec_i4(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size) {
     tinyqwen::matvec_i4(w, x, y, out_dim, in_dim, group_size);
 }
@@ -340,6 +367,9 @@ static int launch_op(const tqhip_op &op, hipStream_t s) {
         }
         case TQHIP_OP_VQ2_MATVEC: return launch_vq2_matvec(w, op.x, op.y, op.out_dim, op.in_dim, s);
         case TQHIP_OP_I4_MATMUL: return launch_i4_matmul(w, op.x, op.y, op.out_dim, op.in_dim, op.n, op.group_size, s);
+        case TQHIP_OP_BIIP_ROTATE:
+            return launch_biip_rotate(op.x, op.y, op.in_dim, static_cast<const float *>(op.w2),
+                                      static_cast<const float *>(op.w3), op.group_size, s);
         default: return kBadShape;
     }
 }
@@ -442,3 +472,4 @@ TINYQWEN_MATVEC_I4_PAIR_VARIANT(tqhip_matvec_pair_i4, "hip");
 TINYQWEN_MATVEC_QKV_I4_VARIANT(tqhip_matvec_qkv_i4, "hip");
 TINYQWEN_MATVEC_VQ2_VARIANT(tqhip_matvec_vq2, "hip");
 TINYQWEN_MATMUL_I4_VARIANT(tqhip_matmul_i4, "hip");
+TINYQWEN_BIIP_ROTATE_VARIANT(tqhip_biip_rotate, "hip");

@@ -1,7 +1,7 @@
-// dispatch.cpp -- registry for the i4 / VQ2 / i4-matmul families (see dispatch.h).
+// dispatch.cpp -- registry for the i4 / VQ2 / i4-matmul / BiIP-rotation families (see dispatch.h).
 //
 // Behaviour follows the reference's kernels/dispatch.cpp: i4 (:353-441),
-// VQ2 (:465-532) and matmul_i4 (:650-660). Registries are filled by static
+// VQ2 (:465-532), matmul_i4 (:650-660) and biip_rotate_activation (:880-889). Registries are filled by static
 // initialisers before main and only read afterwards; the current selection is
 // meant to be set once at start-up, as in the reference.
 
@@ -77,6 +77,10 @@ Family<MatmulI4Fn> &mm_i4() {
     static Family<MatmulI4Fn> f;
     return f;
 }
+Family<BiipRotateFn> &biip() {
+    static Family<BiipRotateFn> f;
+    return f;
+}
 
 }  // namespace
 
@@ -140,6 +144,17 @@ bool set_matmul_i4_impl_by_name(const char *name) { return mm_i4().select(name);
 const char *matmul_i4_impl_name() { return mm_i4().name(); }
 void matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size) {
     mm_i4().resolve("matmul_i4")(w, x, y, M, K, N, group_size);
+}
+
+// The reference accepts "ref" here for every op and falls back to its scalar
+// _ref functions (dispatch.cpp:777-800, :880-889); this library has no CPU
+// path, so like the other families it accepts only registered names.
+void register_biip_rotate_impl(const char *name, BiipRotateFn fn) { biip().table[name] = fn; }
+bool set_ops_impl_by_name(const char *name) { return biip().select(name); }
+const char *ops_impl_name() { return biip().name(); }
+void biip_rotate_activation(const float *x, float *y, int dim, const float *scale, const float *sign,
+                            int block_size) {
+    biip().resolve("biip_rotate_activation")(x, y, dim, scale, sign, block_size);
 }
 
 }  // namespace tinyqwen

@@ -61,8 +61,22 @@ bool set_matmul_i4_impl_by_name(const char *name);
 const char *matmul_i4_impl_name();
 void matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size);
 
+// BiIP activation rotation (dispatch.h:220-231 of the reference): one of the
+// reference's "ops" (rmsnorm, rope, ... share one selected name,
+// dispatch.cpp:777-800). Only the BiIP member of that family is on this
+// library's path, so only it is registered here.
+using BiipRotateFn = void (*)(const float *x, float *y, int dim, const float *scale, const float *sign,
+                              int block_size);
+void register_biip_rotate_impl(const char *name, BiipRotateFn fn);
+bool set_ops_impl_by_name(const char *name);
+const char *ops_impl_name();
+void biip_rotate_activation(const float *x, float *y, int dim, const float *scale, const float *sign,
+                            int block_size);
+
 }  // namespace tinyqwen
 
+#define TINYQWEN_BIIP_ROTATE_VARIANT(fn, name) \
+    [[maybe_unused]] static const bool tqwen_reg_biip_##fn = (tinyqwen::register_biip_rotate_impl(name, fn), true)
 #define TINYQWEN_MATVEC_I4_VARIANT(fn, name) \
     [[maybe_unused]] static const bool tqwen_reg_i4_##fn = (tinyqwen::register_matvec_i4_impl(name, fn), true)
 #define TINYQWEN_MATVEC_I4_PAIR_VARIANT(fn, name) \
