@@ -85,6 +85,12 @@ int tqhip_matvec_qkv_i4_dev(const uint8_t *wq, const uint8_t *wk, const uint8_t 
                             float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size, void *stream);
 int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                         void *stream);
+/* Compact-i4 embedding lookup: out[t][0..dim) = dequant_i4_row(embed, rows[t],
+ * dim, group_size, .) for t < n (kernels/ref_ops.h:183-205, called per prompt
+ * token by runtime/qwen_forward_prefill.cpp:180); rows is a device array of
+ * token ids. Bit-identical to the reference's row decode. */
+int tqhip_dequant_i4_rows_dev(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
+                              void *stream);
 /* The BiIP rotation on device buffers (y may alias x). */
 int tqhip_biip_rotate_dev(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,
                           void *stream);

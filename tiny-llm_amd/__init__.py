@@ -54,6 +54,7 @@ _SIGS = {
     "tqhip_matvec_qkv_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matmul_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_biip_rotate_dev": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp]),
+    "tqhip_dequant_i4_rows_dev": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     # registry
     "tqhip_set_ops_impl_by_name": (_i, [ctypes.c_char_p]),
     "tqhip_ops_impl_name": (ctypes.c_char_p, []),
@@ -242,6 +243,11 @@ def biip_rotate(x: np.ndarray, scale, sign: np.ndarray, block_size: int) -> np.n
 def biip_rotate_dev(x, y, dim: int, scale, sign, block_size: int, stream: "Stream | None" = None) -> None:
     _check(lib().tqhip_biip_rotate_dev(_ptr(x), _ptr(y), dim, None if scale is None else _ptr(scale), _ptr(sign),
                                        block_size, _stream(stream)), "tqhip_biip_rotate_dev")
+
+
+def dequant_i4_rows_dev(embed, rows, n: int, dim: int, group_size: int, out, stream: "Stream | None" = None) -> None:
+    _check(lib().tqhip_dequant_i4_rows_dev(_ptr(embed), _ptr(rows), n, dim, group_size, _ptr(out), _stream(stream)),
+           "tqhip_dequant_i4_rows_dev")
 
 
 def matmul_vq2(w: np.ndarray, x: np.ndarray, M: int, K: int, N: int) -> np.ndarray:

@@ -251,6 +251,10 @@ int tqhip_matvec_i4_generic_dev(const uint8_t *w, const float *x, float *y, int 
                                 void *stream) {
     return launch_i4_matvec_generic(w, x, y, out_dim, in_dim, group_size, static_cast<hipStream_t>(stream));
 }
+int tqhip_dequant_i4_rows_dev(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
+                              void *stream) {
+    return launch_i4_embed_rows(embed, rows, n, dim, group_size, out, static_cast<hipStream_t>(stream));
+}
 int tqhip_biip_rotate_dev(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,
                           void *stream) {
     return launch_biip_rotate(x, y, dim, scale, sign, block_size, static_cast<hipStream_t>(stream));

@@ -60,6 +60,8 @@ int launch_i4_matvec_generic(const uint8_t *w, const float *x, float *y, int out
 int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, const int *out_dim, const float *x,
                            int in_dim, int group_size, hipStream_t stream);
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
+int launch_i4_embed_rows(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
+                         hipStream_t stream);
 int launch_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,
                        hipStream_t stream);
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
