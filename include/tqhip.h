@@ -41,6 +41,8 @@ extern "C" {
 #define TQHIP_EBADGROUP (-2)    /* group_size odd or < 2 */
 #define TQHIP_ETOOLARGE (-3)    /* shape exceeds the kernel's 32-bit addressing */
 #define TQHIP_ELAUNCH (-4)      /* the kernel launch failed */
+#define TQHIP_EFILE (-5)        /* a .tqwen file was unreadable, invalid or of an unsupported kind */
+#define TQHIP_EHIP (-6)         /* a HIP allocation or copy failed */
 
 /* ---- 1. host-pointer entry points (the "hip" variants) ------------------ */
 
@@ -181,6 +183,40 @@ int tqhip_run_ops_timed(const tqhip_op *ops, int n_ops, int repeats, void *strea
 int tqhip_ops_graph_create(const tqhip_op *ops, int n_ops, void *stream, void **graph_out);
 int tqhip_ops_graph_launch(void *graph, void *stream);
 int tqhip_ops_graph_destroy(void *graph);
+
+/* ---- 5b. .tqwen weight files ---------------------------------------------
+ * Replaces ModelFile::load (runtime/model_loader.h:228, runtime/model_loader.cpp:267-784)
+ * for the files this library serves: format versions 1..3, file dtype f32 / f16 / i4 / VQ2,
+ * model types Qwen2 (0) and Qwen3.5 (1). Such a file is accepted exactly when the reference
+ * accepts it, with the reference's first failing check as the message (validation stages 1,
+ * 2, 4, 4b, 5, 5b). GPTQ-int4 files and the MoE model types (2, 3) are rejected with
+ * TQHIP_EFILE. Only the header and the tensor table are read by inspect; upload streams the
+ * data region into one HBM allocation, where every tensor keeps its file offset
+ * (device = base + offset - data_offset, 64-byte aligned), so the i4 / VQ2 tensors feed the
+ * _dev entry points as they are. */
+typedef struct tqhip_tensor_info {
+    char name[65];            /* NUL-terminated (the file pads names to 64 bytes) */
+    int dtype;                /* 0 f32, 1 f16, 3 i4, 4 VQ2 (runtime/tiny_format.h:197-205) */
+    int ndim;
+    uint64_t shape[4];        /* shape[ndim..3] = 0; i4 / VQ2 are [out_dim, in_dim] */
+    uint64_t offset, nbytes;  /* absolute file offset and byte size of the payload */
+    const void *device;       /* HBM address after tqhip_model_upload, else NULL */
+} tqhip_tensor_info;
+/* Reads and validates `path`; *model gets a handle (TQHIP_OK) or NULL (TQHIP_EFILE, with
+ * the reason in err when err_len > 0). Needs no GPU. */
+int tqhip_model_inspect(const char *path, void **model, char *err, int err_len);
+/* Copies the data region to HBM on the current device (once; later calls return TQHIP_OK).
+ * TQHIP_EFILE if the file's size changed since inspect, TQHIP_EHIP on a HIP failure. */
+int tqhip_model_upload(void *model);
+int tqhip_model_tensor_count(const void *model);
+int tqhip_model_tensor_at(const void *model, int index, tqhip_tensor_info *info);  /* file order */
+/* ModelFile::get (runtime/model_loader.h:298, runtime/model_loader.cpp:793-796): TQHIP_OK, or TQHIP_EBADSHAPE when absent. */
+int tqhip_model_find(const void *model, const char *name, tqhip_tensor_info *info);
+/* Header fields a caller needs to drive the kernels (ModelConfig, runtime/model_loader.h:44-100). */
+int tqhip_model_quant_group_size(const void *model);  /* 0 in v1 files and unquantized files */
+int tqhip_model_file_dtype(const void *model);
+int tqhip_model_type(const void *model);               /* 0 for v1 files */
+void tqhip_model_free(void *model);                   /* frees the HBM copy too */
 
 /* ---- 6. synthetic inputs (portable generator, identical on every host) -- */
 

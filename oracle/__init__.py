@@ -62,6 +62,11 @@ _REF_SIGS = {
     "tqref_float_to_half_n": (None, [_vp, _vp, ctypes.c_longlong]),
     "tqref_unknown_i4_name_rejected": (_i, []),
     "tqref_biip_rotate": (None, [_vp, _vp, _i, _vp, _vp, _i]),
+    "tqref_model_load": (_i, [ctypes.c_char_p, ctypes.c_char_p, _i]),
+    "tqref_model_tensor_count": (_i, []),
+    "tqref_model_tensor_at": (_i, [_i, ctypes.c_char_p, _vp, _vp, _vp, _vp, _vp]),
+    "tqref_model_quant_group_size": (_i, []),
+    "tqref_model_type": (_i, []),
 }
 
 _LIB = None

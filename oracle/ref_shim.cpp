@@ -2,7 +2,8 @@
 //
 // TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile (target `ref`) together
 // with the reference's unmodified sources, read in place from the reference
-// tree: kernels/dispatch.cpp, kernels/*/*_ref.cpp and kernels/biip/biip_rotate.cpp. The result,
+// tree: kernels/dispatch.cpp, kernels/*/*_ref.cpp, kernels/biip/biip_rotate.cpp,
+// runtime/model_loader.cpp and runtime/tensor.cpp. The result,
 // oracle/_ref/libtqref.so, is the compiled reference `ref` path; tests and
 // tests/golden/make_golden.py use it to pin the restatement in oracle.cpp.
 //
@@ -11,11 +12,14 @@
 // code under test is exactly what tinyqwen's runtime would call.
 
 #include "dispatch.h"
+#include "model_loader.h"
 #include "ref_ops.h"
 
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
+#include <string>
 
 namespace {
 void select_ref() {
@@ -86,5 +90,47 @@ void tqref_biip_rotate(const float *x, float *y, int dim, const float *scale, co
     if (!tinyqwen::set_ops_impl_by_name("ref")) std::abort();
     tinyqwen::biip_rotate_activation(x, y, dim, scale, sign, block_size);
 }
+
+// The reference's own .tqwen loader (ModelFile::load, runtime/model_loader.cpp:267),
+// full load without expert offload, as tinyqwen's runtime calls it. One model
+// at a time: tqref_model_load replaces the previous one.
+static tinyqwen::ModelFile *g_model = nullptr;
+
+int tqref_model_load(const char *path, char *err, int err_len) {
+    delete g_model;
+    g_model = new tinyqwen::ModelFile;
+    std::string msg;
+    const bool ok = g_model->load(path, &msg);
+    if (err && err_len > 0) {
+        std::strncpy(err, msg.c_str(), err_len - 1);
+        err[err_len - 1] = 0;
+    }
+    if (!ok) {
+        delete g_model;
+        g_model = nullptr;
+    }
+    return ok ? 1 : 0;
+}
+
+int tqref_model_tensor_count(void) { return g_model ? static_cast<int>(g_model->tensor_count()) : 0; }
+
+// Tensor i in file order: name (NUL-terminated, 65 bytes), dtype, ndim,
+// shape[4], file offset, nbytes, and the quant group size of the model.
+int tqref_model_tensor_at(int i, char *name, int *dtype, int *ndim, uint64_t *shape, uint64_t *offset,
+                          uint64_t *nbytes) {
+    if (!g_model || i < 0 || i >= static_cast<int>(g_model->tensor_count())) return 0;
+    const tinyqwen::TensorView *t = g_model->get(g_model->tensor_names()[i]);
+    std::memset(name, 0, 65);
+    std::strncpy(name, t->name.c_str(), 64);
+    *dtype = static_cast<int>(t->dtype);
+    *ndim = t->ndim;
+    for (int d = 0; d < 4; ++d) shape[d] = t->shape[d];
+    *offset = t->file_offset;
+    *nbytes = t->nbytes;
+    return 1;
+}
+
+int tqref_model_quant_group_size(void) { return g_model ? static_cast<int>(g_model->config().quant_group_size) : -1; }
+int tqref_model_type(void) { return g_model ? static_cast<int>(g_model->config().model_type) : -1; }
 
 }  // extern "C"

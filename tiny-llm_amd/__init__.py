@@ -20,7 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtqhip.so")
 
-OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH = 0, -1, -2, -3, -4
+OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH, EFILE, EHIP = 0, -1, -2, -3, -4, -5, -6
 OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV, OP_BIIP_ROTATE = 1, 2, 3, 4, 5, 6
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -35,6 +35,12 @@ class Op(ctypes.Structure):
     _fields_ = [("kind", _i), ("w", _vp), ("x", _vp), ("y", _vp),
                 ("out_dim", _i), ("in_dim", _i), ("n", _i), ("group_size", _i),
                 ("w2", _vp), ("w3", _vp), ("y2", _vp), ("y3", _vp), ("out_dim2", _i)]
+
+
+class TensorInfo(ctypes.Structure):
+    """tqhip_tensor_info: one entry of a .tqwen tensor table (plus its HBM address once uploaded)."""
+    _fields_ = [("name", ctypes.c_char * 65), ("dtype", _i), ("ndim", _i), ("shape", ctypes.c_uint64 * 4),
+                ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64), ("device", _vp)]
 
 
 _SIGS = {
@@ -97,6 +103,16 @@ _SIGS = {
     "tqhip_ops_graph_create": (_i, [ctypes.POINTER(Op), _i, _vp, ctypes.POINTER(_vp)]),
     "tqhip_ops_graph_launch": (_i, [_vp, _vp]),
     "tqhip_ops_graph_destroy": (_i, [_vp]),
+    # .tqwen weight files
+    "tqhip_model_inspect": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.c_char_p, _i]),
+    "tqhip_model_upload": (_i, [_vp]),
+    "tqhip_model_tensor_count": (_i, [_vp]),
+    "tqhip_model_tensor_at": (_i, [_vp, _i, ctypes.POINTER(TensorInfo)]),
+    "tqhip_model_find": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(TensorInfo)]),
+    "tqhip_model_quant_group_size": (_i, [_vp]),
+    "tqhip_model_file_dtype": (_i, [_vp]),
+    "tqhip_model_type": (_i, [_vp]),
+    "tqhip_model_free": (None, [_vp]),
     # synthetic inputs
     "tq_synth_seed": (ctypes.c_uint64, [ctypes.c_uint64, _i, ctypes.c_char_p]),
     "tq_synth_i4": (None, [_vp, _i, _i, _i, ctypes.c_uint64, ctypes.c_float, ctypes.c_float,
@@ -447,3 +463,68 @@ def run_ops_timed(ops: list, repeats: int, stream: "Stream | None" = None) -> np
     _check(lib().tqhip_run_ops_timed(arr, len(ops), repeats, _stream(stream), out.ctypes.data_as(_f32p)),
            "tqhip_run_ops_timed")
     return out
+
+
+# ---- .tqwen weight files ----------------------------------------------------------------------
+
+class ModelFile:
+    """A validated .tqwen file, optionally resident in HBM.
+
+    Mirrors tinyqwen::ModelFile (runtime/model_loader.h:180-330): ``load`` raises
+    ValueError with the reference loader's message where the reference rejects the
+    file, ``get`` returns None for an absent name, ``tensor_names`` is in file order.
+    ``upload`` copies the data region to HBM; each tensor's ``device`` address then
+    feeds the ``*_dev`` entry points directly.
+    """
+
+    def __init__(self, path: str):
+        handle = _vp()
+        err = ctypes.create_string_buffer(512)
+        rc = lib().tqhip_model_inspect(os.fsencode(path), ctypes.byref(handle), err, len(err))
+        if rc != OK:
+            raise ValueError(err.value.decode(errors="replace") or f"tqhip_model_inspect failed ({rc})")
+        self._h = handle.value
+
+    load = classmethod(lambda cls, path: cls(path))
+
+    def upload(self) -> None:
+        _check(lib().tqhip_model_upload(self._h), "tqhip_model_upload")
+
+    def tensor_count(self) -> int:
+        return int(lib().tqhip_model_tensor_count(self._h))
+
+    def tensor_at(self, i: int) -> TensorInfo:
+        info = TensorInfo()
+        _check(lib().tqhip_model_tensor_at(self._h, i, ctypes.byref(info)), "tqhip_model_tensor_at")
+        return info
+
+    def tensor_names(self) -> list:
+        return [self.tensor_at(i).name.decode() for i in range(self.tensor_count())]
+
+    def get(self, name: str) -> "TensorInfo | None":
+        info = TensorInfo()
+        rc = lib().tqhip_model_find(self._h, name.encode(), ctypes.byref(info))
+        return info if rc == OK else None
+
+    @property
+    def quant_group_size(self) -> int:
+        return int(lib().tqhip_model_quant_group_size(self._h))
+
+    @property
+    def dtype(self) -> int:
+        return int(lib().tqhip_model_file_dtype(self._h))
+
+    @property
+    def model_type(self) -> int:
+        return int(lib().tqhip_model_type(self._h))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().tqhip_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -49,6 +49,8 @@ enum Status : int {
     kBadGroup = -2,      // group_size is odd or < 2
     kTooLarge = -3,      // a byte offset does not fit the 32-bit buffer range
     kLaunchFailed = -4,  // hipGetLastError after the launch was not hipSuccess
+    kBadFile = -5,       // a .tqwen file was unreadable, invalid or of an unsupported kind
+    kHipFailed = -6,     // a HIP allocation or copy failed
 };
 
 // Device-pointer launchers (defined in the .hip files). All return a Status.
