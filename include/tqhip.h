@@ -202,9 +202,23 @@ typedef struct tqhip_tensor_info {
     uint64_t offset, nbytes;  /* absolute file offset and byte size of the payload */
     const void *device;       /* HBM address after tqhip_model_upload, else NULL */
 } tqhip_tensor_info;
+/* Model configuration from the header (ModelConfig, runtime/model_loader.h:44-100). */
+typedef struct tqhip_model_config {
+    int n_layers, hidden_size, intermediate_size, n_heads, n_kv_heads, head_dim, vocab_size, max_seq_len;
+    int tied_embeddings;
+    float rms_norm_eps, rope_theta;
+    int model_type;           /* 0 Qwen2 (also every v1 file), 1 Qwen3.5 */
+    int quant_group_size;     /* 0 in v1 files and unquantized files */
+    int file_dtype;           /* header dtype: 0 f32, 1 f16, 3 i4, 4 VQ2 */
+} tqhip_model_config;
 /* Reads and validates `path`; *model gets a handle (TQHIP_OK) or NULL (TQHIP_EFILE, with
  * the reason in err when err_len > 0). Needs no GPU. */
 int tqhip_model_inspect(const char *path, void **model, char *err, int err_len);
+/* The same for a whole file already in host memory (ModelFile::base(), file_bytes(),
+ * runtime/model_loader.h:262-268), as a caller holding a loaded ModelFile has it. The image
+ * must stay valid until tqhip_model_upload returns. */
+int tqhip_model_inspect_memory(const void *image, uint64_t bytes, void **model, char *err, int err_len);
+int tqhip_model_config_get(const void *model, tqhip_model_config *config);
 /* Copies the data region to HBM on the current device (once; later calls return TQHIP_OK).
  * TQHIP_EFILE if the file's size changed since inspect, TQHIP_EHIP on a HIP failure. */
 int tqhip_model_upload(void *model);
@@ -217,6 +231,28 @@ int tqhip_model_quant_group_size(const void *model);  /* 0 in v1 files and unqua
 int tqhip_model_file_dtype(const void *model);
 int tqhip_model_type(const void *model);               /* 0 for v1 files */
 void tqhip_model_free(void *model);                   /* frees the HBM copy too */
+
+/* ---- 5c. device-resident decode engine -----------------------------------
+ * The gpu_decode boundary (GpuDecodeCreateFn / StepFn / ResetFn / DestroyFn / LogitsFn,
+ * kernels/dispatch.h:337-378; the reference's engine is kernels/cuda/gpu_engine.cu, which
+ * serves f32 / f16 files). This engine serves dense i4 files (model type 0: Qwen2.x with
+ * q/k/v biases, Qwen3 dense with q/k norms): weights as uploaded by tqhip_model_upload, an
+ * fp32 KV cache of max_seq_len positions and all activations in HBM, one HIP-graph replay
+ * per step; only the token id and the next token cross PCIe.
+ *
+ * create: max_seq_len <= 0 takes the model's; above it, TQHIP_EBADSHAPE. A missing tensor, a
+ * wrong shape or an unsupported file gives TQHIP_EFILE; the message is in err. Uploads the
+ * model if it is not yet uploaded; the model must outlive the engine.
+ * step: QwenModel::forward_token (runtime/qwen_forward_token.cpp:83) at position
+ * seq_len: returns the argmax token of the logits, or TQHIP_EBADSHAPE for a token outside
+ * [0, vocab) or a full cache (the reference aborts there), TQHIP_ELAUNCH on a HIP failure.
+ * logits: device pointer to the last step's vocab_size logits (valid until destroy). */
+int tqhip_decode_create(void *model, int max_seq_len, char *err, int err_len, void **engine);
+int tqhip_decode_step(void *engine, int token_id);
+void tqhip_decode_reset(void *engine);      /* back to position 0 (KvCache::reset) */
+void tqhip_decode_destroy(void *engine);
+const float *tqhip_decode_logits(const void *engine);
+int tqhip_decode_seq_len(const void *engine);
 
 /* ---- 6. synthetic inputs (portable generator, identical on every host) -- */
 

@@ -67,6 +67,10 @@ _REF_SIGS = {
     "tqref_model_tensor_at": (_i, [_i, ctypes.c_char_p, _vp, _vp, _vp, _vp, _vp]),
     "tqref_model_quant_group_size": (_i, []),
     "tqref_model_type": (_i, []),
+    "tqref_decode_create": (_i, [ctypes.c_char_p, _i, ctypes.c_char_p, _i]),
+    "tqref_decode_step": (_i, [_i]),
+    "tqref_decode_logits": (None, [_vp, _i]),
+    "tqref_decode_reset": (None, []),
 }
 
 _LIB = None

@@ -3,7 +3,8 @@
 // TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile (target `ref`) together
 // with the reference's unmodified sources, read in place from the reference
 // tree: kernels/dispatch.cpp, kernels/*/*_ref.cpp, kernels/biip/biip_rotate.cpp,
-// runtime/model_loader.cpp and runtime/tensor.cpp. The result,
+// runtime/model_loader.cpp, runtime/tensor.cpp and the CPU forward of
+// runtime/ (QwenModel and what it links). The result,
 // oracle/_ref/libtqref.so, is the compiled reference `ref` path; tests and
 // tests/golden/make_golden.py use it to pin the restatement in oracle.cpp.
 //
@@ -13,12 +14,15 @@
 
 #include "dispatch.h"
 #include "model_loader.h"
+#include "profiler.h"
+#include "qwen_model.h"
 #include "ref_ops.h"
 
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <string>
 
 namespace {
@@ -132,5 +136,34 @@ int tqref_model_tensor_at(int i, char *name, int *dtype, int *ndim, uint64_t *sh
 
 int tqref_model_quant_group_size(void) { return g_model ? static_cast<int>(g_model->config().quant_group_size) : -1; }
 int tqref_model_type(void) { return g_model ? static_cast<int>(g_model->config().model_type) : -1; }
+
+// The reference's CPU decode (QwenModel::create + forward_token,
+// runtime/qwen_model.h:117-149) on a .tqwen file, with the `ref` kernels. One
+// model at a time.
+static tinyqwen::ModelFile *g_dfile = nullptr;
+static tinyqwen::Profiler *g_dprof = nullptr;
+static std::unique_ptr<tinyqwen::QwenModel> g_dmodel;
+
+int tqref_decode_create(const char *path, int max_seq_len, char *err, int err_len) {
+    select_ref();
+    g_dmodel.reset();
+    delete g_dfile;
+    g_dfile = new tinyqwen::ModelFile;
+    if (!g_dprof) g_dprof = new tinyqwen::Profiler(false);
+    std::string msg;
+    bool ok = g_dfile->load(path, &msg);
+    if (ok) ok = tinyqwen::QwenModel::create(*g_dfile, max_seq_len, *g_dprof, &msg, &g_dmodel);
+    if (err && err_len > 0) {
+        std::strncpy(err, msg.c_str(), err_len - 1);
+        err[err_len - 1] = 0;
+    }
+    return ok ? 1 : 0;
+}
+
+int tqref_decode_step(int token) { return g_dmodel->forward_token(token, nullptr, 5, true); }
+
+void tqref_decode_logits(float *out, int n) { std::memcpy(out, g_dmodel->last_logits(), sizeof(float) * n); }
+
+void tqref_decode_reset(void) { g_dmodel->reset(); }
 
 }  // extern "C"

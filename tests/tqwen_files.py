@@ -159,3 +159,52 @@ def vq2_model(group_size: int = 64, hidden: int = 256, vocab: int = 500, seed: i
                vocab_size=vocab, max_seq_len=128, quant_group_size=group_size)
     cfg.update(fields)
     return build(ts, version=3, dtype=VQ2, **cfg), ts
+
+
+def dense_i4_model(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864, vocab=2000, layers=2,
+                   group_size=64, tied=True, biases=True, qk_norm=False, embed_f32=False, seed=0,
+                   max_seq_len=256) -> tuple:
+    """A dense Qwen2.x-shaped i4 file with every tensor QwenModel binds (runtime/qwen_model.cpp:437-640):
+    embedding (i4, or fp32), per layer two RMSNorm weights, q/k/v/o and gate/up/down (i4), optional
+    q/k/v biases and q/k norms, the final norm and, when not tied, lm_head. Norm weights are drawn
+    around 1 and biases around 0. Returns (image, config dict, {name: (dtype, shape, bytes)})."""
+    rng = np.random.default_rng(seed)
+    qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
+    ts = []
+
+    def vec(name, n, mean, std):
+        ts.append(f32_tensor(name, rng.normal(mean, std, n).astype(np.float32)))
+
+    def mat(name, rows, cols):
+        ts.append(tensor(name, I4, (rows, cols), i4_payload(rows, cols, group_size, int(rng.integers(1 << 30)))))
+
+    if embed_f32:
+        ts.append(f32_tensor("model.embed_tokens.weight", rng.normal(0, 0.05, (vocab, hidden)).astype(np.float32)))
+    else:
+        mat("model.embed_tokens.weight", vocab, hidden)
+    for li in range(layers):
+        p = f"model.layers.{li}."
+        vec(p + "input_layernorm.weight", hidden, 1.0, 0.1)
+        vec(p + "post_attention_layernorm.weight", hidden, 1.0, 0.1)
+        mat(p + "self_attn.q_proj.weight", qd, hidden)
+        mat(p + "self_attn.k_proj.weight", kvd, hidden)
+        mat(p + "self_attn.v_proj.weight", kvd, hidden)
+        mat(p + "self_attn.o_proj.weight", hidden, qd)
+        if biases:
+            vec(p + "self_attn.q_proj.bias", qd, 0.0, 0.1)
+            vec(p + "self_attn.k_proj.bias", kvd, 0.0, 0.1)
+            vec(p + "self_attn.v_proj.bias", kvd, 0.0, 0.1)
+        if qk_norm:
+            vec(p + "self_attn.q_norm.weight", head_dim, 1.0, 0.1)
+            vec(p + "self_attn.k_norm.weight", head_dim, 1.0, 0.1)
+        mat(p + "mlp.gate_proj.weight", inter, hidden)
+        mat(p + "mlp.up_proj.weight", inter, hidden)
+        mat(p + "mlp.down_proj.weight", hidden, inter)
+    vec("model.norm.weight", hidden, 1.0, 0.1)
+    if not tied or embed_f32:
+        mat("lm_head.weight", vocab, hidden)
+    cfg = dict(n_layers=layers, hidden_size=hidden, intermediate_size=inter, n_heads=n_heads,
+               n_kv_heads=n_kv_heads, head_dim=head_dim, vocab_size=vocab, max_seq_len=max_seq_len,
+               tied_embeddings=int(tied), rms_norm_eps=1e-6, rope_theta=1e6, quant_group_size=group_size)
+    img = build(ts, version=3, dtype=I4, **cfg)
+    return img, cfg, {t["name"]: (t["dtype"], t["shape"], t["data"]) for t in ts}

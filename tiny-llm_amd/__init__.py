@@ -43,6 +43,15 @@ class TensorInfo(ctypes.Structure):
                 ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64), ("device", _vp)]
 
 
+
+class ModelConfig(ctypes.Structure):
+    """tqhip_model_config: the header's model configuration."""
+    _fields_ = [(n, _i) for n in ("n_layers", "hidden_size", "intermediate_size", "n_heads", "n_kv_heads",
+                                  "head_dim", "vocab_size", "max_seq_len", "tied_embeddings")] + \
+               [("rms_norm_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("model_type", _i),
+                ("quant_group_size", _i), ("file_dtype", _i)]
+
+
 _SIGS = {
     # host-pointer entry points (the "hip" variants)
     "tqhip_matvec_i4": (None, [_vp, _vp, _vp, _i, _i, _i]),
@@ -113,6 +122,15 @@ _SIGS = {
     "tqhip_model_file_dtype": (_i, [_vp]),
     "tqhip_model_type": (_i, [_vp]),
     "tqhip_model_free": (None, [_vp]),
+    "tqhip_model_inspect_memory": (_i, [_vp, ctypes.c_uint64, ctypes.POINTER(_vp), ctypes.c_char_p, _i]),
+    "tqhip_model_config_get": (_i, [_vp, ctypes.POINTER(ModelConfig)]),
+    # device-resident decode engine
+    "tqhip_decode_create": (_i, [_vp, _i, ctypes.c_char_p, _i, ctypes.POINTER(_vp)]),
+    "tqhip_decode_step": (_i, [_vp, _i]),
+    "tqhip_decode_reset": (None, [_vp]),
+    "tqhip_decode_destroy": (None, [_vp]),
+    "tqhip_decode_logits": (_vp, [_vp]),
+    "tqhip_decode_seq_len": (_i, [_vp]),
     # synthetic inputs
     "tq_synth_seed": (ctypes.c_uint64, [ctypes.c_uint64, _i, ctypes.c_char_p]),
     "tq_synth_i4": (None, [_vp, _i, _i, _i, ctypes.c_uint64, ctypes.c_float, ctypes.c_float,
@@ -507,6 +525,12 @@ class ModelFile:
         return info if rc == OK else None
 
     @property
+    def config(self) -> ModelConfig:
+        c = ModelConfig()
+        _check(lib().tqhip_model_config_get(self._h, ctypes.byref(c)), "tqhip_model_config_get")
+        return c
+
+    @property
     def quant_group_size(self) -> int:
         return int(lib().tqhip_model_quant_group_size(self._h))
 
@@ -521,6 +545,52 @@ class ModelFile:
     def close(self) -> None:
         if getattr(self, "_h", None):
             lib().tqhip_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DecodeEngine:
+    """Device-resident decode engine over an uploaded i4 ModelFile (the gpu_decode boundary,
+    kernels/dispatch.h:337-378): ``step(token)`` returns the argmax next token, ``logits()``
+    copies the last step's logits to the host, ``reset()`` returns to position 0."""
+
+    def __init__(self, model: ModelFile, max_seq_len: int = 0):
+        handle = _vp()
+        err = ctypes.create_string_buffer(512)
+        rc = lib().tqhip_decode_create(model._h, max_seq_len, err, len(err), ctypes.byref(handle))
+        if rc != OK:
+            raise ValueError(err.value.decode(errors="replace") or f"tqhip_decode_create failed ({rc})")
+        self._h = handle.value
+        self._model = model  # the engine reads the model's HBM copy
+        self.vocab = model.config.vocab_size
+
+    def step(self, token: int) -> int:
+        r = int(lib().tqhip_decode_step(self._h, int(token)))
+        if r < 0:
+            raise RuntimeError(f"tqhip_decode_step failed with status {r}")
+        return r
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        _check(lib().tqhip_memcpy_d2h(out.ctypes.data, lib().tqhip_decode_logits(self._h), out.nbytes),
+               "hipMemcpy D2H")
+        return out
+
+    def reset(self) -> None:
+        lib().tqhip_decode_reset(self._h)
+
+    @property
+    def seq_len(self) -> int:
+        return int(lib().tqhip_decode_seq_len(self._h))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().tqhip_decode_destroy(self._h)
             self._h = None
 
     def __del__(self):

@@ -1,0 +1,581 @@
+// decode_engine.hip -- device-resident decode engine for dense i4 Qwen2 / Qwen3 models.
+//
+// The "gpu_decode" boundary of the reference (kernels/dispatch.h:337-378: create /
+// step / reset / destroy / logits on an opaque engine). The reference's CUDA engine
+// (kernels/cuda/gpu_engine.cu) serves f32 / f16 files; this one serves the i4
+// HQQ files whose projections the library's matvec kernels run. Weights stay
+// where tqhip_model_upload put them (one HBM allocation per model), activations,
+// the fp32 KV cache and the argmax live in one more allocation, and a step is
+// one HIP-graph replay on the engine's stream: only the token id and the next
+// token cross PCIe.
+//
+// One step follows QwenModel::forward_token (runtime/qwen_forward_token.cpp:83-700)
+// for a Qwen2.x layer: embedding row, RMSNorm, fused q/k/v matvec, biases,
+// optional per-head q/k RMSNorm (Qwen3 dense), RoPE, KV write, attention over
+// positions 0..pos, o matvec, residual, RMSNorm, fused gate/up matvec, SwiGLU,
+// down matvec, residual, final RMSNorm, lm_head matvec, argmax. The small
+// kernels below fuse the elementwise work between the matvecs: residual add
+// with the following RMSNorm, and biases, q/k norm, RoPE and the KV write in one
+// launch.
+
+#include "../../include/tqhip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "tq_common.h"
+
+// The elementwise steps below round every product and sum separately, as the
+// reference's scalar C++ does; contraction into FMAs would change low bits.
+#pragma clang fp contract(off)
+
+namespace tqhip {
+namespace {
+
+constexpr int kNormThreads = 1024;
+constexpr int kMaxHidden = 16 * kNormThreads;  // values per thread kept in registers
+constexpr int kAttnThreads = 256;
+constexpr int kAttnChunk = 4096;               // scores of one chunk of positions in LDS
+constexpr int kArgmaxThreads = 256, kArgmaxPerThread = 8;
+constexpr int kArgmaxPerBlock = kArgmaxThreads * kArgmaxPerThread;
+
+// Fixed-order block sum: a 64-lane butterfly, then every thread adds the wave
+// totals in wave order, so all threads hold the same value.
+template <int NT>
+__device__ double block_sum(double v, double *red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < NT / 64; ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+
+template <int NT>
+__device__ float block_max(float v, float *red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int w = 1; w < NT / 64; ++w) t = fmaxf(t, red[w]);
+    __syncthreads();
+    return t;
+}
+
+// hidden += delta (when given); out = rmsnorm(hidden) * w. rmsnorm_ref
+// (kernels/rmsnorm/rmsnorm_ref.cpp): double sum of squares, float mean,
+// 1 / sqrt(mean + eps), then (x * scale) * w.
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm(float *hidden, const float *delta, const float *w,
+                                                           float *out, int n, float eps) {
+    __shared__ double red[kNormThreads / 64];
+    float h[kMaxHidden / kNormThreads];
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < kMaxHidden / kNormThreads; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        h[j] = 0.0f;
+        if (i < n) {
+            float v = hidden[i];
+            if (delta) {
+                v = v + delta[i];
+                hidden[i] = v;
+            }
+            h[j] = v;
+            ss += static_cast<double>(v) * static_cast<double>(v);
+        }
+    }
+    ss = block_sum<kNormThreads>(ss, red);
+    const float mean_sq = static_cast<float>(ss / n);
+    const float scale = 1.0f / sqrtf(mean_sq + eps);
+#pragma unroll
+    for (int j = 0; j < kMaxHidden / kNormThreads; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        if (i < n) out[i] = (h[j] * scale) * w[i];
+    }
+}
+
+// Row `*token` of an fp32 embedding table.
+__global__ void embed_f32_row(const float *table, const int *token, float *out, int n) {
+    const size_t base = static_cast<size_t>(*token) * n;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = table[base + i];
+}
+
+// One wave per head: blocks [0, n_heads) finish q heads, the rest k heads and
+// write k and v into the cache at `*pos`. Biases (qb/kb/vb may be null), then
+// the per-head RMSNorm when qn/kn are given, then RoPE (rope_ref,
+// kernels/rope/rope_ref.cpp: pairs (i, i + half), inv_freq = theta^(-2i/d)).
+__global__ __launch_bounds__(64) void qkv_finish(float *q, float *k, const float *v, const float *qb,
+                                                 const float *kb, const float *vb, const float *qn,
+                                                 const float *kn, float *kcache, float *vcache, const int *pos_ptr,
+                                                 int n_heads, int hd, int max_seq, float theta, float eps) {
+    __shared__ float xs[256];
+    const int t = threadIdx.x;
+    const bool is_q = static_cast<int>(blockIdx.x) < n_heads;
+    const int head = is_q ? blockIdx.x : blockIdx.x - n_heads;
+    float *x = (is_q ? q : k) + head * hd;
+    const float *b = is_q ? qb : kb;
+    const float *nw = is_q ? qn : kn;
+    const int pos = *pos_ptr;
+    for (int i = t; i < hd; i += 64) xs[i] = b ? x[i] + b[head * hd + i] : x[i];
+    __syncthreads();
+    if (nw) {
+        double ss = 0.0;
+        for (int i = t; i < hd; i += 64) ss += static_cast<double>(xs[i]) * static_cast<double>(xs[i]);
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float scale = 1.0f / sqrtf(static_cast<float>(ss / hd) + eps);
+        __syncthreads();
+        for (int i = t; i < hd; i += 64) xs[i] = (xs[i] * scale) * nw[i];
+        __syncthreads();
+    }
+    const int half = hd / 2;
+    float *kc = is_q ? nullptr : kcache + (static_cast<size_t>(head) * max_seq + pos) * hd;
+    for (int i = t; i < half; i += 64) {
+        const float inv_freq = powf(theta, -static_cast<float>(2 * i) / static_cast<float>(hd));
+        const float angle = static_cast<float>(pos) * inv_freq;
+        const float c = cosf(angle), s = sinf(angle);
+        const float x0 = xs[i], x1 = xs[i + half];
+        const float r0 = x0 * c - x1 * s;
+        const float r1 = x1 * c + x0 * s;
+        x[i] = r0;
+        x[i + half] = r1;
+        if (kc) {
+            kc[i] = r0;
+            kc[i + half] = r1;
+        }
+    }
+    if (!is_q) {
+        float *vc = vcache + (static_cast<size_t>(head) * max_seq + pos) * hd;
+        for (int i = t; i < hd; i += 64) vc[i] = vb ? v[head * hd + i] + vb[head * hd + i] : v[head * hd + i];
+    }
+}
+
+// One workgroup per query head over positions 0..*pos of its KV head
+// (attention_decode_ref, kernels/attention/attention_decode_ref.cpp: scores
+// q.k * scale, softmax, sum of p * v). Positions go in chunks; within a chunk
+// the scores sit in LDS and the softmax is max / exp / sum, across chunks the
+// running max rescales the partial sums. Thread t accumulates dimension
+// t % hd over every (NT / hd)-th position of a chunk.
+__global__ __launch_bounds__(kAttnThreads) void attention_decode(const float *q, const float *kcache,
+                                                                 const float *vcache, float *out, const int *pos_ptr,
+                                                                 int heads_per_kv, int hd, int max_seq, float scale) {
+    __shared__ float qs[256];
+    __shared__ float sc[kAttnChunk];
+    __shared__ float part[kAttnThreads];
+    __shared__ double dred[kAttnThreads / 64];
+    __shared__ float fred[kAttnThreads / 64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int head = blockIdx.x, kvh = head / heads_per_kv;
+    const int seq = *pos_ptr + 1;
+    const float *kh = kcache + static_cast<size_t>(kvh) * max_seq * hd;
+    const float *vh = vcache + static_cast<size_t>(kvh) * max_seq * hd;
+    for (int i = t; i < hd; i += kAttnThreads) qs[i] = q[head * hd + i];
+    __syncthreads();
+    const int slices = kAttnThreads / hd, d = t % hd, slice = t / hd;
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    for (int c0 = 0; c0 < seq; c0 += kAttnChunk) {
+        const int len = min(kAttnChunk, seq - c0);
+        for (int j = wave; j < len; j += kAttnThreads / 64) {
+            const float *kr = kh + static_cast<size_t>(c0 + j) * hd;
+            float dot = 0.0f;
+            for (int i = lane; i < hd; i += 64) dot += qs[i] * kr[i];
+            for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+            if (lane == 0) sc[j] = dot * scale;
+        }
+        __syncthreads();
+        float cmax = -INFINITY;
+        for (int j = t; j < len; j += kAttnThreads) cmax = fmaxf(cmax, sc[j]);
+        cmax = block_max<kAttnThreads>(cmax, fred);
+        const float m_new = fmaxf(m, cmax);
+        double csum = 0.0;
+        for (int j = t; j < len; j += kAttnThreads) {
+            const float p = expf(sc[j] - m_new);
+            sc[j] = p;
+            csum += p;
+        }
+        csum = block_sum<kAttnThreads>(csum, dred);
+        const float rescale = expf(m - m_new);
+        l = l * rescale + static_cast<float>(csum);
+        acc = acc * rescale;
+        for (int j = slice; j < len; j += slices) acc += sc[j] * vh[static_cast<size_t>(c0 + j) * hd + d];
+        m = m_new;
+        __syncthreads();
+    }
+    part[t] = acc;
+    __syncthreads();
+    if (slice == 0) {
+        float o = part[d];
+        for (int s = 1; s < slices; ++s) o += part[s * hd + d];
+        out[head * hd + d] = o * (1.0f / l);
+    }
+}
+
+// gate = silu(gate) * up (swiglu_ref, kernels/silu/swiglu_ref.cpp).
+__global__ void swiglu(float *gate, const float *up, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float g = gate[i];
+        const float s = g / (1.0f + expf(-g));
+        gate[i] = s * up[i];
+    }
+}
+
+// First index of the largest value (argmax_ref, kernels/argmax/argmax_ref.cpp):
+// each block scans its slice, the final block reduces the block winners; ties
+// go to the lower index.
+__device__ void better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__device__ void block_argmax(float &bv, int &bi) {
+    __shared__ float rv[kArgmaxThreads / 64];
+    __shared__ int ri[kArgmaxThreads / 64];
+    for (int o = 32; o > 0; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    if ((threadIdx.x & 63) == 0) {
+        rv[threadIdx.x >> 6] = bv;
+        ri[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    bv = rv[0];
+    bi = ri[0];
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) better(bv, bi, rv[w], ri[w]);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_partial(const float *x, int n, float *pv, int *pi) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    const int base = blockIdx.x * kArgmaxPerBlock;
+    for (int j = 0; j < kArgmaxPerThread; ++j) {
+        const int i = base + j * kArgmaxThreads + threadIdx.x;
+        if (i < n) better(bv, bi, x[i], i);
+    }
+    block_argmax(bv, bi);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = bv;
+        pi[blockIdx.x] = bi;
+    }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final(const float *pv, const int *pi, int nb, int *out) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int b = threadIdx.x; b < nb; b += kArgmaxThreads) better(bv, bi, pv[b], pi[b]);
+    block_argmax(bv, bi);
+    if (threadIdx.x == 0) *out = bi == 0x7fffffff ? 0 : bi;
+}
+
+struct Layer {
+    const float *in_ln = nullptr, *post_ln = nullptr;
+    const float *qb = nullptr, *kb = nullptr, *vb = nullptr, *qn = nullptr, *kn = nullptr;
+    const uint8_t *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    const uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+};
+
+struct Engine {
+    tqhip_model_config c{};
+    int q_dim = 0, kv_dim = 0, gs = 0, max_seq = 0, amax_blocks = 0;
+    float attn_scale = 0.0f;
+    const void *embed = nullptr;
+    bool embed_i4 = false;
+    const uint8_t *lm_head = nullptr;
+    const float *final_norm = nullptr;
+    std::vector<Layer> layers;
+    float *hidden = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr,
+          *o = nullptr, *gate = nullptr, *up = nullptr, *ffn = nullptr, *logits = nullptr, *kv = nullptr,
+          *amax_v = nullptr;
+    int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next
+    int *host_io = nullptr;                     // pinned mirror of dev_io
+    size_t layer_stride = 0;                    // floats per layer and plane: n_kv_heads * max_seq * head_dim
+    void *arena = nullptr;
+    hipStream_t stream = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int seq_len = 0;
+};
+
+int forward(Engine &e) {
+    hipStream_t s = e.stream;
+    const int H = e.c.hidden_size, I = e.c.intermediate_size;
+    int st = kOk;
+    if (e.embed_i4) {
+        st = launch_i4_embed_rows(static_cast<const uint8_t *>(e.embed), e.dev_io + 1, 1, H, e.gs, e.hidden, s);
+        if (st != kOk) return st;
+    } else {
+        embed_f32_row<<<(H + 255) / 256, 256, 0, s>>>(static_cast<const float *>(e.embed), e.dev_io + 1, e.hidden, H);
+    }
+    add_rmsnorm<<<1, kNormThreads, 0, s>>>(e.hidden, nullptr, e.layers[0].in_ln, e.normed, H, e.c.rms_norm_eps);
+    for (size_t li = 0; li < e.layers.size(); ++li) {
+        const Layer &L = e.layers[li];
+        float *kc = e.kv + (2 * li) * e.layer_stride, *vc = e.kv + (2 * li + 1) * e.layer_stride;
+        const uint8_t *w3[3] = {L.q, L.k, L.v};
+        float *y3[3] = {e.q, e.k, e.v};
+        const int d3[3] = {e.q_dim, e.kv_dim, e.kv_dim};
+        if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
+        qkv_finish<<<e.c.n_heads + e.c.n_kv_heads, 64, 0, s>>>(e.q, e.k, e.v, L.qb, L.kb, L.vb, L.qn, L.kn, kc, vc,
+                                                               e.dev_io, e.c.n_heads, e.c.head_dim, e.max_seq,
+                                                               e.c.rope_theta, e.c.rms_norm_eps);
+        attention_decode<<<e.c.n_heads, kAttnThreads, 0, s>>>(e.q, kc, vc, e.attn, e.dev_io,
+                                                              e.c.n_heads / e.c.n_kv_heads, e.c.head_dim, e.max_seq,
+                                                              e.attn_scale);
+        if ((st = launch_i4_matvec(L.o, e.attn, e.o, H, e.q_dim, e.gs, s)) != kOk) return st;
+        add_rmsnorm<<<1, kNormThreads, 0, s>>>(e.hidden, e.o, L.post_ln, e.normed, H, e.c.rms_norm_eps);
+        const uint8_t *w2[2] = {L.gate, L.up};
+        float *y2[2] = {e.gate, e.up};
+        const int d2[2] = {I, I};
+        if ((st = launch_i4_matvec_group(2, w2, y2, d2, e.normed, H, e.gs, s)) != kOk) return st;
+        swiglu<<<(I + 255) / 256, 256, 0, s>>>(e.gate, e.up, I);
+        if ((st = launch_i4_matvec(L.down, e.gate, e.ffn, H, I, e.gs, s)) != kOk) return st;
+        const float *next_ln = li + 1 < e.layers.size() ? e.layers[li + 1].in_ln : e.final_norm;
+        add_rmsnorm<<<1, kNormThreads, 0, s>>>(e.hidden, e.ffn, next_ln, e.normed, H, e.c.rms_norm_eps);
+    }
+    if ((st = launch_i4_matvec(e.lm_head, e.normed, e.logits, e.c.vocab_size, H, e.gs, s)) != kOk) return st;
+    argmax_partial<<<e.amax_blocks, kArgmaxThreads, 0, s>>>(e.logits, e.c.vocab_size, e.amax_v, e.amax_i);
+    argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, e.amax_blocks, e.dev_io + 2);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+void release(Engine *e) {
+    if (e->exec) (void)hipGraphExecDestroy(e->exec);
+    if (e->graph) (void)hipGraphDestroy(e->graph);
+    if (e->arena) (void)hipFree(e->arena);
+    if (e->host_io) (void)hipHostFree(e->host_io);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+}
+
+// Resolves a tensor of the model with the expected dtype and shape.
+struct Binder {
+    void *model;
+    std::string *err;
+    const void *get(const std::string &name, int dtype, uint64_t d0, uint64_t d1, bool optional = false) {
+        tqhip_tensor_info info;
+        if (tqhip_model_find(model, name.c_str(), &info) != kOk) {
+            if (!optional) *err = "gpu engine: missing tensor " + name;
+            return nullptr;
+        }
+        const bool shape_ok = d1 == 0 ? (info.ndim == 1 && info.shape[0] == d0)
+                                      : (info.ndim == 2 && info.shape[0] == d0 && info.shape[1] == d1);
+        if (info.dtype != dtype || !shape_ok) {
+            *err = "gpu engine: tensor " + name + " has an unexpected dtype or shape";
+            return nullptr;
+        }
+        return info.device;
+    }
+};
+
+int create(void *model, int max_seq_len, std::string *err, Engine **out) {
+    tqhip_model_config c;
+    if (tqhip_model_config_get(model, &c) != kOk) {
+        *err = "gpu engine: no model";
+        return kBadFile;
+    }
+    if (c.file_dtype != 3 || c.model_type != 0) {
+        *err = "gpu engine: serves dense (Qwen2 / Qwen3) i4 files only";
+        return kBadFile;
+    }
+    if (max_seq_len <= 0) max_seq_len = c.max_seq_len;
+    if (max_seq_len > c.max_seq_len) {
+        *err = "gpu engine: max_seq_len " + std::to_string(max_seq_len) + " exceeds the model limit " +
+               std::to_string(c.max_seq_len);
+        return kBadShape;
+    }
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) {
+        *err = "gpu engine: head_dim must be 64, 128 or 256";
+        return kBadShape;
+    }
+    if (c.hidden_size > kMaxHidden) {
+        *err = "gpu engine: hidden_size above " + std::to_string(kMaxHidden);
+        return kBadShape;
+    }
+    const int st = tqhip_model_upload(model);
+    if (st != kOk) {
+        *err = "gpu engine: weight upload failed";
+        return st;
+    }
+    Engine *e = new Engine;
+    e->c = c;
+    e->q_dim = c.n_heads * c.head_dim;
+    e->kv_dim = c.n_kv_heads * c.head_dim;
+    e->gs = c.quant_group_size;
+    e->max_seq = max_seq_len;
+    e->attn_scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
+    const uint64_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
+    Binder b{model, err};
+    bool ok = true;
+    auto vec = [&](const std::string &n, uint64_t d, bool opt = false) {
+        const float *p = static_cast<const float *>(b.get(n, 0, d, 0, opt));
+        if (!p && (!opt || !err->empty())) ok = false;
+        return p;
+    };
+    auto mat = [&](const std::string &n, uint64_t d0, uint64_t d1) {
+        const uint8_t *p = static_cast<const uint8_t *>(b.get(n, 3, d0, d1));
+        if (!p) ok = false;
+        return p;
+    };
+    tqhip_tensor_info emb;
+    if (tqhip_model_find(model, "model.embed_tokens.weight", &emb) != kOk) {
+        *err = "gpu engine: missing tensor model.embed_tokens.weight";
+        ok = false;
+    } else {
+        e->embed_i4 = emb.dtype == 3;
+        e->embed = b.get("model.embed_tokens.weight", e->embed_i4 ? 3 : 0, V, H);  // i4 or fp32 [vocab, hidden]
+        ok = e->embed != nullptr;
+    }
+    if (ok) e->final_norm = vec("model.norm.weight", H);
+    if (ok) {
+        tqhip_tensor_info lm;
+        if (tqhip_model_find(model, "lm_head.weight", &lm) == kOk) {
+            e->lm_head = mat("lm_head.weight", V, H);
+        } else if (c.tied_embeddings && e->embed_i4) {
+            e->lm_head = static_cast<const uint8_t *>(e->embed);
+        } else {
+            *err = c.tied_embeddings ? "gpu engine: a tied fp32 embedding needs an fp32 lm_head, which is not served"
+                                     : "gpu engine: missing tensor lm_head.weight";
+            ok = false;
+        }
+    }
+    e->layers.resize(c.n_layers);
+    for (int i = 0; ok && i < c.n_layers; ++i) {
+        const std::string p = "model.layers." + std::to_string(i) + ".";
+        Layer &L = e->layers[i];
+        L.in_ln = vec(p + "input_layernorm.weight", H);
+        L.post_ln = vec(p + "post_attention_layernorm.weight", H);
+        L.q = mat(p + "self_attn.q_proj.weight", e->q_dim, H);
+        L.k = mat(p + "self_attn.k_proj.weight", e->kv_dim, H);
+        L.v = mat(p + "self_attn.v_proj.weight", e->kv_dim, H);
+        L.o = mat(p + "self_attn.o_proj.weight", H, e->q_dim);
+        L.gate = mat(p + "mlp.gate_proj.weight", I, H);
+        L.up = mat(p + "mlp.up_proj.weight", I, H);
+        L.down = mat(p + "mlp.down_proj.weight", H, I);
+        if (!ok) break;
+        L.qb = vec(p + "self_attn.q_proj.bias", e->q_dim, true);
+        L.kb = vec(p + "self_attn.k_proj.bias", e->kv_dim, true);
+        L.vb = vec(p + "self_attn.v_proj.bias", e->kv_dim, true);
+        L.qn = vec(p + "self_attn.q_norm.weight", c.head_dim, true);
+        L.kn = vec(p + "self_attn.k_norm.weight", c.head_dim, true);
+        if (ok && (L.qn == nullptr) != (L.kn == nullptr)) {
+            *err = "gpu engine: layer " + std::to_string(i) + ": q_norm/k_norm must both be present or both absent";
+            ok = false;
+        }
+    }
+    if (!ok) {
+        release(e);
+        return kBadFile;
+    }
+
+    // One allocation: activations (each 256-byte aligned), the fp32 KV cache
+    // [layer][k|v][kv_head][max_seq][head_dim], the argmax partials.
+    e->layer_stride = static_cast<size_t>(c.n_kv_heads) * max_seq_len * c.head_dim;
+    e->amax_blocks = (c.vocab_size + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
+    const size_t counts[] = {H, H, static_cast<size_t>(e->q_dim), static_cast<size_t>(e->kv_dim),
+                             static_cast<size_t>(e->kv_dim), static_cast<size_t>(e->q_dim), H, I, I, H, V,
+                             2 * static_cast<size_t>(c.n_layers) * e->layer_stride,
+                             static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 4};
+    float **slots[] = {&e->hidden, &e->normed, &e->q, &e->k, &e->v, &e->attn, &e->o, &e->gate, &e->up, &e->ffn,
+                       &e->logits, &e->kv, &e->amax_v};
+    size_t offs[15], total = 0;
+    for (int i = 0; i < 15; ++i) {
+        offs[i] = total;
+        total += (counts[i] * 4 + 255) / 256 * 256;
+    }
+    if (hipMalloc(&e->arena, total) != hipSuccess || hipStreamCreate(&e->stream) != hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void **>(&e->host_io), 4 * sizeof(int)) != hipSuccess) {
+        *err = "gpu engine: HIP allocation failed";
+        release(e);
+        return kHipFailed;
+    }
+    uint8_t *base = static_cast<uint8_t *>(e->arena);
+    for (int i = 0; i < 13; ++i) *slots[i] = reinterpret_cast<float *>(base + offs[i]);
+    e->amax_i = reinterpret_cast<int *>(base + offs[13]);
+    e->dev_io = reinterpret_cast<int *>(base + offs[14]);
+    if (hipMemsetAsync(e->arena, 0, total, e->stream) != hipSuccess) {
+        *err = "gpu engine: HIP memset failed";
+        release(e);
+        return kHipFailed;
+    }
+    // One eager pass at position 0 with token 0 sets up the matvec launches'
+    // per-stream scratch outside the capture; its KV rows are rewritten by the
+    // first real step.
+    int rc = forward(*e);
+    if (rc == kOk && hipStreamSynchronize(e->stream) != hipSuccess) rc = kLaunchFailed;
+    if (rc == kOk && hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) rc = kLaunchFailed;
+    if (rc == kOk) {
+        const int fst = forward(*e);
+        const hipError_t end = hipStreamEndCapture(e->stream, &e->graph);
+        if (fst != kOk || end != hipSuccess) rc = fst != kOk ? fst : kLaunchFailed;
+    }
+    if (rc == kOk && hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0) != hipSuccess) rc = kLaunchFailed;
+    if (rc != kOk) {
+        *err = "gpu engine: setting up the step graph failed";
+        release(e);
+        return rc;
+    }
+    *out = e;
+    return kOk;
+}
+
+}  // namespace
+}  // namespace tqhip
+
+using namespace tqhip;
+
+extern "C" {
+
+int tqhip_decode_create(void *model, int max_seq_len, char *err, int err_len, void **engine) {
+    if (!engine) return kBadShape;
+    *engine = nullptr;
+    std::string msg;
+    Engine *e = nullptr;
+    const int rc = model ? create(model, max_seq_len, &msg, &e) : kBadFile;
+    if (rc != kOk) {
+        if (msg.empty()) msg = "gpu engine: no model";
+        if (err && err_len > 0) {
+            std::strncpy(err, msg.c_str(), err_len - 1);
+            err[err_len - 1] = 0;
+        }
+        return rc;
+    }
+    *engine = e;
+    return kOk;
+}
+
+int tqhip_decode_step(void *engine, int token_id) {
+    Engine *e = static_cast<Engine *>(engine);
+    if (!e || token_id < 0 || token_id >= e->c.vocab_size || e->seq_len >= e->max_seq) return kBadShape;
+    e->host_io[0] = e->seq_len;
+    e->host_io[1] = token_id;
+    if (hipMemcpyAsync(e->dev_io, e->host_io, 2 * sizeof(int), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+        hipGraphLaunch(e->exec, e->stream) != hipSuccess ||
+        hipMemcpyAsync(e->host_io + 2, e->dev_io + 2, sizeof(int), hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return kLaunchFailed;
+    e->seq_len += 1;
+    return e->host_io[2];
+}
+
+void tqhip_decode_reset(void *engine) {
+    if (engine) static_cast<Engine *>(engine)->seq_len = 0;
+}
+
+void tqhip_decode_destroy(void *engine) {
+    Engine *e = static_cast<Engine *>(engine);
+    if (!e) return;
+    (void)hipStreamSynchronize(e->stream);
+    release(e);
+}
+
+const float *tqhip_decode_logits(const void *engine) {
+    return engine ? static_cast<const Engine *>(engine)->logits : nullptr;
+}
+
+int tqhip_decode_seq_len(const void *engine) { return engine ? static_cast<const Engine *>(engine)->seq_len : -1; }
+
+}  // extern "C"

@@ -47,7 +47,9 @@ struct Tensor {
 };
 
 struct Model {
-    std::string path;
+    std::string path;                  // empty for an image in memory
+    const uint8_t *image = nullptr;    // the caller's copy of the whole file, or null
+    tqhip_model_config config{};
     uint64_t file_bytes = 0, data_offset = 0;
     uint32_t version = 0, dtype = 0, model_type = 0, quant_group_size = 0;
     std::vector<Tensor> tensors;  // file order
@@ -82,8 +84,19 @@ FILE *open_sized(const std::string &path, uint64_t *bytes, std::string *err) {
     return f;
 }
 
-bool read_at(FILE *f, uint64_t off, size_t n, uint8_t *dst, std::string *err) {
+// A file or a caller's in-memory image of one.
+struct Source {
+    FILE *f = nullptr;
+    const uint8_t *mem = nullptr;
+};
+
+bool read_at(const Source &src, uint64_t off, size_t n, uint8_t *dst, std::string *err) {
     if (n == 0) return true;
+    if (src.mem) {
+        std::memcpy(dst, src.mem + off, n);
+        return true;
+    }
+    FILE *f = src.f;
     if (std::fseek(f, static_cast<long>(off), SEEK_SET) != 0 || std::fread(dst, 1, n, f) != n)
         return fail(err, "short read");
     return true;
@@ -93,7 +106,7 @@ bool read_at(FILE *f, uint64_t off, size_t n, uint8_t *dst, std::string *err) {
 // order and with its messages (callers match on them), for header and tensor
 // fields at their tiny_format.h offsets.
 // Only the header and the tensor table are read: no check looks at tensor data.
-bool validate(Model &m, FILE *f, std::string *err) {
+bool validate(Model &m, const Source &f, std::string *err) {
     // stage 1: header
     if (m.file_bytes < kHeaderBytes) return fail(err, "file too small for header: " + m.path);
     std::vector<uint8_t> b(kHeaderBytes);
@@ -124,6 +137,10 @@ bool validate(Model &m, FILE *f, std::string *err) {
         return fail(err, "model config contains zero fields");
     if (n_heads % n_kv != 0) return fail(err, "n_heads % n_kv_heads != 0");
     if (eps <= 0.0f || theta <= 0.0f) return fail(err, "rms_norm_eps / rope_theta must be positive");
+    m.config = tqhip_model_config{static_cast<int>(n_layers), static_cast<int>(hidden), static_cast<int>(inter),
+                                  static_cast<int>(n_heads), static_cast<int>(n_kv), static_cast<int>(head_dim),
+                                  static_cast<int>(vocab), static_cast<int>(max_seq),
+                                  static_cast<int>(rd<uint32_t>(&b[48]) != 0), eps, theta, 0, 0, 0};
 
     // stage 2: tensor table
     std::vector<uint8_t> entries(count * kEntryBytes);
@@ -221,6 +238,9 @@ bool validate(Model &m, FILE *f, std::string *err) {
                 return fail(err, "tensor '" + t.name + "': i4 embed nbytes mismatch" + want_got(want, t.nbytes));
         }
     }
+    m.config.model_type = static_cast<int>(m.model_type);
+    m.config.quant_group_size = static_cast<int>(m.quant_group_size);
+    m.config.file_dtype = static_cast<int>(m.dtype);
     return true;
 }
 
@@ -256,7 +276,7 @@ int tqhip_model_inspect(const char *path, void **model, char *err, int err_len) 
     Model *m = new Model;
     m->path = path;
     FILE *f = open_sized(path, &m->file_bytes, &msg);
-    const bool ok = f && validate(*m, f, &msg);
+    const bool ok = f && validate(*m, Source{f, nullptr}, &msg);
     if (f) std::fclose(f);
     if (!ok) {
         copy_err(msg, err, err_len);
@@ -267,15 +287,47 @@ int tqhip_model_inspect(const char *path, void **model, char *err, int err_len) 
     return kOk;
 }
 
+int tqhip_model_inspect_memory(const void *image, uint64_t bytes, void **model, char *err, int err_len) {
+    if (!image || !model) return kBadFile;
+    *model = nullptr;
+    std::string msg;
+    Model *m = new Model;
+    m->image = static_cast<const uint8_t *>(image);
+    m->file_bytes = bytes;
+    if (!validate(*m, Source{nullptr, m->image}, &msg)) {
+        copy_err(msg, err, err_len);
+        delete m;
+        return kBadFile;
+    }
+    *model = m;
+    return kOk;
+}
+
+int tqhip_model_config_get(const void *model, tqhip_model_config *out) {
+    if (!model || !out) return kBadShape;
+    *out = static_cast<const Model *>(model)->config;
+    return kOk;
+}
+
 int tqhip_model_upload(void *model) {
     Model *m = static_cast<Model *>(model);
     if (!m) return kBadShape;
     if (m->device) return kOk;
+    const size_t n = m->file_bytes - m->data_offset;
+    if (m->image) {
+        void *dev = nullptr;
+        if (n > 0 && hipMalloc(&dev, n) != hipSuccess) return kHipFailed;
+        if (n > 0 && hipMemcpy(dev, m->image + m->data_offset, n, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipFree(dev);
+            return kHipFailed;
+        }
+        m->device = dev;
+        return kOk;
+    }
     std::string msg;
     uint64_t bytes = 0;
     FILE *f = open_sized(m->path, &bytes, &msg);
     if (!f) return kBadFile;
-    const size_t n = m->file_bytes - m->data_offset;
     int rc = bytes == m->file_bytes ? kOk : kBadFile;  // the file changed since it was inspected
     void *dev = nullptr;
     if (rc == kOk && n > 0 && hipMalloc(&dev, n) != hipSuccess) rc = kHipFailed;
@@ -284,7 +336,7 @@ int tqhip_model_upload(void *model) {
     std::vector<uint8_t> chunk(std::min<size_t>(n, kUploadChunk));
     for (size_t done = 0; rc == kOk && done < n;) {
         const size_t len = std::min(chunk.size(), n - done);
-        if (!read_at(f, m->data_offset + done, len, chunk.data(), &msg)) rc = kBadFile;
+        if (!read_at(Source{f, nullptr}, m->data_offset + done, len, chunk.data(), &msg)) rc = kBadFile;
         else if (hipMemcpy(static_cast<uint8_t *>(dev) + done, chunk.data(), len, hipMemcpyHostToDevice) != hipSuccess)
             rc = kHipFailed;
         done += len;
