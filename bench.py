@@ -35,6 +35,11 @@ Printed (one JSON line on stdout):
                rotated copies, us and GB/s
   host_call    the reference-signature host-pointer entry point (x H2D,
                kernel, y D2H; weights cached in HBM), PCIe-inclusive us
+  engine       the device-resident decode engine (tqhip_decode_*) on a
+               Qwen2.5-0.5B-shaped dense i4 HQQ@64 model (24 layers, 14/2 heads,
+               tied i4 embedding, q/k/v biases, random weights): ms per token
+               and tokens/s of step() (one graph replay, token in and next
+               token out), over --steps tokens after --warmup tokens
   cpu_baseline the compiled reference's `ref` matvec (oracle/_ref, tiny-llm's
                kernels/matvec/matvec_i4_ref.cpp built unmodified), row-split
                over host threads, on the same step; the C++ restatement is
@@ -327,6 +332,51 @@ def host_call(tq, reps=50):
     return rows
 
 
+def engine(tq, steps, warmup):
+    """Decode engine tokens/s on a synthetic Qwen2.5-0.5B-shaped dense i4 model held in memory."""
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
+    import tqwen_files
+    img, cfg, _ = tqwen_files.dense_i4_model(hidden=HIDDEN, n_heads=14, n_kv_heads=2, head_dim=64, inter=INTER,
+                                             vocab=VOCAB, layers=N_LAYERS, group_size=G, seed=11,
+                                             max_seq_len=4096)
+    m = tq.ModelFile.from_image(img)
+    t0 = time.perf_counter()
+    m.upload()
+    upload_s = time.perf_counter() - t0
+    eng = tq.DecodeEngine(m, warmup + steps + 1)
+    tok = 1
+    for _ in range(warmup):
+        tok = eng.step(tok)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = eng.step(tok)
+    dt = (time.perf_counter() - t0) / steps
+    eng.close()
+    m.close()
+    cpu = None
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
+    ref = oracle.ref_lib()
+    if ref is not None:  # the reference's own CPU decode (QwenModel::forward_token, `ref` kernels) on the same file
+        import tempfile
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "bench.tqwen")
+            with open(path, "wb") as f:
+                f.write(img)
+            err = ctypes.create_string_buffer(512)
+            if ref.tqref_decode_create(path.encode(), 16, err, len(err)):
+                ref.tqref_decode_step(1)
+                n, t0 = 3, time.perf_counter()
+                for t in range(n):
+                    ref.tqref_decode_step(t + 2)
+                cpu = {"ms_per_token": round((time.perf_counter() - t0) / n * 1e3, 1), "tokens": n, "cores": 1,
+                       "kind": "reference"}
+    return {"model": "Qwen2.5-0.5B-shaped dense i4 HQQ@64 (24 layers, hidden 896, 14/2 heads, inter 4864, "
+                     "vocab 151936, tied i4 embedding), random weights",
+            "file_bytes": len(img), "upload_s": round(upload_s, 3), "positions": f"{warmup}..{warmup + steps - 1}",
+            "ms_per_token": round(dt * 1e3, 4), "tokens_per_s": round(1.0 / dt, 1), "cpu_reference": cpu}
+
+
 def cpu_baseline(work, budget_s=12.0):
     """The reference's ref matvec (or the restatement) over the same step, row-split across threads."""
     sys.path.insert(0, REPO)
@@ -390,6 +440,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill dequant-GEMM timings")
     ap.add_argument("--no-host-call", action="store_true", help="skip the host-pointer (PCIe-inclusive) timing")
     ap.add_argument("--no-vq2", action="store_true", help="skip the VQ2 matvec timings")
+    ap.add_argument("--no-engine", action="store_true", help="skip the device-resident decode engine timing")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
     ap.add_argument("--no-configs2", action="store_true", help="skip the configs[2] gate/up, down and attention matvecs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
@@ -458,6 +509,11 @@ def main():
         log(f"[bench] host-pointer call (x H2D + kernel + y D2H, weights cached): " +
             ", ".join(f"{r['shape']} {r['us']} us" for r in host))
 
+    eng = None if args.no_engine else engine(tq, args.steps, args.warmup)
+    if eng:
+        log(f"[bench] decode engine: {eng['ms_per_token']} ms/token, {eng['tokens_per_s']} tokens/s "
+            f"(positions {eng['positions']})")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(work)
@@ -483,6 +539,7 @@ def main():
         "prefill": pre,
         "vq2": v,
         "host_call": host,
+        "engine": eng,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -505,6 +505,20 @@ class ModelFile:
 
     load = classmethod(lambda cls, path: cls(path))
 
+    @classmethod
+    def from_image(cls, image) -> "ModelFile":
+        """A whole .tqwen file held in memory (bytes / bytearray / uint8 array); kept alive by the object."""
+        buf = np.frombuffer(image, np.uint8)
+        handle = _vp()
+        err = ctypes.create_string_buffer(512)
+        rc = lib().tqhip_model_inspect_memory(buf.ctypes.data, buf.size, ctypes.byref(handle), err, len(err))
+        if rc != OK:
+            raise ValueError(err.value.decode(errors="replace") or f"tqhip_model_inspect_memory failed ({rc})")
+        obj = cls.__new__(cls)
+        obj._h = handle.value
+        obj._image = buf
+        return obj
+
     def upload(self) -> None:
         _check(lib().tqhip_model_upload(self._h), "tqhip_model_upload")
 

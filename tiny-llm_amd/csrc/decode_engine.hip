@@ -15,8 +15,8 @@
 // positions 0..pos, o matvec, residual, RMSNorm, fused gate/up matvec, SwiGLU,
 // down matvec, residual, final RMSNorm, lm_head matvec, argmax. The small
 // kernels below fuse the elementwise work between the matvecs: residual add
-// with the following RMSNorm, and biases, q/k norm, RoPE and the KV write in one
-// launch.
+// with the following RMSNorm, and biases, q/k norm, RoPE, the KV write and the
+// attention in one launch.
 
 #include "../../include/tqhip.h"
 
@@ -24,6 +24,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -106,86 +107,115 @@ __global__ void embed_f32_row(const float *table, const int *token, float *out, 
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = table[base + i];
 }
 
-// One wave per head: blocks [0, n_heads) finish q heads, the rest k heads and
-// write k and v into the cache at `*pos`. Biases (qb/kb/vb may be null), then
-// the per-head RMSNorm when qn/kn are given, then RoPE (rope_ref,
-// kernels/rope/rope_ref.cpp: pairs (i, i + half), inv_freq = theta^(-2i/d)).
-__global__ __launch_bounds__(64) void qkv_finish(float *q, float *k, const float *v, const float *qb,
-                                                 const float *kb, const float *vb, const float *qn,
-                                                 const float *kn, float *kcache, float *vcache, const int *pos_ptr,
-                                                 int n_heads, int hd, int max_seq, float theta, float eps) {
-    __shared__ float xs[256];
-    const int t = threadIdx.x;
-    const bool is_q = static_cast<int>(blockIdx.x) < n_heads;
-    const int head = is_q ? blockIdx.x : blockIdx.x - n_heads;
-    float *x = (is_q ? q : k) + head * hd;
-    const float *b = is_q ? qb : kb;
-    const float *nw = is_q ? qn : kn;
-    const int pos = *pos_ptr;
-    for (int i = t; i < hd; i += 64) xs[i] = b ? x[i] + b[head * hd + i] : x[i];
-    __syncthreads();
-    if (nw) {
-        double ss = 0.0;
-        for (int i = t; i < hd; i += 64) ss += static_cast<double>(xs[i]) * static_cast<double>(xs[i]);
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        const float scale = 1.0f / sqrtf(static_cast<float>(ss / hd) + eps);
-        __syncthreads();
-        for (int i = t; i < hd; i += 64) xs[i] = (xs[i] * scale) * nw[i];
-        __syncthreads();
-    }
+// RoPE of the q and k heads held in LDS (rope_ref, kernels/rope/rope_ref.cpp:
+// pairs (i, i + half), inv_freq = theta^(-2i/d), angle = pos * inv_freq; the
+// same cos / sin for both heads).
+__device__ void rope2_lds(float *qx, float *kx, int hd, int pos, float theta) {
     const int half = hd / 2;
-    float *kc = is_q ? nullptr : kcache + (static_cast<size_t>(head) * max_seq + pos) * hd;
-    for (int i = t; i < half; i += 64) {
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
         const float inv_freq = powf(theta, -static_cast<float>(2 * i) / static_cast<float>(hd));
         const float angle = static_cast<float>(pos) * inv_freq;
         const float c = cosf(angle), s = sinf(angle);
-        const float x0 = xs[i], x1 = xs[i + half];
-        const float r0 = x0 * c - x1 * s;
-        const float r1 = x1 * c + x0 * s;
-        x[i] = r0;
-        x[i + half] = r1;
-        if (kc) {
-            kc[i] = r0;
-            kc[i + half] = r1;
+        float *xs[2] = {qx, kx};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float *x = xs[h];
+            const float x0 = x[i], x1 = x[i + half];
+            const float r0 = x0 * c - x1 * s;
+            const float r1 = x1 * c + x0 * s;
+            x[i] = r0;
+            x[i + half] = r1;
         }
-    }
-    if (!is_q) {
-        float *vc = vcache + (static_cast<size_t>(head) * max_seq + pos) * hd;
-        for (int i = t; i < hd; i += 64) vc[i] = vb ? v[head * hd + i] + vb[head * hd + i] : v[head * hd + i];
     }
 }
 
-// One workgroup per query head over positions 0..*pos of its KV head
-// (attention_decode_ref, kernels/attention/attention_decode_ref.cpp: scores
-// q.k * scale, softmax, sum of p * v). Positions go in chunks; within a chunk
-// the scores sit in LDS and the softmax is max / exp / sum, across chunks the
-// running max rescales the partial sums. Thread t accumulates dimension
-// t % hd over every (NT / hd)-th position of a chunk.
-__global__ __launch_bounds__(kAttnThreads) void attention_decode(const float *q, const float *kcache,
-                                                                 const float *vcache, float *out, const int *pos_ptr,
-                                                                 int heads_per_kv, int hd, int max_seq, float scale) {
-    __shared__ float qs[256];
+// 1 / rms of one head in LDS (rmsnorm_ref on a head slice), summed by one wave.
+__device__ float head_rms_scale(const float *x, int hd, float eps) {
+    const int lane = threadIdx.x & 63;
+    double ss = 0.0;
+    for (int i = lane; i < hd; i += 64) ss += static_cast<double>(x[i]) * static_cast<double>(x[i]);
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    return 1.0f / sqrtf(static_cast<float>(ss / hd) + eps);
+}
+
+// One workgroup per query head: finishes its q head and the k / v head of its
+// group from the raw projections (biases, optional per-head RMSNorm for q and
+// k, RoPE), writes k and v at `*pos` into the cache (the group's first head
+// only), then attends over positions 0..pos (attention_decode_ref,
+// kernels/attention/attention_decode_ref.cpp: scores q.k * scale, softmax, sum
+// of p * v). Every head of a group computes the new k / v itself and uses its
+// own copy at position pos, so no head reads a cache row another workgroup is
+// writing. Thread j scores position j of a chunk of up to 4096 positions (its
+// whole key row in float4 loads); the softmax over a chunk is max / exp / sum,
+// and across chunks the running max rescales the partial sums. Thread t then
+// accumulates dimension t % hd over every (NT / hd)-th position.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_step(
+    const float *q, const float *k, const float *v, const float *qb, const float *kb, const float *vb,
+    const float *qn, const float *kn, float *kcache, float *vcache, float *out, const int *pos_ptr, int heads_per_kv,
+    int max_seq, float theta, float eps, float scale) {
+    constexpr int hd = HD;
+    __shared__ __align__(16) float qs[256];
+    __shared__ __align__(16) float ks[256];
+    __shared__ float vs[256];
     __shared__ float sc[kAttnChunk];
     __shared__ float part[kAttnThreads];
+    __shared__ float norm_scale[2];
     __shared__ double dred[kAttnThreads / 64];
     __shared__ float fred[kAttnThreads / 64];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x;
     const int head = blockIdx.x, kvh = head / heads_per_kv;
-    const int seq = *pos_ptr + 1;
+    const int pos = *pos_ptr, seq = pos + 1;
+    for (int i = t; i < hd; i += kAttnThreads) {
+        const int qi = head * hd + i, ki = kvh * hd + i;
+        qs[i] = qb ? q[qi] + qb[qi] : q[qi];
+        ks[i] = kb ? k[ki] + kb[ki] : k[ki];
+        vs[i] = vb ? v[ki] + vb[ki] : v[ki];
+    }
+    __syncthreads();
+    if (qn) {
+        const int wave = t >> 6;
+        if (wave < 2) {
+            const float s0 = head_rms_scale(wave == 0 ? qs : ks, hd, eps);
+            if ((t & 63) == 0) norm_scale[wave] = s0;
+        }
+        __syncthreads();
+        for (int i = t; i < hd; i += kAttnThreads) {
+            qs[i] = (qs[i] * norm_scale[0]) * qn[i];
+            ks[i] = (ks[i] * norm_scale[1]) * kn[i];
+        }
+        __syncthreads();
+    }
+    rope2_lds(qs, ks, hd, pos, theta);
+    __syncthreads();
     const float *kh = kcache + static_cast<size_t>(kvh) * max_seq * hd;
     const float *vh = vcache + static_cast<size_t>(kvh) * max_seq * hd;
-    for (int i = t; i < hd; i += kAttnThreads) qs[i] = q[head * hd + i];
-    __syncthreads();
+    if (head % heads_per_kv == 0) {
+        float *kw = kcache + (static_cast<size_t>(kvh) * max_seq + pos) * hd;
+        float *vw = vcache + (static_cast<size_t>(kvh) * max_seq + pos) * hd;
+        for (int i = t; i < hd; i += kAttnThreads) {
+            kw[i] = ks[i];
+            vw[i] = vs[i];
+        }
+    }
     const int slices = kAttnThreads / hd, d = t % hd, slice = t / hd;
     float m = -INFINITY, l = 0.0f, acc = 0.0f;
     for (int c0 = 0; c0 < seq; c0 += kAttnChunk) {
         const int len = min(kAttnChunk, seq - c0);
-        for (int j = wave; j < len; j += kAttnThreads / 64) {
-            const float *kr = kh + static_cast<size_t>(c0 + j) * hd;
+        for (int j = t; j < len; j += kAttnThreads) {
+            const int p = c0 + j;
+            const float4 *kr = reinterpret_cast<const float4 *>(p == pos ? ks : kh + static_cast<size_t>(p) * hd);
+            const float4 *q4 = reinterpret_cast<const float4 *>(qs);
             float dot = 0.0f;
-            for (int i = lane; i < hd; i += 64) dot += qs[i] * kr[i];
-            for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
-            if (lane == 0) sc[j] = dot * scale;
+#pragma unroll
+            for (int i = 0; i < hd / 4; ++i) {
+                const float4 a = q4[i], b = kr[i];
+                dot += a.x * b.x;
+                dot += a.y * b.y;
+                dot += a.z * b.z;
+                dot += a.w * b.w;
+            }
+            sc[j] = dot * scale;
         }
         __syncthreads();
         float cmax = -INFINITY;
@@ -202,7 +232,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode(const float *q,
         const float rescale = expf(m - m_new);
         l = l * rescale + static_cast<float>(csum);
         acc = acc * rescale;
-        for (int j = slice; j < len; j += slices) acc += sc[j] * vh[static_cast<size_t>(c0 + j) * hd + d];
+        // Eight positions' loads issued together, then added in position order.
+        int j = slice;
+        for (; j + 7 * slices < len; j += 8 * slices) {
+            float vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int p = c0 + j + u * slices;
+                vv[u] = p == pos ? vs[d] : vh[static_cast<size_t>(p) * hd + d];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += sc[j + u * slices] * vv[u];
+        }
+        for (; j < len; j += slices) {
+            const int p = c0 + j;
+            acc += sc[j] * (p == pos ? vs[d] : vh[static_cast<size_t>(p) * hd + d]);
+        }
         m = m_new;
         __syncthreads();
     }
@@ -210,7 +255,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode(const float *q,
     __syncthreads();
     if (slice == 0) {
         float o = part[d];
-        for (int s = 1; s < slices; ++s) o += part[s * hd + d];
+        for (int s2 = 1; s2 < slices; ++s2) o += part[s2 * hd + d];
         out[head * hd + d] = o * (1.0f / l);
     }
 }
@@ -298,6 +343,7 @@ struct Engine {
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    bool eager = false;  // TQHIP_DECODE_EAGER=1: launch the step kernel by kernel (for profilers)
     int seq_len = 0;
 };
 
@@ -319,12 +365,11 @@ int forward(Engine &e) {
         float *y3[3] = {e.q, e.k, e.v};
         const int d3[3] = {e.q_dim, e.kv_dim, e.kv_dim};
         if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
-        qkv_finish<<<e.c.n_heads + e.c.n_kv_heads, 64, 0, s>>>(e.q, e.k, e.v, L.qb, L.kb, L.vb, L.qn, L.kn, kc, vc,
-                                                               e.dev_io, e.c.n_heads, e.c.head_dim, e.max_seq,
-                                                               e.c.rope_theta, e.c.rms_norm_eps);
-        attention_decode<<<e.c.n_heads, kAttnThreads, 0, s>>>(e.q, kc, vc, e.attn, e.dev_io,
-                                                              e.c.n_heads / e.c.n_kv_heads, e.c.head_dim, e.max_seq,
-                                                              e.attn_scale);
+        auto attn = e.c.head_dim == 64 ? attention_step<64> : e.c.head_dim == 128 ? attention_step<128>
+                                                                                  : attention_step<256>;
+        attn<<<e.c.n_heads, kAttnThreads, 0, s>>>(e.q, e.k, e.v, L.qb, L.kb, L.vb, L.qn, L.kn, kc, vc, e.attn,
+                                                  e.dev_io, e.c.n_heads / e.c.n_kv_heads, e.max_seq, e.c.rope_theta,
+                                                  e.c.rms_norm_eps, e.attn_scale);
         if ((st = launch_i4_matvec(L.o, e.attn, e.o, H, e.q_dim, e.gs, s)) != kOk) return st;
         add_rmsnorm<<<1, kNormThreads, 0, s>>>(e.hidden, e.o, L.post_ln, e.normed, H, e.c.rms_norm_eps);
         const uint8_t *w2[2] = {L.gate, L.up};
@@ -506,13 +551,17 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     // first real step.
     int rc = forward(*e);
     if (rc == kOk && hipStreamSynchronize(e->stream) != hipSuccess) rc = kLaunchFailed;
-    if (rc == kOk && hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) rc = kLaunchFailed;
-    if (rc == kOk) {
+    const char *eager = std::getenv("TQHIP_DECODE_EAGER");
+    e->eager = eager && eager[0] == '1';
+    if (rc == kOk && !e->eager && hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+        rc = kLaunchFailed;
+    if (rc == kOk && !e->eager) {
         const int fst = forward(*e);
         const hipError_t end = hipStreamEndCapture(e->stream, &e->graph);
         if (fst != kOk || end != hipSuccess) rc = fst != kOk ? fst : kLaunchFailed;
     }
-    if (rc == kOk && hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0) != hipSuccess) rc = kLaunchFailed;
+    if (rc == kOk && !e->eager && hipGraphInstantiate(&e->exec, e->graph, nullptr, nullptr, 0) != hipSuccess)
+        rc = kLaunchFailed;
     if (rc != kOk) {
         *err = "gpu engine: setting up the step graph failed";
         release(e);
@@ -553,7 +602,7 @@ int tqhip_decode_step(void *engine, int token_id) {
     e->host_io[0] = e->seq_len;
     e->host_io[1] = token_id;
     if (hipMemcpyAsync(e->dev_io, e->host_io, 2 * sizeof(int), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
-        hipGraphLaunch(e->exec, e->stream) != hipSuccess ||
+        (e->eager ? forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) ||
         hipMemcpyAsync(e->host_io + 2, e->dev_io + 2, sizeof(int), hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
         hipStreamSynchronize(e->stream) != hipSuccess)
         return kLaunchFailed;
