@@ -107,28 +107,6 @@ __global__ void embed_f32_row(const float *table, const int *token, float *out, 
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = table[base + i];
 }
 
-// RoPE of the q and k heads held in LDS (rope_ref, kernels/rope/rope_ref.cpp:
-// pairs (i, i + half), inv_freq = theta^(-2i/d), angle = pos * inv_freq; the
-// same cos / sin for both heads).
-__device__ void rope2_lds(float *qx, float *kx, int hd, int pos, float theta) {
-    const int half = hd / 2;
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const float inv_freq = powf(theta, -static_cast<float>(2 * i) / static_cast<float>(hd));
-        const float angle = static_cast<float>(pos) * inv_freq;
-        const float c = cosf(angle), s = sinf(angle);
-        float *xs[2] = {qx, kx};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float *x = xs[h];
-            const float x0 = x[i], x1 = x[i + half];
-            const float r0 = x0 * c - x1 * s;
-            const float r1 = x1 * c + x0 * s;
-            x[i] = r0;
-            x[i + half] = r1;
-        }
-    }
-}
-
 // 1 / rms of one head in LDS (rmsnorm_ref on a head slice), summed by one wave.
 __device__ float head_rms_scale(const float *x, int hd, float eps) {
     const int lane = threadIdx.x & 63;
@@ -140,24 +118,32 @@ __device__ float head_rms_scale(const float *x, int hd, float eps) {
 
 // One workgroup per query head: finishes its q head and the k / v head of its
 // group from the raw projections (biases, optional per-head RMSNorm for q and
-// k, RoPE), writes k and v at `*pos` into the cache (the group's first head
-// only), then attends over positions 0..pos (attention_decode_ref,
-// kernels/attention/attention_decode_ref.cpp: scores q.k * scale, softmax, sum
-// of p * v). Every head of a group computes the new k / v itself and uses its
-// own copy at position pos, so no head reads a cache row another workgroup is
-// writing. Thread j scores position j of a chunk of up to 4096 positions (its
-// whole key row in float4 loads); the softmax over a chunk is max / exp / sum,
-// and across chunks the running max rescales the partial sums. Thread t then
-// accumulates dimension t % hd over every (NT / hd)-th position.
+// k, RoPE as rope_ref, kernels/rope/rope_ref.cpp: pairs (i, i + half),
+// inv_freq = theta^(-2i/d), angle = pos * inv_freq), writes k and v at `*pos`
+// into the cache (the group's first head only), then attends over positions
+// 0..pos (attention_decode_ref, kernels/attention/attention_decode_ref.cpp:
+// scores q.k * scale, softmax, sum of p * v). Every head of a group computes
+// the new k / v itself and uses its own copy at position pos, so no head reads
+// a cache row another workgroup is writing.
+//
+// Latency is the cost here (14 workgroups at Qwen2.5-0.5B), so the memory
+// round trips are overlapped: the q / k / v loads, thread t's key row for
+// position t (head_dim <= 128) and the first eight value rows of its slice are
+// all issued at entry, and the RoPE angles are computed while they are in
+// flight. Thread j scores position j of a chunk of up to 4096 positions; the
+// softmax over a chunk is max / exp / sum, and across chunks the running max
+// rescales the partial sums. Thread t accumulates dimension t % hd over every
+// (NT / hd)-th position, in position order.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_step(
     const float *q, const float *k, const float *v, const float *qb, const float *kb, const float *vb,
     const float *qn, const float *kn, float *kcache, float *vcache, float *out, const int *pos_ptr, int heads_per_kv,
     int max_seq, float theta, float eps, float scale) {
-    constexpr int hd = HD;
-    __shared__ __align__(16) float qs[256];
-    __shared__ __align__(16) float ks[256];
-    __shared__ float vs[256];
+    constexpr int hd = HD, half = HD / 2, slices = kAttnThreads / HD;
+    constexpr bool kPrefetchKey = HD <= 128;
+    __shared__ __align__(16) float qs[HD];
+    __shared__ __align__(16) float ks[HD];
+    __shared__ float vs[HD];
     __shared__ float sc[kAttnChunk];
     __shared__ float part[kAttnThreads];
     __shared__ float norm_scale[2];
@@ -166,11 +152,43 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step(
     const int t = threadIdx.x;
     const int head = blockIdx.x, kvh = head / heads_per_kv;
     const int pos = *pos_ptr, seq = pos + 1;
-    for (int i = t; i < hd; i += kAttnThreads) {
-        const int qi = head * hd + i, ki = kvh * hd + i;
-        qs[i] = qb ? q[qi] + qb[qi] : q[qi];
-        ks[i] = kb ? k[ki] + kb[ki] : k[ki];
-        vs[i] = vb ? v[ki] + vb[ki] : v[ki];
+    const int d = t % hd, slice = t / hd;
+    const float *kh = kcache + static_cast<size_t>(kvh) * max_seq * hd;
+    const float *vh = vcache + static_cast<size_t>(kvh) * max_seq * hd;
+
+    float qv = 0.0f, kv = 0.0f, vv = 0.0f;
+    if (t < hd) {
+        const int qi = head * hd + t, ki = kvh * hd + t;
+        qv = qb ? q[qi] + qb[qi] : q[qi];
+        kv = kb ? k[ki] + kb[ki] : k[ki];
+        vv = vb ? v[ki] + vb[ki] : v[ki];
+    }
+    float4 kreg[kPrefetchKey ? HD / 4 : 1];
+    const bool key_pre = kPrefetchKey && t < seq && t != pos && t < kAttnChunk;
+    if constexpr (kPrefetchKey) {
+        if (key_pre) {
+            const float4 *kr = reinterpret_cast<const float4 *>(kh + static_cast<size_t>(t) * hd);
+#pragma unroll
+            for (int i = 0; i < HD / 4; ++i) kreg[i] = kr[i];
+        }
+    }
+    float vreg[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int p = slice + u * slices;
+        vreg[u] = p < seq && p != pos ? vh[static_cast<size_t>(p) * hd + d] : 0.0f;
+    }
+    float c = 0.0f, s = 0.0f;
+    if (t < half) {
+        const float inv_freq = powf(theta, -static_cast<float>(2 * t) / static_cast<float>(hd));
+        const float angle = static_cast<float>(pos) * inv_freq;
+        c = cosf(angle);
+        s = sinf(angle);
+    }
+    if (t < hd) {
+        qs[t] = qv;
+        ks[t] = kv;
+        vs[t] = vv;
     }
     __syncthreads();
     if (qn) {
@@ -180,40 +198,56 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step(
             if ((t & 63) == 0) norm_scale[wave] = s0;
         }
         __syncthreads();
-        for (int i = t; i < hd; i += kAttnThreads) {
-            qs[i] = (qs[i] * norm_scale[0]) * qn[i];
-            ks[i] = (ks[i] * norm_scale[1]) * kn[i];
+        if (t < hd) {
+            qs[t] = (qs[t] * norm_scale[0]) * qn[t];
+            ks[t] = (ks[t] * norm_scale[1]) * kn[t];
         }
         __syncthreads();
     }
-    rope2_lds(qs, ks, hd, pos, theta);
-    __syncthreads();
-    const float *kh = kcache + static_cast<size_t>(kvh) * max_seq * hd;
-    const float *vh = vcache + static_cast<size_t>(kvh) * max_seq * hd;
-    if (head % heads_per_kv == 0) {
-        float *kw = kcache + (static_cast<size_t>(kvh) * max_seq + pos) * hd;
-        float *vw = vcache + (static_cast<size_t>(kvh) * max_seq + pos) * hd;
-        for (int i = t; i < hd; i += kAttnThreads) {
-            kw[i] = ks[i];
-            vw[i] = vs[i];
+    if (t < half) {
+        float *xs[2] = {qs, ks};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            float *x = xs[h];
+            const float x0 = x[t], x1 = x[t + half];
+            const float r0 = x0 * c - x1 * s;
+            const float r1 = x1 * c + x0 * s;
+            x[t] = r0;
+            x[t + half] = r1;
         }
     }
-    const int slices = kAttnThreads / hd, d = t % hd, slice = t / hd;
+    __syncthreads();
+    if (head % heads_per_kv == 0 && t < hd) {
+        kcache[(static_cast<size_t>(kvh) * max_seq + pos) * hd + t] = ks[t];
+        vcache[(static_cast<size_t>(kvh) * max_seq + pos) * hd + t] = vs[t];
+    }
+
     float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    const float4 *q4 = reinterpret_cast<const float4 *>(qs);
     for (int c0 = 0; c0 < seq; c0 += kAttnChunk) {
         const int len = min(kAttnChunk, seq - c0);
         for (int j = t; j < len; j += kAttnThreads) {
             const int p = c0 + j;
-            const float4 *kr = reinterpret_cast<const float4 *>(p == pos ? ks : kh + static_cast<size_t>(p) * hd);
-            const float4 *q4 = reinterpret_cast<const float4 *>(qs);
             float dot = 0.0f;
+            if (kPrefetchKey && p == t && key_pre) {
 #pragma unroll
-            for (int i = 0; i < hd / 4; ++i) {
-                const float4 a = q4[i], b = kr[i];
-                dot += a.x * b.x;
-                dot += a.y * b.y;
-                dot += a.z * b.z;
-                dot += a.w * b.w;
+                for (int i = 0; i < HD / 4; ++i) {
+                    const float4 a = q4[i], b = kreg[kPrefetchKey ? i : 0];
+                    dot += a.x * b.x;
+                    dot += a.y * b.y;
+                    dot += a.z * b.z;
+                    dot += a.w * b.w;
+                }
+            } else {
+                const float4 *kr = reinterpret_cast<const float4 *>(p == pos ? ks : kh + static_cast<size_t>(p) * hd);
+#pragma unroll
+                for (int i = 0; i < HD / 4; ++i) {
+                    const float4 a = q4[i], b = kr[i];
+                    dot += a.x * b.x;
+                    dot += a.y * b.y;
+                    dot += a.z * b.z;
+                    dot += a.w * b.w;
+                }
             }
             sc[j] = dot * scale;
         }
@@ -232,17 +266,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step(
         const float rescale = expf(m - m_new);
         l = l * rescale + static_cast<float>(csum);
         acc = acc * rescale;
-        // Eight positions' loads issued together, then added in position order.
         int j = slice;
+        if (c0 == 0) {  // the first eight positions of the slice, loaded at entry
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int jj = slice + u * slices;
+                if (jj < len) acc += sc[jj] * (jj == pos ? vs[d] : vreg[u]);
+            }
+            j = slice + 8 * slices;
+        }
+        // Eight positions' loads issued together, then added in position order.
         for (; j + 7 * slices < len; j += 8 * slices) {
-            float vv[8];
+            float vb8[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int p = c0 + j + u * slices;
-                vv[u] = p == pos ? vs[d] : vh[static_cast<size_t>(p) * hd + d];
+                vb8[u] = p == pos ? vs[d] : vh[static_cast<size_t>(p) * hd + d];
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc += sc[j + u * slices] * vv[u];
+            for (int u = 0; u < 8; ++u) acc += sc[j + u * slices] * vb8[u];
         }
         for (; j < len; j += slices) {
             const int p = c0 + j;
