@@ -7,7 +7,8 @@ Qwen2.x / Qwen3 model as QwenModel::forward_token runs it
   embedding row      dequant_i4_row (kernels/ref_ops.h:183-205) or the fp32 row
   rmsnorm            kernels/rmsnorm/rmsnorm_ref.cpp:14-30
   q/k/v, o, gate/up, down, lm_head projections
-                     matvec_i4 (the C restatement in oracle.cpp)
+                     matvec_i4 / matvec_vq2 by the tensor's dtype (the C restatement
+                     in oracle.cpp); fp16 vectors of VQ2 files converted once
   biases, q/k norm   runtime/qwen_forward_token.cpp:338-372
   rope               kernels/rope/rope_ref.cpp:13-56
   KV write           runtime/kv_cache.h:118-129 ([layer][kv_head][max_seq][head_dim])
@@ -24,9 +25,9 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import dequant_i4_row, matvec_i4
+from . import dequant_i4_row, halves_to_floats, matvec_i4, matvec_vq2
 
-F32, I4 = 0, 3
+F32, F16, I4, VQ2 = 0, 1, 3, 4
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
@@ -109,11 +110,18 @@ class DenseDecoder:
     def _vec(self, name):
         if name not in self.t:
             return None
-        return np.frombuffer(self.t[name][2], np.float32)
+        dt, _, data = self.t[name]
+        if dt == F16:  # bound as fp32 once (runtime/qwen_model.cpp:182-190)
+            return halves_to_floats(np.frombuffer(data, np.uint16))
+        return np.frombuffer(data, np.float32)
 
     def _mv(self, name, x, out_dim, in_dim):
-        w = np.frombuffer(self.t[name][2], np.uint8)
-        return matvec_i4(w, np.ascontiguousarray(x, np.float32), out_dim, in_dim, self.gs, threads=8)
+        dt, _, data = self.t[name]
+        w = np.frombuffer(data, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        if dt == VQ2:
+            return matvec_vq2(w, x, out_dim, in_dim, threads=8)
+        return matvec_i4(w, x, out_dim, in_dim, self.gs, threads=8)
 
     def step(self, token: int) -> np.ndarray:
         c = self.c

@@ -2,7 +2,8 @@
 decode (QwenModel::forward_token, compiled from the reference tree into oracle/_ref):
 the same logits and the same next token, step after step, on dense i4 files of
 several shapes (biases, Qwen3 q/k norms, fp32 embedding with separate lm_head,
-group 128, GQA ratios 1 / 4 / 7)."""
+group 128, GQA ratios 1 / 2 / 4 / 7, and VQ2 files with fp16 vectors, tied to
+the compact-i4 embedding or with a VQ2 lm_head)."""
 import ctypes
 
 import numpy as np
@@ -17,6 +18,9 @@ CASES = {
                          tied=False),
     "qwen3_qknorm": dict(hidden=256, n_heads=2, n_kv_heads=2, head_dim=128, inter=512, vocab=300, layers=2,
                          biases=False, qk_norm=True),
+    "vq2_qwen2": dict(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=512, vocab=300, layers=2, vq2=True),
+    "vq2_untied": dict(hidden=256, n_heads=4, n_kv_heads=1, head_dim=64, inter=384, vocab=200, layers=1, vq2=True,
+                       tied=False),
     "embed_f32_g128": dict(hidden=256, n_heads=4, n_kv_heads=1, head_dim=64, inter=512, vocab=200, layers=1,
                            group_size=128, embed_f32=True, tied=False),
 }

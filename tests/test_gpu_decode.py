@@ -22,6 +22,10 @@ CASES = {
                                layers=2, biases=False, qk_norm=True),
     "embed_f32_g128_untied": dict(hidden=512, n_heads=8, n_kv_heads=1, head_dim=64, inter=1024, vocab=500,
                                   layers=1, group_size=128, embed_f32=True, tied=False),
+    "vq2_qwen25_shape": dict(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864, vocab=2000, layers=2,
+                             vq2=True),
+    "vq2_untied_gqa4": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=500, layers=1,
+                            vq2=True, tied=False),
     "head_dim256": dict(hidden=512, n_heads=2, n_kv_heads=1, head_dim=256, inter=768, vocab=300, layers=1),
 }
 PROMPT = [11, 257, 3, 3, 0, 199, 42, 5, 123, 7, 64, 99]
@@ -109,10 +113,14 @@ def test_errors(gpu, tmp_path):
     eng.step(2)
     assert lib.tqhip_decode_step(eng._h, 1) == gpu.EBADSHAPE  # cache full
     eng.close()
-    img, _ = tf.vq2_model(hidden=128, vocab=50)
+    path = tmp_path / "f32.tqwen"
+    path.write_bytes(bytes(tf.build([tf.f32_tensor("a", [1.0, 2.0])])))
+    with pytest.raises(ValueError, match="i4 and VQ2 files only"):
+        gpu.DecodeEngine(gpu.ModelFile(str(path)))
+    img, _ = tf.vq2_model(hidden=128, vocab=50)  # a VQ2 file without the layer tensors
     path = tmp_path / "v.tqwen"
     path.write_bytes(bytes(img))
-    with pytest.raises(ValueError, match="i4 files only"):
+    with pytest.raises(ValueError, match="missing tensor"):
         gpu.DecodeEngine(gpu.ModelFile(str(path)))
     img, _, ts = tf.dense_i4_model(hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, inter=256, vocab=100,
                                    layers=1)

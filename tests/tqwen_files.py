@@ -163,25 +163,31 @@ def vq2_model(group_size: int = 64, hidden: int = 256, vocab: int = 500, seed: i
 
 def dense_i4_model(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864, vocab=2000, layers=2,
                    group_size=64, tied=True, biases=True, qk_norm=False, embed_f32=False, seed=0,
-                   max_seq_len=256) -> tuple:
+                   max_seq_len=256, vq2=False) -> tuple:
     """A dense Qwen2.x-shaped i4 file with every tensor QwenModel binds (runtime/qwen_model.cpp:437-640):
     embedding (i4, or fp32), per layer two RMSNorm weights, q/k/v/o and gate/up/down (i4), optional
     q/k/v biases and q/k norms, the final norm and, when not tied, lm_head. Norm weights are drawn
-    around 1 and biases around 0. Returns (image, config dict, {name: (dtype, shape, bytes)})."""
+    around 1 and biases around 0. vq2=True writes a VQ2 file instead: VQ2 projections, fp16
+    norms and biases, the compact-i4 embedding (runtime/model_loader.cpp:394-404, 705-719).
+    Returns (image, config dict, {name: (dtype, shape, bytes)})."""
     rng = np.random.default_rng(seed)
     qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
     ts = []
 
     def vec(name, n, mean, std):
-        ts.append(f32_tensor(name, rng.normal(mean, std, n).astype(np.float32)))
+        v = rng.normal(mean, std, n)
+        ts.append(tensor(name, F16, (n,), v.astype(np.float16).tobytes()) if vq2 else f32_tensor(name, v))
 
-    def mat(name, rows, cols):
-        ts.append(tensor(name, I4, (rows, cols), i4_payload(rows, cols, group_size, int(rng.integers(1 << 30)))))
+    def mat(name, rows, cols, i4=False):
+        if vq2 and not i4:
+            ts.append(tensor(name, VQ2, (rows, cols), vq2_payload(rows, cols, int(rng.integers(1 << 30)))))
+        else:
+            ts.append(tensor(name, I4, (rows, cols), i4_payload(rows, cols, group_size, int(rng.integers(1 << 30)))))
 
     if embed_f32:
         ts.append(f32_tensor("model.embed_tokens.weight", rng.normal(0, 0.05, (vocab, hidden)).astype(np.float32)))
     else:
-        mat("model.embed_tokens.weight", vocab, hidden)
+        mat("model.embed_tokens.weight", vocab, hidden, i4=True)
     for li in range(layers):
         p = f"model.layers.{li}."
         vec(p + "input_layernorm.weight", hidden, 1.0, 0.1)
@@ -206,5 +212,5 @@ def dense_i4_model(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864
     cfg = dict(n_layers=layers, hidden_size=hidden, intermediate_size=inter, n_heads=n_heads,
                n_kv_heads=n_kv_heads, head_dim=head_dim, vocab_size=vocab, max_seq_len=max_seq_len,
                tied_embeddings=int(tied), rms_norm_eps=1e-6, rope_theta=1e6, quant_group_size=group_size)
-    img = build(ts, version=3, dtype=I4, **cfg)
+    img = build(ts, version=3, dtype=VQ2 if vq2 else I4, **cfg)
     return img, cfg, {t["name"]: (t["dtype"], t["shape"], t["data"]) for t in ts}

@@ -1,9 +1,9 @@
-// decode_engine.hip -- device-resident decode engine for dense i4 Qwen2 / Qwen3 models.
+// decode_engine.hip -- device-resident decode engine for dense i4 / VQ2 Qwen2 / Qwen3 models.
 //
 // The "gpu_decode" boundary of the reference (kernels/dispatch.h:337-378: create /
 // step / reset / destroy / logits on an opaque engine). The reference's CUDA engine
 // (kernels/cuda/gpu_engine.cu) serves f32 / f16 files; this one serves the i4
-// HQQ files whose projections the library's matvec kernels run. Weights stay
+// HQQ and VQ2 files whose projections the library's matvec kernels run. Weights stay
 // where tqhip_model_upload put them (one HBM allocation per model), activations,
 // the fp32 KV cache and the argmax live in one more allocation, and a step is
 // one HIP-graph replay on the engine's stream: only the token id and the next
@@ -376,6 +376,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final(const float *pv, 
     if (threadIdx.x == 0) *out = bi == 0x7fffffff ? 0 : bi;
 }
 
+// fp16 -> fp32 of the fp16 vectors a VQ2 file may carry (norms, biases); the
+// reference converts them once at load with half_to_float (runtime/qwen_model.cpp:182-190).
+__global__ void f16_to_f32(const _Float16 *src, float *dst, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = static_cast<float>(src[i]);
+}
+
 struct Layer {
     const float *in_ln = nullptr, *post_ln = nullptr;
     const float *qb = nullptr, *kb = nullptr, *vb = nullptr, *qn = nullptr, *kn = nullptr;
@@ -385,6 +392,7 @@ struct Layer {
 
 struct Engine {
     tqhip_model_config c{};
+    int pd = 3, lm_dtype = 3;  // projection dtype and lm_head dtype: 3 i4, 4 VQ2
     int q_dim = 0, kv_dim = 0, gs = 0, max_seq = 0, amax_blocks = 0;
     float attn_scale = 0.0f;
     const void *embed = nullptr;
@@ -406,6 +414,10 @@ struct Engine {
     int seq_len = 0;
 };
 
+int mv(const Engine &e, const uint8_t *w, int dtype, const float *x, float *y, int M, int K, hipStream_t s) {
+    return dtype == 4 ? launch_vq2_matvec(w, x, y, M, K, s) : launch_i4_matvec(w, x, y, M, K, e.gs, s);
+}
+
 int forward(Engine &e) {
     hipStream_t s = e.stream;
     const int H = e.c.hidden_size, I = e.c.intermediate_size;
@@ -423,24 +435,34 @@ int forward(Engine &e) {
         const uint8_t *w3[3] = {L.q, L.k, L.v};
         float *y3[3] = {e.q, e.k, e.v};
         const int d3[3] = {e.q_dim, e.kv_dim, e.kv_dim};
-        if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
+        if (e.pd == 3) {
+            if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
+        } else {
+            for (int j = 0; j < 3; ++j)
+                if ((st = mv(e, w3[j], e.pd, e.normed, y3[j], d3[j], H, s)) != kOk) return st;
+        }
         auto attn = e.c.head_dim == 64 ? attention_step<64> : e.c.head_dim == 128 ? attention_step<128>
                                                                                   : attention_step<256>;
         attn<<<e.c.n_heads, kAttnThreads, 0, s>>>(e.q, e.k, e.v, L.qb, L.kb, L.vb, L.qn, L.kn, kc, vc, e.attn,
                                                   e.dev_io, e.c.n_heads / e.c.n_kv_heads, e.max_seq, e.c.rope_theta,
                                                   e.c.rms_norm_eps, e.attn_scale);
-        if ((st = launch_i4_matvec(L.o, e.attn, e.o, H, e.q_dim, e.gs, s)) != kOk) return st;
+        if ((st = mv(e, L.o, e.pd, e.attn, e.o, H, e.q_dim, s)) != kOk) return st;
         launch_add_rmsnorm(e.hidden, e.o, L.post_ln, e.normed, H, e.c.rms_norm_eps, s);
         const uint8_t *w2[2] = {L.gate, L.up};
         float *y2[2] = {e.gate, e.up};
         const int d2[2] = {I, I};
-        if ((st = launch_i4_matvec_group(2, w2, y2, d2, e.normed, H, e.gs, s)) != kOk) return st;
+        if (e.pd == 3) {
+            if ((st = launch_i4_matvec_group(2, w2, y2, d2, e.normed, H, e.gs, s)) != kOk) return st;
+        } else {
+            for (int j = 0; j < 2; ++j)
+                if ((st = mv(e, w2[j], e.pd, e.normed, y2[j], d2[j], H, s)) != kOk) return st;
+        }
         swiglu<<<(I + 255) / 256, 256, 0, s>>>(e.gate, e.up, I);
-        if ((st = launch_i4_matvec(L.down, e.gate, e.ffn, H, I, e.gs, s)) != kOk) return st;
+        if ((st = mv(e, L.down, e.pd, e.gate, e.ffn, H, I, s)) != kOk) return st;
         const float *next_ln = li + 1 < e.layers.size() ? e.layers[li + 1].in_ln : e.final_norm;
         launch_add_rmsnorm(e.hidden, e.ffn, next_ln, e.normed, H, e.c.rms_norm_eps, s);
     }
-    if ((st = launch_i4_matvec(e.lm_head, e.normed, e.logits, e.c.vocab_size, H, e.gs, s)) != kOk) return st;
+    if ((st = mv(e, e.lm_head, e.lm_dtype, e.normed, e.logits, e.c.vocab_size, H, s)) != kOk) return st;
     argmax_partial<<<e.amax_blocks, kArgmaxThreads, 0, s>>>(e.logits, e.c.vocab_size, e.amax_v, e.amax_i);
     argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, e.amax_blocks, e.dev_io + 2);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
@@ -481,9 +503,16 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         *err = "gpu engine: no model";
         return kBadFile;
     }
-    if (c.file_dtype != 3 || c.model_type != 0) {
-        *err = "gpu engine: serves dense (Qwen2 / Qwen3) i4 files only";
+    if ((c.file_dtype != 3 && c.file_dtype != 4) || c.model_type != 0) {
+        *err = "gpu engine: serves dense (Qwen2 / Qwen3) i4 and VQ2 files only";
         return kBadFile;
+    }
+    for (int i = 0, n = tqhip_model_tensor_count(model); i < n; ++i) {
+        tqhip_tensor_info info;
+        if (tqhip_model_tensor_at(model, i, &info) == kOk && std::strstr(info.name, ".rot_sign")) {
+            *err = "gpu engine: BiIP-rotated models are not served";
+            return kBadFile;
+        }
     }
     if (max_seq_len <= 0) max_seq_len = c.max_seq_len;
     if (max_seq_len > c.max_seq_len) {
@@ -509,18 +538,40 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     e->q_dim = c.n_heads * c.head_dim;
     e->kv_dim = c.n_kv_heads * c.head_dim;
     e->gs = c.quant_group_size;
+    e->pd = c.file_dtype;
     e->max_seq = max_seq_len;
     e->attn_scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
     const uint64_t H = c.hidden_size, I = c.intermediate_size, V = c.vocab_size;
     Binder b{model, err};
     bool ok = true;
-    auto vec = [&](const std::string &n, uint64_t d, bool opt = false) {
-        const float *p = static_cast<const float *>(b.get(n, 0, d, 0, opt));
+    // fp16 vectors (VQ2 files) are converted into the arena after it exists:
+    // (source, length, the pointer to patch).
+    struct F16Vec {
+        const void *src;
+        int n;
+        const float **slot;
+    };
+    std::vector<F16Vec> f16s;
+    size_t f16_floats = 0;
+    auto vec_into = [&](const std::string &n, uint64_t d, const float **slot, bool opt = false) {
+        tqhip_tensor_info info;
+        const bool half = e->pd == 4 && tqhip_model_find(model, n.c_str(), &info) == kOk && info.dtype == 1;
+        const void *p = b.get(n, half ? 1 : 0, d, 0, opt);
         if (!p && (!opt || !err->empty())) ok = false;
+        if (p && half) {
+            f16s.push_back({p, static_cast<int>(d), slot});
+            f16_floats += (d + 63) / 64 * 64;
+            p = nullptr;  // patched after the arena is allocated
+        }
+        *slot = static_cast<const float *>(p);
+    };
+    auto vec = [&](const std::string &n, uint64_t d, bool opt = false) {
+        const float *p = nullptr;
+        vec_into(n, d, &p, opt);
         return p;
     };
     auto mat = [&](const std::string &n, uint64_t d0, uint64_t d1) {
-        const uint8_t *p = static_cast<const uint8_t *>(b.get(n, 3, d0, d1));
+        const uint8_t *p = static_cast<const uint8_t *>(b.get(n, e->pd, d0, d1));
         if (!p) ok = false;
         return p;
     };
@@ -533,12 +584,15 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         e->embed = b.get("model.embed_tokens.weight", e->embed_i4 ? 3 : 0, V, H);  // i4 or fp32 [vocab, hidden]
         ok = e->embed != nullptr;
     }
-    if (ok) e->final_norm = vec("model.norm.weight", H);
+    if (ok) vec_into("model.norm.weight", H, &e->final_norm);
     if (ok) {
         tqhip_tensor_info lm;
         if (tqhip_model_find(model, "lm_head.weight", &lm) == kOk) {
-            e->lm_head = mat("lm_head.weight", V, H);
+            e->lm_dtype = lm.dtype == 3 ? 3 : e->pd;  // an i4 lm_head in a VQ2 file, or the file's own
+            e->lm_head = static_cast<const uint8_t *>(b.get("lm_head.weight", e->lm_dtype, V, H));
+            ok = e->lm_head != nullptr;
         } else if (c.tied_embeddings && e->embed_i4) {
+            e->lm_dtype = 3;
             e->lm_head = static_cast<const uint8_t *>(e->embed);
         } else {
             *err = c.tied_embeddings ? "gpu engine: a tied fp32 embedding needs an fp32 lm_head, which is not served"
@@ -550,8 +604,8 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     for (int i = 0; ok && i < c.n_layers; ++i) {
         const std::string p = "model.layers." + std::to_string(i) + ".";
         Layer &L = e->layers[i];
-        L.in_ln = vec(p + "input_layernorm.weight", H);
-        L.post_ln = vec(p + "post_attention_layernorm.weight", H);
+        vec_into(p + "input_layernorm.weight", H, &L.in_ln);
+        vec_into(p + "post_attention_layernorm.weight", H, &L.post_ln);
         L.q = mat(p + "self_attn.q_proj.weight", e->q_dim, H);
         L.k = mat(p + "self_attn.k_proj.weight", e->kv_dim, H);
         L.v = mat(p + "self_attn.v_proj.weight", e->kv_dim, H);
@@ -560,11 +614,11 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         L.up = mat(p + "mlp.up_proj.weight", I, H);
         L.down = mat(p + "mlp.down_proj.weight", H, I);
         if (!ok) break;
-        L.qb = vec(p + "self_attn.q_proj.bias", e->q_dim, true);
-        L.kb = vec(p + "self_attn.k_proj.bias", e->kv_dim, true);
-        L.vb = vec(p + "self_attn.v_proj.bias", e->kv_dim, true);
-        L.qn = vec(p + "self_attn.q_norm.weight", c.head_dim, true);
-        L.kn = vec(p + "self_attn.k_norm.weight", c.head_dim, true);
+        vec_into(p + "self_attn.q_proj.bias", e->q_dim, &L.qb, true);
+        vec_into(p + "self_attn.k_proj.bias", e->kv_dim, &L.kb, true);
+        vec_into(p + "self_attn.v_proj.bias", e->kv_dim, &L.vb, true);
+        vec_into(p + "self_attn.q_norm.weight", c.head_dim, &L.qn, true);
+        vec_into(p + "self_attn.k_norm.weight", c.head_dim, &L.kn, true);
         if (ok && (L.qn == nullptr) != (L.kn == nullptr)) {
             *err = "gpu engine: layer " + std::to_string(i) + ": q_norm/k_norm must both be present or both absent";
             ok = false;
@@ -582,11 +636,12 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     const size_t counts[] = {H, H, static_cast<size_t>(e->q_dim), static_cast<size_t>(e->kv_dim),
                              static_cast<size_t>(e->kv_dim), static_cast<size_t>(e->q_dim), H, I, I, H, V,
                              2 * static_cast<size_t>(c.n_layers) * e->layer_stride,
-                             static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 4};
+                             static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 4,
+                             f16_floats};
     float **slots[] = {&e->hidden, &e->normed, &e->q, &e->k, &e->v, &e->attn, &e->o, &e->gate, &e->up, &e->ffn,
                        &e->logits, &e->kv, &e->amax_v};
-    size_t offs[15], total = 0;
-    for (int i = 0; i < 15; ++i) {
+    size_t offs[16], total = 0;
+    for (int i = 0; i < 16; ++i) {
         offs[i] = total;
         total += (counts[i] * 4 + 255) / 256 * 256;
     }
@@ -604,6 +659,12 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         *err = "gpu engine: HIP memset failed";
         release(e);
         return kHipFailed;
+    }
+    float *conv = reinterpret_cast<float *>(base + offs[15]);
+    for (const F16Vec &f : f16s) {
+        f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);
+        *f.slot = conv;
+        conv += (f.n + 63) / 64 * 64;
     }
     // One eager pass at position 0 with token 0 sets up the matvec launches'
     // per-stream scratch outside the capture; its KV rows are rewritten by the
