@@ -237,7 +237,8 @@ void tqhip_model_free(void *model);                   /* frees the HBM copy too 
  * kernels/dispatch.h:337-378; the reference's engine is kernels/cuda/gpu_engine.cu, which
  * serves f32 / f16 files). This engine serves dense i4 and VQ2 files (model type 0: Qwen2.x
  * with q/k/v biases, Qwen3 dense with q/k norms; VQ2 files with fp16 or fp32 vectors and a
- * compact-i4 or VQ2 lm_head; not BiIP-rotated): weights as uploaded by tqhip_model_upload, an
+ * compact-i4 or VQ2 lm_head; BiIP rotations where the file has them): weights as uploaded by
+ * tqhip_model_upload, an
  * fp32 KV cache of max_seq_len positions and all activations in HBM, one HIP-graph replay
  * per step; only the token id and the next token cross PCIe.
  *

@@ -16,6 +16,8 @@ Qwen2.x / Qwen3 model as QwenModel::forward_token runs it
                      positions in order)
   swiglu             kernels/silu/swiglu_ref.cpp:12-19
   argmax             kernels/argmax/argmax_ref.cpp:11-20 (first index of the maximum)
+  BiIP rotation      biip_rotate (oracle/__init__.py) ahead of a projection carrying
+                     rot_sign / rot_scale (runtime/qwen_model.cpp:229-238)
 
 Every step keeps the reference's fp32 operation order; sums the reference
 takes in double are taken in double. tests/test_decode_oracle.py pins this
@@ -25,7 +27,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import dequant_i4_row, halves_to_floats, matvec_i4, matvec_vq2
+from . import biip_rotate, dequant_i4_row, halves_to_floats, matvec_i4, matvec_vq2
 
 F32, F16, I4, VQ2 = 0, 1, 3, 4
 
@@ -119,6 +121,11 @@ class DenseDecoder:
         dt, _, data = self.t[name]
         w = np.frombuffer(data, np.uint8)
         x = np.ascontiguousarray(x, np.float32)
+        prefix = name[:-len(".weight")]
+        sign = self._vec(prefix + ".rot_sign")
+        if sign is not None:  # mv_rot (runtime/qwen_model.cpp:229-238), bind_rot's block size (:59-66, 427-435)
+            bs = next((b for b in (256, 128, 64, 32, 16, 8, 4, 2) if in_dim % b == 0), 1)
+            x = biip_rotate(x, self._vec(prefix + ".rot_scale"), sign, bs)
         if dt == VQ2:
             return matvec_vq2(w, x, out_dim, in_dim, threads=8)
         return matvec_i4(w, x, out_dim, in_dim, self.gs, threads=8)

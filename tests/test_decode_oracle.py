@@ -21,6 +21,10 @@ CASES = {
     "vq2_qwen2": dict(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=512, vocab=300, layers=2, vq2=True),
     "vq2_untied": dict(hidden=256, n_heads=4, n_kv_heads=1, head_dim=64, inter=384, vocab=200, layers=1, vq2=True,
                        tied=False),
+    "vq2_rotated": dict(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=384, vocab=300, layers=2,
+                        vq2=True, rotated=True),
+    "i4_rotated_odd_inter": dict(hidden=256, n_heads=4, n_kv_heads=1, head_dim=64, inter=200, vocab=100, layers=1,
+                                 rotated=True),
     "embed_f32_g128": dict(hidden=256, n_heads=4, n_kv_heads=1, head_dim=64, inter=512, vocab=200, layers=1,
                            group_size=128, embed_f32=True, tied=False),
 }
@@ -46,6 +50,7 @@ def test_restatement_matches_reference_decode(orc, ref, tmp_path, case):
     dec = DenseDecoder(cfg, tensors, 16)
     want = np.empty(cfg["vocab_size"], np.float32)
     for t in TOKENS:
+        t %= cfg["vocab_size"]
         nxt = ref.tqref_decode_step(t)
         ref.tqref_decode_logits(want.ctypes.data, want.size)
         got = dec.step(t)

@@ -26,6 +26,10 @@ CASES = {
                              vq2=True),
     "vq2_untied_gqa4": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=500, layers=1,
                             vq2=True, tied=False),
+    "vq2_rotated_qwen25_shape": dict(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864, vocab=2000,
+                                     layers=2, vq2=True, rotated=True),
+    "i4_rotated": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1200, vocab=300, layers=1,
+                       rotated=True),
     "head_dim256": dict(hidden=512, n_heads=2, n_kv_heads=1, head_dim=256, inter=768, vocab=300, layers=1),
 }
 PROMPT = [11, 257, 3, 3, 0, 199, 42, 5, 123, 7, 64, 99]

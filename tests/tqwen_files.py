@@ -163,12 +163,14 @@ def vq2_model(group_size: int = 64, hidden: int = 256, vocab: int = 500, seed: i
 
 def dense_i4_model(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864, vocab=2000, layers=2,
                    group_size=64, tied=True, biases=True, qk_norm=False, embed_f32=False, seed=0,
-                   max_seq_len=256, vq2=False) -> tuple:
+                   max_seq_len=256, vq2=False, rotated=False) -> tuple:
     """A dense Qwen2.x-shaped i4 file with every tensor QwenModel binds (runtime/qwen_model.cpp:437-640):
     embedding (i4, or fp32), per layer two RMSNorm weights, q/k/v/o and gate/up/down (i4), optional
     q/k/v biases and q/k norms, the final norm and, when not tied, lm_head. Norm weights are drawn
     around 1 and biases around 0. vq2=True writes a VQ2 file instead: VQ2 projections, fp16
     norms and biases, the compact-i4 embedding (runtime/model_loader.cpp:394-404, 705-719).
+    rotated=True adds BiIP rotation vectors (rot_sign of +-1, rot_scale around 1) to every
+    projection (runtime/qwen_model.cpp:427-435, 641-647).
     Returns (image, config dict, {name: (dtype, shape, bytes)})."""
     rng = np.random.default_rng(seed)
     qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
@@ -177,6 +179,13 @@ def dense_i4_model(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864
     def vec(name, n, mean, std):
         v = rng.normal(mean, std, n)
         ts.append(tensor(name, F16, (n,), v.astype(np.float16).tobytes()) if vq2 else f32_tensor(name, v))
+
+    def rot(prefix, n):
+        if rotated:
+            sign = np.where(rng.random(n) < 0.5, -1.0, 1.0)
+            ts.append(tensor(prefix + ".rot_sign", F16, (n,), sign.astype(np.float16).tobytes()) if vq2
+                      else f32_tensor(prefix + ".rot_sign", sign))
+            vec(prefix + ".rot_scale", n, 1.0, 0.2)
 
     def mat(name, rows, cols, i4=False):
         if vq2 and not i4:
@@ -206,6 +215,10 @@ def dense_i4_model(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864
         mat(p + "mlp.gate_proj.weight", inter, hidden)
         mat(p + "mlp.up_proj.weight", inter, hidden)
         mat(p + "mlp.down_proj.weight", hidden, inter)
+        for n, k in (("self_attn.q_proj", hidden), ("self_attn.k_proj", hidden), ("self_attn.v_proj", hidden),
+                     ("self_attn.o_proj", qd), ("mlp.gate_proj", hidden), ("mlp.up_proj", hidden),
+                     ("mlp.down_proj", inter)):
+            rot(p + n, k)
     vec("model.norm.weight", hidden, 1.0, 0.1)
     if not tied or embed_f32:
         mat("lm_head.weight", vocab, hidden)

@@ -22,6 +22,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -383,7 +384,15 @@ __global__ void f16_to_f32(const _Float16 *src, float *dst, int n) {
     if (i < n) dst[i] = static_cast<float>(src[i]);
 }
 
+// BiIP rotation ahead of one projection (RotParams, runtime/qwen_model.h:316-320).
+struct Rot {
+    const float *sign = nullptr, *scale = nullptr;
+    int bs = 0;
+};
+
 struct Layer {
+    Rot rq, rk, rv, ro, rg, ru, rd;
+    bool rotated = false;
     const float *in_ln = nullptr, *post_ln = nullptr;
     const float *qb = nullptr, *kb = nullptr, *vb = nullptr, *qn = nullptr, *kn = nullptr;
     const uint8_t *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
@@ -402,7 +411,7 @@ struct Engine {
     std::vector<Layer> layers;
     float *hidden = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr,
           *o = nullptr, *gate = nullptr, *up = nullptr, *ffn = nullptr, *logits = nullptr, *kv = nullptr,
-          *amax_v = nullptr;
+          *amax_v = nullptr, *rotbuf = nullptr;
     int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next
     int *host_io = nullptr;                     // pinned mirror of dev_io
     size_t layer_stride = 0;                    // floats per layer and plane: n_kv_heads * max_seq * head_dim
@@ -416,6 +425,18 @@ struct Engine {
 
 int mv(const Engine &e, const uint8_t *w, int dtype, const float *x, float *y, int M, int K, hipStream_t s) {
     return dtype == 4 ? launch_vq2_matvec(w, x, y, M, K, s) : launch_i4_matvec(w, x, y, M, K, e.gs, s);
+}
+
+// mv_rot (runtime/qwen_model.cpp:229-238): the activation rotated into rotbuf
+// first when the projection carries a rotation.
+int mvr(const Engine &e, const uint8_t *w, int dtype, const float *x, float *y, int M, int K, const Rot &r,
+        hipStream_t s) {
+    if (r.sign) {
+        const int st = launch_biip_rotate(x, e.rotbuf, K, r.scale, r.sign, r.bs, s);
+        if (st != kOk) return st;
+        x = e.rotbuf;
+    }
+    return mv(e, w, dtype, x, y, M, K, s);
 }
 
 int forward(Engine &e) {
@@ -435,30 +456,32 @@ int forward(Engine &e) {
         const uint8_t *w3[3] = {L.q, L.k, L.v};
         float *y3[3] = {e.q, e.k, e.v};
         const int d3[3] = {e.q_dim, e.kv_dim, e.kv_dim};
-        if (e.pd == 3) {
+        const Rot *r3[3] = {&L.rq, &L.rk, &L.rv};
+        if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
         } else {
             for (int j = 0; j < 3; ++j)
-                if ((st = mv(e, w3[j], e.pd, e.normed, y3[j], d3[j], H, s)) != kOk) return st;
+                if ((st = mvr(e, w3[j], e.pd, e.normed, y3[j], d3[j], H, *r3[j], s)) != kOk) return st;
         }
         auto attn = e.c.head_dim == 64 ? attention_step<64> : e.c.head_dim == 128 ? attention_step<128>
                                                                                   : attention_step<256>;
         attn<<<e.c.n_heads, kAttnThreads, 0, s>>>(e.q, e.k, e.v, L.qb, L.kb, L.vb, L.qn, L.kn, kc, vc, e.attn,
                                                   e.dev_io, e.c.n_heads / e.c.n_kv_heads, e.max_seq, e.c.rope_theta,
                                                   e.c.rms_norm_eps, e.attn_scale);
-        if ((st = mv(e, L.o, e.pd, e.attn, e.o, H, e.q_dim, s)) != kOk) return st;
+        if ((st = mvr(e, L.o, e.pd, e.attn, e.o, H, e.q_dim, L.ro, s)) != kOk) return st;
         launch_add_rmsnorm(e.hidden, e.o, L.post_ln, e.normed, H, e.c.rms_norm_eps, s);
         const uint8_t *w2[2] = {L.gate, L.up};
         float *y2[2] = {e.gate, e.up};
         const int d2[2] = {I, I};
-        if (e.pd == 3) {
+        const Rot *r2[2] = {&L.rg, &L.ru};
+        if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(2, w2, y2, d2, e.normed, H, e.gs, s)) != kOk) return st;
         } else {
             for (int j = 0; j < 2; ++j)
-                if ((st = mv(e, w2[j], e.pd, e.normed, y2[j], d2[j], H, s)) != kOk) return st;
+                if ((st = mvr(e, w2[j], e.pd, e.normed, y2[j], d2[j], H, *r2[j], s)) != kOk) return st;
         }
         swiglu<<<(I + 255) / 256, 256, 0, s>>>(e.gate, e.up, I);
-        if ((st = mv(e, L.down, e.pd, e.gate, e.ffn, H, I, s)) != kOk) return st;
+        if ((st = mvr(e, L.down, e.pd, e.gate, e.ffn, H, I, L.rd, s)) != kOk) return st;
         const float *next_ln = li + 1 < e.layers.size() ? e.layers[li + 1].in_ln : e.final_norm;
         launch_add_rmsnorm(e.hidden, e.ffn, next_ln, e.normed, H, e.c.rms_norm_eps, s);
     }
@@ -506,13 +529,6 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     if ((c.file_dtype != 3 && c.file_dtype != 4) || c.model_type != 0) {
         *err = "gpu engine: serves dense (Qwen2 / Qwen3) i4 and VQ2 files only";
         return kBadFile;
-    }
-    for (int i = 0, n = tqhip_model_tensor_count(model); i < n; ++i) {
-        tqhip_tensor_info info;
-        if (tqhip_model_tensor_at(model, i, &info) == kOk && std::strstr(info.name, ".rot_sign")) {
-            *err = "gpu engine: BiIP-rotated models are not served";
-            return kBadFile;
-        }
     }
     if (max_seq_len <= 0) max_seq_len = c.max_seq_len;
     if (max_seq_len > c.max_seq_len) {
@@ -619,6 +635,28 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         vec_into(p + "self_attn.v_proj.bias", e->kv_dim, &L.vb, true);
         vec_into(p + "self_attn.q_norm.weight", c.head_dim, &L.qn, true);
         vec_into(p + "self_attn.k_norm.weight", c.head_dim, &L.kn, true);
+        // bind_rot (runtime/qwen_model.cpp:427-435): sign present = rotated; the
+        // block is the largest of 256, 128, ..., 2 dividing in_features, else 1.
+        auto rot = [&](const std::string &prefix, int in_f, Rot &r) {
+            vec_into(prefix + ".rot_sign", in_f, &r.sign, true);
+            vec_into(prefix + ".rot_scale", in_f, &r.scale, true);
+            tqhip_tensor_info si;
+            if (tqhip_model_find(model, (prefix + ".rot_sign").c_str(), &si) != kOk) return;
+            r.bs = 1;
+            for (int bs : {256, 128, 64, 32, 16, 8, 4, 2})
+                if (in_f % bs == 0) {
+                    r.bs = bs;
+                    break;
+                }
+            L.rotated = true;
+        };
+        rot(p + "self_attn.q_proj", c.hidden_size, L.rq);
+        rot(p + "self_attn.k_proj", c.hidden_size, L.rk);
+        rot(p + "self_attn.v_proj", c.hidden_size, L.rv);
+        rot(p + "self_attn.o_proj", e->q_dim, L.ro);
+        rot(p + "mlp.gate_proj", c.hidden_size, L.rg);
+        rot(p + "mlp.up_proj", c.hidden_size, L.ru);
+        rot(p + "mlp.down_proj", c.intermediate_size, L.rd);
         if (ok && (L.qn == nullptr) != (L.kn == nullptr)) {
             *err = "gpu engine: layer " + std::to_string(i) + ": q_norm/k_norm must both be present or both absent";
             ok = false;
@@ -637,11 +675,11 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
                              static_cast<size_t>(e->kv_dim), static_cast<size_t>(e->q_dim), H, I, I, H, V,
                              2 * static_cast<size_t>(c.n_layers) * e->layer_stride,
                              static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 4,
-                             f16_floats};
+                             f16_floats, std::max<size_t>(std::max<size_t>(H, I), e->q_dim)};
     float **slots[] = {&e->hidden, &e->normed, &e->q, &e->k, &e->v, &e->attn, &e->o, &e->gate, &e->up, &e->ffn,
                        &e->logits, &e->kv, &e->amax_v};
-    size_t offs[16], total = 0;
-    for (int i = 0; i < 16; ++i) {
+    size_t offs[17], total = 0;
+    for (int i = 0; i < 17; ++i) {
         offs[i] = total;
         total += (counts[i] * 4 + 255) / 256 * 256;
     }
@@ -660,6 +698,7 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         release(e);
         return kHipFailed;
     }
+    e->rotbuf = reinterpret_cast<float *>(base + offs[16]);
     float *conv = reinterpret_cast<float *>(base + offs[15]);
     for (const F16Vec &f : f16s) {
         f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);
