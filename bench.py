@@ -39,7 +39,8 @@ Printed (one JSON line on stdout):
                Qwen2.5-0.5B-shaped dense i4 HQQ@64 model (24 layers, 14/2 heads,
                tied i4 embedding, q/k/v biases, random weights): ms per token
                and tokens/s of step() (one graph replay, token in and next
-               token out), over --steps tokens after --warmup tokens
+               token out), over --steps tokens after --warmup tokens; the same
+               for a BiIP-rotated VQ2 file of that shape (vq2_rotated)
   cpu_baseline the compiled reference's `ref` matvec (oracle/_ref, tiny-llm's
                kernels/matvec/matvec_i4_ref.cpp built unmodified), row-split
                over host threads, on the same step; the C++ restatement is
@@ -371,8 +372,25 @@ def engine(tq, steps, warmup):
                     ref.tqref_decode_step(t + 2)
                 cpu = {"ms_per_token": round((time.perf_counter() - t0) / n * 1e3, 1), "tokens": n, "cores": 1,
                        "kind": "reference"}
+    # the same shape as a BiIP-rotated VQ2 file (VQ2 projections, fp16 vectors, compact-i4 embedding)
+    img2, _, _ = tqwen_files.dense_i4_model(hidden=HIDDEN, n_heads=14, n_kv_heads=2, head_dim=64, inter=INTER,
+                                            vocab=VOCAB, layers=N_LAYERS, group_size=G, seed=12, max_seq_len=4096,
+                                            vq2=True, rotated=True)
+    m2 = tq.ModelFile.from_image(img2)
+    eng2 = tq.DecodeEngine(m2, warmup + steps + 1)
+    tok = 1
+    for _ in range(warmup):
+        tok = eng2.step(tok)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = eng2.step(tok)
+    dt2 = (time.perf_counter() - t0) / steps
+    eng2.close()
+    m2.close()
+    vq2 = {"model": "the same shape as a BiIP-rotated VQ2 file", "file_bytes": len(img2),
+           "ms_per_token": round(dt2 * 1e3, 4), "tokens_per_s": round(1.0 / dt2, 1)}
     return {"model": "Qwen2.5-0.5B-shaped dense i4 HQQ@64 (24 layers, hidden 896, 14/2 heads, inter 4864, "
-                     "vocab 151936, tied i4 embedding), random weights",
+                     "vocab 151936, tied i4 embedding), random weights", "vq2_rotated": vq2,
             "file_bytes": len(img), "upload_s": round(upload_s, 3), "positions": f"{warmup}..{warmup + steps - 1}",
             "ms_per_token": round(dt * 1e3, 4), "tokens_per_s": round(1.0 / dt, 1), "cpu_reference": cpu}
 
@@ -512,7 +530,7 @@ def main():
     eng = None if args.no_engine else engine(tq, args.steps, args.warmup)
     if eng:
         log(f"[bench] decode engine: {eng['ms_per_token']} ms/token, {eng['tokens_per_s']} tokens/s "
-            f"(positions {eng['positions']})")
+            f"(positions {eng['positions']}); rotated VQ2 file: {eng['vq2_rotated']['ms_per_token']} ms/token")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -26,11 +26,34 @@ namespace {
 constexpr int kBiipThreads = 256;
 constexpr int kBiipChunk = 2048;  // elements per workgroup: whole blocks (block_size divides it)
 
+// Up to three rotations of one x (their own sign / scale / output), one per
+// grid row: the q / k / v or gate / up projections of a rotated layer.
+struct RotSets {
+    const float *scale[3];
+    const float *sign[3];
+    float *y[3];
+};
+
+__device__ void rotate_chunk(float *v, const float *x, float *y, int dim, const float *__restrict__ scale,
+                             const float *__restrict__ sign, int lg_bs, float inv_sqrt);
+
 __global__ __launch_bounds__(kBiipThreads) void biip_rotate_kernel(const float *x, float *y, int dim,
                                                                    const float *__restrict__ scale,
                                                                    const float *__restrict__ sign, int lg_bs,
                                                                    float inv_sqrt) {
     __shared__ float v[kBiipChunk];
+    rotate_chunk(v, x, y, dim, scale, sign, lg_bs, inv_sqrt);
+}
+
+__global__ __launch_bounds__(kBiipThreads) void biip_rotate_sets(const float *x, RotSets rs, int dim, int lg_bs,
+                                                                 float inv_sqrt) {
+    __shared__ float v[kBiipChunk];
+    const int k = blockIdx.y;
+    rotate_chunk(v, x, rs.y[k], dim, rs.scale[k], rs.sign[k], lg_bs, inv_sqrt);
+}
+
+__device__ void rotate_chunk(float *v, const float *x, float *y, int dim, const float *__restrict__ scale,
+                             const float *__restrict__ sign, int lg_bs, float inv_sqrt) {
     const int base = blockIdx.x * kBiipChunk;
     const int n = min(kBiipChunk, dim - base);  // a whole number of blocks
     for (int i = threadIdx.x; i < n; i += kBiipThreads) {
@@ -65,6 +88,26 @@ int launch_biip_rotate(const float *x, float *y, int dim, const float *scale, co
     const int grid = (dim + kBiipChunk - 1) / kBiipChunk;
     hipLaunchKernelGGL(biip_rotate_kernel, dim3(grid), dim3(kBiipThreads), 0, stream, x, y, dim, scale, sign, lg,
                        inv_sqrt);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+int launch_biip_rotate_n(int n, const float *x, float *const *y, int dim, const float *const *scale,
+                         const float *const *sign, int block_size, hipStream_t stream) {
+    if (n < 1 || n > 3 || dim < 1 || block_size < 1 || (block_size & (block_size - 1)) || block_size > kBiipChunk ||
+        dim % block_size)
+        return kBadShape;
+    int lg = 0;
+    while ((1 << lg) < block_size) ++lg;
+    const float inv_sqrt = 1.0f / std::sqrt(static_cast<float>(block_size));
+    RotSets rs{};
+    for (int k = 0; k < n; ++k) {
+        if (!sign[k] || !y[k]) return kBadShape;
+        rs.scale[k] = scale[k];
+        rs.sign[k] = sign[k];
+        rs.y[k] = y[k];
+    }
+    const int grid = (dim + kBiipChunk - 1) / kBiipChunk;
+    hipLaunchKernelGGL(biip_rotate_sets, dim3(grid, n), dim3(kBiipThreads), 0, stream, x, rs, dim, lg, inv_sqrt);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 

@@ -412,6 +412,7 @@ struct Engine {
     float *hidden = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr,
           *o = nullptr, *gate = nullptr, *up = nullptr, *ffn = nullptr, *logits = nullptr, *kv = nullptr,
           *amax_v = nullptr, *rotbuf = nullptr;
+    size_t rotbuf_floats = 0;
     int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next
     int *host_io = nullptr;                     // pinned mirror of dev_io
     size_t layer_stride = 0;                    // floats per layer and plane: n_kv_heads * max_seq * head_dim
@@ -439,6 +440,27 @@ int mvr(const Engine &e, const uint8_t *w, int dtype, const float *x, float *y, 
     return mv(e, w, dtype, x, y, M, K, s);
 }
 
+// Projections of one x that all carry a rotation with the same block: the n
+// rotations in one launch (into rotbuf, rotset_stride apart), then the n matvecs
+// (one group launch for i4). kNotFused when the rotations differ in presence
+// or block, or rotbuf cannot hold n copies.
+int mv_rotated_set(const Engine &e, int n, const uint8_t *const *w, float *const *y, const int *m, int K,
+                   const Rot *const *r, hipStream_t s) {
+    if (static_cast<size_t>(n) * K > e.rotbuf_floats) return kNotFused;
+    for (int j = 0; j < n; ++j)
+        if (!r[j]->sign || r[j]->bs != r[0]->bs) return kNotFused;
+    float *xr[3];
+    const float *sc[3], *sg[3];
+    for (int j = 0; j < n; ++j) {
+        xr[j] = e.rotbuf + static_cast<size_t>(j) * K;
+        sc[j] = r[j]->scale;
+        sg[j] = r[j]->sign;
+    }
+    int st = launch_biip_rotate_n(n, e.normed, xr, K, sc, sg, r[0]->bs, s);
+    for (int j = 0; j < n && st == kOk; ++j) st = mv(e, w[j], e.pd, xr[j], y[j], m[j], K, s);
+    return st;
+}
+
 int forward(Engine &e) {
     hipStream_t s = e.stream;
     const int H = e.c.hidden_size, I = e.c.intermediate_size;
@@ -459,6 +481,8 @@ int forward(Engine &e) {
         const Rot *r3[3] = {&L.rq, &L.rk, &L.rv};
         if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
+        } else if ((st = mv_rotated_set(e, 3, w3, y3, d3, H, r3, s)) != kNotFused) {
+            if (st != kOk) return st;
         } else {
             for (int j = 0; j < 3; ++j)
                 if ((st = mvr(e, w3[j], e.pd, e.normed, y3[j], d3[j], H, *r3[j], s)) != kOk) return st;
@@ -476,6 +500,8 @@ int forward(Engine &e) {
         const Rot *r2[2] = {&L.rg, &L.ru};
         if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(2, w2, y2, d2, e.normed, H, e.gs, s)) != kOk) return st;
+        } else if ((st = mv_rotated_set(e, 2, w2, y2, d2, H, r2, s)) != kNotFused) {
+            if (st != kOk) return st;
         } else {
             for (int j = 0; j < 2; ++j)
                 if ((st = mvr(e, w2[j], e.pd, e.normed, y2[j], d2[j], H, *r2[j], s)) != kOk) return st;
@@ -675,7 +701,7 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
                              static_cast<size_t>(e->kv_dim), static_cast<size_t>(e->q_dim), H, I, I, H, V,
                              2 * static_cast<size_t>(c.n_layers) * e->layer_stride,
                              static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 4,
-                             f16_floats, std::max<size_t>(std::max<size_t>(H, I), e->q_dim)};
+                             f16_floats, std::max<size_t>(std::max<size_t>(3 * H, I), e->q_dim)};
     float **slots[] = {&e->hidden, &e->normed, &e->q, &e->k, &e->v, &e->attn, &e->o, &e->gate, &e->up, &e->ffn,
                        &e->logits, &e->kv, &e->amax_v};
     size_t offs[17], total = 0;
@@ -699,6 +725,7 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         return kHipFailed;
     }
     e->rotbuf = reinterpret_cast<float *>(base + offs[16]);
+    e->rotbuf_floats = counts[16];
     float *conv = reinterpret_cast<float *>(base + offs[15]);
     for (const F16Vec &f : f16s) {
         f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);

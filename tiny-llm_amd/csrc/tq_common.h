@@ -51,6 +51,7 @@ enum Status : int {
     kLaunchFailed = -4,  // hipGetLastError after the launch was not hipSuccess
     kBadFile = -5,       // a .tqwen file was unreadable, invalid or of an unsupported kind
     kHipFailed = -6,     // a HIP allocation or copy failed
+    kNotFused = 1,       // a fused path does not apply to these operands; nothing was launched
 };
 
 // Device-pointer launchers (defined in the .hip files). All return a Status.
@@ -66,6 +67,9 @@ int launch_i4_embed_rows(const uint8_t *embed, const int *rows, int n, int dim, 
                          hipStream_t stream);
 int launch_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,
                        hipStream_t stream);
+// n (1..3) rotations of one x with their own scale (may be null) / sign / output, one launch.
+int launch_biip_rotate_n(int n, const float *x, float *const *y, int dim, const float *const *scale,
+                         const float *const *sign, int block_size, hipStream_t stream);
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                      hipStream_t stream);
 
