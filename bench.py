@@ -541,7 +541,8 @@ def main():
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u4 codes x f32 activations (i8 MFMA, i32 accumulate, f32 epilogue)",
+        "vs_baseline": None, "dtype": "u4 codes x f32 activations (f32 VALU in the per-layer lane kernels; i8 MFMA, i32 "
+                 "accumulate, f32 epilogue in the wide matvecs)",
         "data": "synthetic (BASELINE distributions, seeded)",
         "pct_of_peak": round(100 * value / PEAK_GBS, 2),
         "us_per_layer_set": round(us_layer, 2),
