@@ -14,6 +14,14 @@
  * 2. Device-pointer entry points (suffix _dev). Same math on buffers already
  *    in HBM, launched asynchronously on `stream` (a hipStream_t; NULL = the
  *    default stream). They return 0 or a negative TQHIP_E* code and never abort.
+ *    Scratch: some launches need library-owned device scratch (the split-K
+ *    matvec's exchange slots, the prefill GEMM's fp16 copy of X). Each
+ *    (device, stream) has its own, grown on demand between launches (the
+ *    stream is synchronised first), so calls on different streams never share
+ *    it. Under the caller's own stream capture nothing is allocated: a call
+ *    that would need more scratch than the stream already has returns
+ *    TQHIP_EHIP (run it once eagerly on that stream first), and scratch that a
+ *    capture recorded is never freed, so the caller's graph stays valid.
  *
  * 3. Registry. The library carries its own copy of the reference registry for
  *    these families (same names and behaviour, C++ namespace tinyqwen,
@@ -175,9 +183,12 @@ int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream);
 int tqhip_run_ops_timed(const tqhip_op *ops, int n_ops, int repeats, void *stream, float *op_ms);
 /* The op list captured into a HIP graph on `stream` (a created stream, not the
  * null stream) after one eager pass over it, for replay by
- * tqhip_ops_graph_launch. Replays read the buffers the ops name at replay time,
- * and must go to the same stream (the split-K scratch of that stream is part
- * of the graph). No counterpart in the reference, whose runtime calls the
+ * tqhip_ops_graph_launch. Replays read the buffers the ops name at replay time.
+ * The graph owns its scratch (allocated by the eager pass, freed by destroy), so
+ * later calls on any stream cannot disturb a replay, and a replay may go to any
+ * stream; replays of one graph are ordered among themselves (HIP orders the
+ * launches of one executable graph), and destroy waits for the device before
+ * freeing the scratch. No counterpart in the reference, whose runtime calls the
  * registry functions one by one: this is for device-resident decode loops,
  * where it cuts the per-kernel launch cost (about 2.8 -> 1.6 us on MI355X). */
 int tqhip_ops_graph_create(const tqhip_op *ops, int n_ops, void *stream, void **graph_out);

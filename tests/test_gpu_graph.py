@@ -85,3 +85,79 @@ def test_graph_replays_match_eager_runs(gpu, orc):
         assert rel_l2(want["vq2"], ref) <= 1e-5, "vq2"
     finally:
         graph.close()
+
+
+def test_graph_scratch_survives_larger_eager_calls(gpu, orc):
+    """A graph owns its scratch: after it is captured, eager calls that grow the stream's
+    own scratch (a 512-token prefill, split-K matvecs) on the capture stream and on
+    another stream cannot move or free what the replay uses. Every replay, on the capture
+    stream or on another one, equals the eager run before it bit for bit."""
+    K, NT = 896, 7
+    w_mm = gpu.synth_i4(300, K, G, seed=500)
+    w_sp = gpu.synth_i4(2560, 4096, G, seed=501)  # split-K over two parts
+    d_mm, d_sp = gpu.DeviceBuffer.from_array(w_mm), gpu.DeviceBuffer.from_array(w_sp)
+    x_mm = gpu.synth_normal(K * NT, seed=502)
+    x_sp = gpu.synth_normal(4096, seed=503)
+    dx_mm, dx_sp = gpu.DeviceBuffer.from_array(x_mm), gpu.DeviceBuffer.from_array(x_sp)
+    dy_mm, dy_sp = gpu.DeviceBuffer(4 * 300 * NT), gpu.DeviceBuffer(4 * 2560)
+    Op = gpu.Op
+    ops = [Op(gpu.OP_I4_MATMUL, d_mm.ptr, dx_mm.ptr, dy_mm.ptr, 300, K, NT, G, None, None, None, None, 0),
+           Op(gpu.OP_I4_MATVEC, d_sp.ptr, dx_sp.ptr, dy_sp.ptr, 2560, 4096, 1, G, None, None, None, None, 0)]
+    # large eager work: a 512-token prefill (2.6 MB of X scratch) and a wider split-K matvec
+    Mb, Kb, Nb = 9728, 2560, 512
+    w_big = gpu.synth_i4(Mb, Kb, G, seed=504)
+    d_big = gpu.DeviceBuffer.from_array(w_big)
+    dx_big = gpu.DeviceBuffer.from_array(gpu.synth_normal(Kb * Nb, seed=505))
+    dy_big = gpu.DeviceBuffer(4 * Mb * Nb)
+    w_sp2 = gpu.synth_i4(4096, 9728, G, seed=506)
+    d_sp2 = gpu.DeviceBuffer.from_array(w_sp2)
+    dx_sp2, dy_sp2 = gpu.DeviceBuffer.from_array(gpu.synth_normal(9728, seed=507)), gpu.DeviceBuffer(4 * 4096)
+    big = [Op(gpu.OP_I4_MATMUL, d_big.ptr, dx_big.ptr, dy_big.ptr, Mb, Kb, Nb, G, None, None, None, None, 0),
+           Op(gpu.OP_I4_MATVEC, d_sp2.ptr, dx_sp2.ptr, dy_sp2.ptr, 4096, 9728, 1, G, None, None, None, None, 0)]
+
+    s1, s2 = gpu.Stream(), gpu.Stream()
+    graph = gpu.OpsGraph(ops, s1)
+    try:
+        gpu.run_ops(ops, 1, s1)
+        s1.synchronize()
+        want_mm, want_sp = dy_mm.download(np.float32, 300 * NT), dy_sp.download(np.float32, 2560)
+        ref = orc.matmul_i4(w_mm, x_mm, 300, K, NT, G, threads=16)
+        assert rel_l2(want_mm, ref) <= 2e-3 and max_abs_rel(want_mm, ref) <= 1e-3
+        ref = orc.matvec_i4(w_sp, x_sp, 2560, 4096, G, threads=16)
+        assert rel_l2(want_sp, ref) <= 1e-5 and max_abs_rel(want_sp, ref) <= 1e-3
+        for rep, stream in enumerate((s1, s2, s1)):
+            gpu.run_ops(big, 1, s1)  # grows the capture stream's own scratch
+            gpu.run_ops(big, 1, s2)
+            s1.synchronize()
+            s2.synchronize()
+            for b, n in ((dy_mm, 300 * NT), (dy_sp, 2560)):
+                gpu.lib().tqhip_memset(b.ptr, 0xFF, 4 * n)
+            graph.launch(stream)
+            stream.synchronize()
+            assert np.array_equal(dy_mm.download(np.float32, 300 * NT), want_mm), f"replay {rep}: prefill"
+            assert np.array_equal(dy_sp.download(np.float32, 2560), want_sp), f"replay {rep}: split-K"
+    finally:
+        graph.close()
+
+
+def test_prefill_on_two_streams_at_once(gpu, orc):
+    """Two prefill GEMMs in flight together on two streams: each stream has its own fp16
+    copy of X, so neither sees the other's activations."""
+    G_ = 64
+    cases = [(512, 896, 40, 600), (384, 640, 24, 601)]
+    streams = [gpu.Stream(), gpu.Stream()]
+    bufs = []
+    for (M, K, N, seed), s in zip(cases, streams):
+        w = gpu.synth_i4(M, K, G_, seed=seed)
+        x = gpu.synth_normal(K * N, seed=seed + 50)
+        dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M * N)
+        bufs.append((w, x, dw, dx, dy))
+    for rep in range(3):
+        for (M, K, N, _), (w, x, dw, dx, dy), s in zip(cases, bufs, streams):
+            gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G_, stream=s)  # no synchronisation between the two
+        for s in streams:
+            s.synchronize()
+        for (M, K, N, _), (w, x, dw, dx, dy) in zip(cases, bufs):
+            got = dy.download(np.float32, M * N)
+            ref = orc.matmul_i4(w, x, M, K, N, G_, threads=16)
+            assert rel_l2(got, ref) <= 2e-3 and max_abs_rel(got, ref) <= 1e-3, (rep, M, K, N)

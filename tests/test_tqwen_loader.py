@@ -322,3 +322,23 @@ def test_missing_file_and_find(tqa, tmp_path):
         assert tuple(info.shape[:len(t["shape"])]) == t["shape"]
         assert bytes(img[info.offset:info.offset + info.nbytes]) == t["data"]
     assert m.quant_group_size == 64 and m.dtype == tf.I4
+
+
+def test_close_refused_while_an_engine_is_open(tqa, tmp_path):
+    """ModelFile.close() frees the HBM copy a DecodeEngine's captured step reads: the binding
+    refuses it while an engine built on the model is open. (No GPU: the engine here is a
+    stand-in object registered the way DecodeEngine.__init__ registers itself.)"""
+    import weakref
+    img, _ = tf.i4_model(group_size=64, hidden=128, inter=256, vocab=100)
+    m = tqa.ModelFile(write(tmp_path, img))
+    eng = tqa.DecodeEngine.__new__(tqa.DecodeEngine)
+    eng._h = 12345  # an open handle (never passed to the library here)
+    m._engines = weakref.WeakSet([eng])
+    with pytest.raises(RuntimeError, match="still use this model"):
+        m.close()
+    assert m._h
+    eng._h = None  # the engine was closed
+    m.close()
+    assert m._h is None
+    with pytest.raises(ValueError, match="closed"):
+        tqa.DecodeEngine(m)

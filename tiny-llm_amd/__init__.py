@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 
 import numpy as np
 
@@ -175,7 +176,9 @@ def _stream(s):
     return s.ptr if isinstance(s, Stream) else int(s)
 
 
-def _ptr(a) -> int:
+def _ptr(a) -> "int | None":
+    if a is None:
+        return None  # a NULL pointer (calls that are refused before they touch it)
     if isinstance(a, DeviceBuffer):
         return a.ptr
     if isinstance(a, np.ndarray):
@@ -401,6 +404,7 @@ def matmul_i4_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None)
            "tqhip_matmul_i4_dev")
 
 
+
 class Stream:
     def __init__(self):
         p = lib().tqhip_stream_create()
@@ -449,7 +453,8 @@ def run_ops(ops: list, repeats: int, stream: "Stream | None" = None) -> None:
 
 class OpsGraph:
     """An op list captured into a HIP graph (tqhip_ops_graph_create) on a created
-    stream, replayed with launch() on that stream."""
+    stream, replayed with launch() on that stream or on another one (the graph
+    owns its scratch)."""
 
     def __init__(self, ops: list, stream: "Stream"):
         self._arr = (Op * len(ops))(*ops)
@@ -459,8 +464,8 @@ class OpsGraph:
                "tqhip_ops_graph_create")
         self._h = h
 
-    def launch(self) -> None:
-        _check(lib().tqhip_ops_graph_launch(self._h, _stream(self._stream)), "tqhip_ops_graph_launch")
+    def launch(self, stream: "Stream | None" = None) -> None:
+        _check(lib().tqhip_ops_graph_launch(self._h, _stream(stream or self._stream)), "tqhip_ops_graph_launch")
 
     def close(self) -> None:
         if self._h:
@@ -557,7 +562,13 @@ class ModelFile:
         return int(lib().tqhip_model_type(self._h))
 
     def close(self) -> None:
+        """Frees the handle and the HBM copy. Refused while a DecodeEngine built on this
+        model is open: its captured step graph reads the model's HBM copy."""
         if getattr(self, "_h", None):
+            live = [e for e in list(getattr(self, "_engines", ())) if getattr(e, "_h", None)]
+            if live:
+                raise RuntimeError(f"ModelFile.close(): {len(live)} DecodeEngine(s) still use this model; "
+                                   "close them first")
             lib().tqhip_model_free(self._h)
             self._h = None
 
@@ -574,6 +585,8 @@ class DecodeEngine:
     copies the last step's logits to the host, ``reset()`` returns to position 0."""
 
     def __init__(self, model: ModelFile, max_seq_len: int = 0):
+        if not getattr(model, "_h", None):
+            raise ValueError("DecodeEngine: the ModelFile is closed")
         handle = _vp()
         err = ctypes.create_string_buffer(512)
         rc = lib().tqhip_decode_create(model._h, max_seq_len, err, len(err), ctypes.byref(handle))
@@ -581,6 +594,9 @@ class DecodeEngine:
             raise ValueError(err.value.decode(errors="replace") or f"tqhip_decode_create failed ({rc})")
         self._h = handle.value
         self._model = model  # the engine reads the model's HBM copy
+        if not hasattr(model, "_engines"):
+            model._engines = weakref.WeakSet()
+        model._engines.add(self)  # ModelFile.close() refuses while this engine is open
         self.vocab = model.config.vocab_size
 
     def step(self, token: int) -> int:

@@ -338,7 +338,10 @@ void *tqhip_stream_create(void) {
     return hipStreamCreate(&s) == hipSuccess ? static_cast<void *>(s) : nullptr;
 }
 int tqhip_stream_destroy(void *stream) {
-    return hipStreamDestroy(static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (hipStreamSynchronize(s) != hipSuccess) return -1;
+    scratch_forget_stream(s);  // its scratch, unless a graph recorded it
+    return hipStreamDestroy(s) == hipSuccess ? 0 : -1;
 }
 int tqhip_stream_synchronize(void *stream) {
     return hipStreamSynchronize(static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -1;
@@ -418,36 +421,47 @@ int tqhip_run_ops_timed(const tqhip_op *ops, int n_ops, int repeats, void *strea
 // decode loop issues the same calls every token with the same buffers, and a
 // replay costs the GPU about 1.6 us per kernel instead of about 2.8 us for
 // separate launches (measured on MI355X).
+// The graph owns its scratch (split-K slots, prefill X copy): the eager sizing
+// pass and the capture run inside a ScratchScope of that set, so no later call
+// on any stream can grow, free or share what the replays use.
 struct tqhip_ops_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    ScratchSet *scratch = nullptr;
 };
 
 int tqhip_ops_graph_create(const tqhip_op *ops, int n_ops, void *stream, void **graph_out) {
     if (!graph_out || n_ops < 1 || !stream) return kBadShape;  // (the null stream cannot be captured)
     *graph_out = nullptr;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // One eager pass first: it allocates the per-stream scratch and sets kernel
-    // attributes, neither of which may happen inside a capture.
-    int st = tqhip_run_ops(ops, n_ops, 1, stream);
-    if (st != kOk) return st;
-    if (hipStreamSynchronize(s) != hipSuccess) return kLaunchFailed;
-    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return kLaunchFailed;
-    for (int i = 0; i < n_ops && st == kOk; ++i) st = launch_op(ops[i], s);
+    ScratchSet *scratch = scratch_set_new();
     hipGraph_t g = nullptr;
-    const hipError_t end = hipStreamEndCapture(s, &g);
-    if (st != kOk || end != hipSuccess) {
-        if (g) (void)hipGraphDestroy(g);
-        return st != kOk ? st : kLaunchFailed;
+    int st = kOk;
+    {
+        ScratchScope scope(scratch);
+        // One eager pass first: it sizes the graph's scratch and sets kernel
+        // attributes, neither of which may happen inside a capture.
+        st = tqhip_run_ops(ops, n_ops, 1, stream);
+        if (st == kOk && hipStreamSynchronize(s) != hipSuccess) st = kLaunchFailed;
+        if (st == kOk && hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) st = kLaunchFailed;
+        if (st == kOk) {
+            for (int i = 0; i < n_ops && st == kOk; ++i) st = launch_op(ops[i], s);
+            const hipError_t end = hipStreamEndCapture(s, &g);
+            if (st == kOk && end != hipSuccess) st = kLaunchFailed;
+        }
     }
     hipGraphExec_t exec = nullptr;
-    if (hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) {
-        (void)hipGraphDestroy(g);
-        return kLaunchFailed;
+    if (st == kOk && hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) st = kLaunchFailed;
+    if (st != kOk) {
+        if (g) (void)hipGraphDestroy(g);
+        (void)hipStreamSynchronize(s);
+        scratch_set_free(scratch);
+        return st;
     }
     auto *h = new tqhip_ops_graph;
     h->graph = g;
     h->exec = exec;
+    h->scratch = scratch;
     *graph_out = h;
     return kOk;
 }
@@ -464,6 +478,10 @@ int tqhip_ops_graph_destroy(void *graph) {
     int st = kOk;
     if (h->exec && hipGraphExecDestroy(h->exec) != hipSuccess) st = kLaunchFailed;
     if (h->graph && hipGraphDestroy(h->graph) != hipSuccess) st = kLaunchFailed;
+    // replays may still be running on any stream: wait for the device before
+    // the scratch they use goes back
+    if (hipDeviceSynchronize() != hipSuccess) st = kLaunchFailed;
+    scratch_set_free(h->scratch);
     delete h;
     return st;
 }

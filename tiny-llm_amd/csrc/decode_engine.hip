@@ -421,6 +421,7 @@ struct Engine {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool eager = false;  // TQHIP_DECODE_EAGER=1: launch the step kernel by kernel (for profilers)
+    ScratchSet *scratch = nullptr;  // the matvec launches' split-K slots: owned by the engine's graph
     int seq_len = 0;
 };
 
@@ -517,9 +518,16 @@ int forward(Engine &e) {
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
+int eager_forward(Engine &e) {
+    ScratchScope scope(e.scratch);
+    return forward(e);
+}
+
 void release(Engine *e) {
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
     if (e->exec) (void)hipGraphExecDestroy(e->exec);
     if (e->graph) (void)hipGraphDestroy(e->graph);
+    scratch_set_free(e->scratch);
     if (e->arena) (void)hipFree(e->arena);
     if (e->host_io) (void)hipHostFree(e->host_io);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -732,9 +740,10 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         *f.slot = conv;
         conv += (f.n + 63) / 64 * 64;
     }
-    // One eager pass at position 0 with token 0 sets up the matvec launches'
-    // per-stream scratch outside the capture; its KV rows are rewritten by the
-    // first real step.
+    // One eager pass at position 0 with token 0 sizes the engine's scratch
+    // outside the capture; its KV rows are rewritten by the first real step.
+    e->scratch = scratch_set_new();
+    ScratchScope scope(e->scratch);
     int rc = forward(*e);
     if (rc == kOk && hipStreamSynchronize(e->stream) != hipSuccess) rc = kLaunchFailed;
     const char *eager = std::getenv("TQHIP_DECODE_EAGER");
@@ -788,7 +797,7 @@ int tqhip_decode_step(void *engine, int token_id) {
     e->host_io[0] = e->seq_len;
     e->host_io[1] = token_id;
     if (hipMemcpyAsync(e->dev_io, e->host_io, 2 * sizeof(int), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
-        (e->eager ? forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) ||
+        (e->eager ? eager_forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) ||
         hipMemcpyAsync(e->host_io + 2, e->dev_io + 2, sizeof(int), hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
         hipStreamSynchronize(e->stream) != hipSuccess)
         return kLaunchFailed;

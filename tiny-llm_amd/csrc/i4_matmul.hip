@@ -25,7 +25,6 @@
 
 #include <algorithm>
 #include <type_traits>
-#include <mutex>
 
 namespace tqhip {
 namespace {
@@ -637,31 +636,16 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
     }
 }
 
-// Grow-only device workspace for the fp16 copy of X (one per process; the
-// launches that use it are ordered on their streams by the caller).
-struct Workspace {
-    std::mutex mu;
-    void *ptr = nullptr;
-    size_t bytes = 0;
-};
-Workspace &workspace() {
-    static Workspace ws;
-    return ws;
-}
-
-void *workspace_at_least(size_t bytes) {
-    Workspace &ws = workspace();
-    std::lock_guard<std::mutex> lock(ws.mu);
-    if (ws.bytes < bytes) {
-        if (ws.ptr) {
-            TQ_HIP_CHECK(hipDeviceSynchronize());  // earlier launches may still read it
-            TQ_HIP_CHECK(hipFree(ws.ptr));
-        }
-        const size_t want = std::max(bytes, ws.bytes * 2);
-        TQ_HIP_CHECK(hipMalloc(&ws.ptr, want));
-        ws.bytes = want;
-    }
-    return ws.ptr;
+// Raises fn's dynamic-LDS limit to what the CU's 160 KB leaves beside its static LDS
+// (once per kernel; `limit` caches the figure).
+int raise_lds_limit(const void *fn, size_t &limit) {
+    hipFuncAttributes attr{};
+    if (hipFuncGetAttributes(&attr, fn) != hipSuccess || attr.sharedSizeBytes >= 160 * 1024) return kLaunchFailed;
+    const size_t cap = 160 * 1024 - attr.sharedSizeBytes;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(cap)) != hipSuccess)
+        return kLaunchFailed;
+    limit = cap;
+    return kOk;
 }
 
 template <int WM, int WN, int GT>
@@ -674,11 +658,8 @@ int launch_tiles(const uint8_t *w, const _Float16 *xh, const float *xinv, float 
     static size_t limit = 0;  // dynamic LDS the kernel may take (0: not raised from the default 64 KB yet)
     if (lds > 64 * 1024 && limit == 0) {
         // what the CU's 160 KB leaves beside the kernel's static LDS
-        hipFuncAttributes attr{};
         const void *fn = reinterpret_cast<const void *>(i4_matmul_mfma<WM, WN, GT>);
-        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
-        limit = 160 * 1024 - attr.sharedSizeBytes;
-        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(limit)));
+        if (raise_lds_limit(fn, limit) != kOk) return kLaunchFailed;
     }
     if (lds > 64 * 1024 && lds > limit) return kTooLarge;
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
@@ -694,11 +675,8 @@ int launch_tiles2(const uint8_t *w, const _Float16 *xh, const float *xinv, float
     const size_t lds = static_cast<size_t>(S) * (kWSlots * kBM * 4 + BN * 128);
     static size_t limit = 0;
     if (lds > 64 * 1024 && limit == 0) {
-        hipFuncAttributes attr{};
         const void *fn = reinterpret_cast<const void *>(i4_matmul_mfma2<WN, GT, S>);
-        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
-        limit = 160 * 1024 - attr.sharedSizeBytes;
-        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(limit)));
+        if (raise_lds_limit(fn, limit) != kOk) return kLaunchFailed;
     }
     if (lds > 64 * 1024 && lds > limit) return kTooLarge;
     // row offsets of the 128 staged rows and token-row offsets must fit the 32-bit DMA offsets
@@ -716,11 +694,8 @@ int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y
     const size_t lds = static_cast<size_t>(S) * BN * 128;
     static size_t limit = 0;
     if (lds > 64 * 1024 && limit == 0) {
-        hipFuncAttributes attr{};
         const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WN, S, NWV>);
-        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
-        limit = 160 * 1024 - attr.sharedSizeBytes;
-        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(limit)));
+        if (raise_lds_limit(fn, limit) != kOk) return kLaunchFailed;
     }
     if (lds > 64 * 1024 && lds > limit) return kTooLarge;
     if (static_cast<size_t>(BM) * rb + static_cast<size_t>(Kp) * 2 * BN >= (1ull << 31)) return kTooLarge;
@@ -736,25 +711,30 @@ int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y
 // workgroups, more registers).
 int pick_wn(int N) { return N <= 32 ? 1 : N <= 128 ? 2 : 3; }
 
-}  // namespace
+// The MFMA path applies: a group size that is a multiple of 32 and byte offsets within 31 bits.
+bool mfma_applies(int M, int K, int N, int group_size) {
+    const size_t Kp = (static_cast<size_t>(K) + kStepK - 1) / kStepK * kStepK;
+    return group_size % 32 == 0 && i4_row_bytes(K, group_size) * static_cast<size_t>(M) < (1ull << 31) &&
+           Kp * 2 * static_cast<size_t>(N) < (1ull << 31);
+}
 
-int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
-                     hipStream_t stream) {
-    if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+// Other shapes: one matvec per token column.
+int matmul_by_columns(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                      hipStream_t stream) {
+    for (int n = 0; n < N; ++n) {
+        const int st = launch_i4_matvec(w, x + static_cast<size_t>(n) * K, y + static_cast<size_t>(n) * M, M, K,
+                                        group_size, stream);
+        if (st != kOk) return st;
+    }
+    return kOk;
+}
+
+// The MFMA path with X's fp16 copy and per-token scales at ws (prefill_scratch_bytes(K, N) bytes).
+int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size, unsigned char *ws,
+                hipStream_t stream) {
     const size_t rb = i4_row_bytes(K, group_size);
     const size_t Kp = (static_cast<size_t>(K) + kStepK - 1) / kStepK * kStepK;
-    const bool mfma = group_size % 32 == 0 && rb * static_cast<size_t>(M) < (1ull << 31) &&
-                      Kp * 2 * static_cast<size_t>(N) < (1ull << 31);
-    if (!mfma) {
-        for (int n = 0; n < N; ++n) {
-            const int st = launch_i4_matvec(w, x + static_cast<size_t>(n) * K, y + static_cast<size_t>(n) * M, M, K,
-                                            group_size, stream);
-            if (st != kOk) return st;
-        }
-        return kOk;
-    }
     const size_t xh_bytes = (Kp * 2 * N + 255) / 256 * 256;
-    unsigned char *ws = static_cast<unsigned char *>(workspace_at_least(xh_bytes + 4 * static_cast<size_t>(N)));
     _Float16 *xh = reinterpret_cast<_Float16 *>(ws);
     float *xinv = reinterpret_cast<float *>(ws + xh_bytes);
     if (Kp <= static_cast<size_t>(256 * kXRegs))
@@ -789,6 +769,18 @@ int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, i
     if (wn == 1) return launch_tiles<1, 1, 0>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
     if (wn == 2) return launch_tiles<1, 2, 0>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
     return launch_tiles<1, 3, 0>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
+}
+
+}  // namespace
+
+int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                     hipStream_t stream) {
+    if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+    if (!mfma_applies(M, K, N, group_size)) return matmul_by_columns(w, x, y, M, K, N, group_size, stream);
+    void *ws = nullptr;
+    const int st = scratch_prefill(stream, prefill_scratch_bytes(K, N), &ws);  // the stream's (or scope's) buffer
+    if (st != kOk) return st;
+    return matmul_mfma(w, x, y, M, K, N, group_size, static_cast<unsigned char *>(ws), stream);
 }
 
 }  // namespace tqhip

@@ -34,8 +34,6 @@
 #include "tq_common.h"
 
 #include <algorithm>
-#include <mutex>
-#include <unordered_map>
 
 namespace tqhip {
 namespace {
@@ -1718,10 +1716,11 @@ __global__ __launch_bounds__(256) void i4_matvec_rowwave(const uint8_t *__restri
 int device_cus() {
     static int cus = 0;
     if (cus == 0) {
-        int dev = 0;
-        TQ_HIP_CHECK(hipGetDevice(&dev));
-        TQ_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        if (cus < 1) cus = 1;
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            return 1;  // no device: whatever is launched next fails and reports it
+        cus = n;
     }
     return cus;
 }
@@ -1733,10 +1732,11 @@ int fit_dynamic_lds(const void *fn, size_t lds, size_t &limit) {
     if (lds <= 64 * 1024) return kOk;
     if (limit == 0) {
         hipFuncAttributes attr{};
-        TQ_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
+        if (hipFuncGetAttributes(&attr, fn) != hipSuccess) return kLaunchFailed;
         if (attr.sharedSizeBytes >= static_cast<size_t>(kLdsBytes)) return kTooLarge;
         const size_t cap = kLdsBytes - attr.sharedSizeBytes;
-        TQ_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(cap)));
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(cap)) != hipSuccess)
+            return kLaunchFailed;
         limit = cap;
     }
     return lds <= limit ? kOk : kTooLarge;
@@ -1872,32 +1872,6 @@ int launch_lds(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX, DEPTH>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, limit);
 }
 
-// Per-stream scratch of the split-K kernel: the exchange slots of every tile,
-// empty (zero) between launches. Launches on one stream are ordered; launches
-// on different streams get different buffers.
-struct SplitScratch {
-    unsigned long long *slots = nullptr;
-    size_t cap = 0;
-};
-std::mutex g_split_mu;
-std::unordered_map<hipStream_t, SplitScratch> g_split;
-
-int split_scratch(hipStream_t stream, size_t nslots, unsigned long long **slots) {
-    std::lock_guard<std::mutex> lock(g_split_mu);
-    SplitScratch &sc = g_split[stream];
-    if (sc.cap < nslots) {
-        if (hipStreamSynchronize(stream) != hipSuccess) return kLaunchFailed;  // earlier launches may still use it
-        if (sc.slots) (void)hipFree(sc.slots);
-        sc = SplitScratch{};
-        const size_t n = std::max(nslots, static_cast<size_t>(1) << 14);
-        if (hipMalloc(&sc.slots, n * sizeof(unsigned long long)) != hipSuccess) return kLaunchFailed;
-        if (hipMemset(sc.slots, 0, n * sizeof(unsigned long long)) != hipSuccess) return kLaunchFailed;
-        sc.cap = n;
-    }
-    *slots = sc.slots;
-    return kOk;
-}
-
 template <int GT, int CPW, int PW, int NWMAX>
 int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int Tmax, hipStream_t stream) {
     static size_t limit = 0;
@@ -1912,7 +1886,7 @@ int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int
     if (lds > kLdsBytes) return kTooLarge;
     if (S < 2 || S > 4) return kTooLarge;  // the exchange tree has two levels
     unsigned long long *slots = nullptr;
-    const int st = split_scratch(stream, static_cast<size_t>(tiles) * 3 * kTile, &slots);
+    const int st = scratch_split_slots(stream, static_cast<size_t>(tiles) * 3 * kTile, &slots);
     if (st != kOk) return st;
     const int fit = fit_dynamic_lds(reinterpret_cast<const void *>(i4_matvec_split<GT, CPW, PW, NWMAX>), lds, limit);
     if (fit != kOk) return fit;

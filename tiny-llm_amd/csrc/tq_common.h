@@ -72,5 +72,39 @@ int launch_biip_rotate_n(int n, const float *x, float *const *y, int dim, const 
                          const float *const *sign, int block_size, hipStream_t stream);
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                      hipStream_t stream);
+// Bytes of prefill scratch (fp16 X rows padded to 64 elements, 256-byte aligned, then one
+// float per token) a matmul of K x N takes.
+inline size_t prefill_scratch_bytes(int K, int N) {
+    const size_t Kp = (static_cast<size_t>(K) + 63) / 64 * 64;
+    return (Kp * 2 * static_cast<size_t>(N) + 255) / 256 * 256 + 4 * static_cast<size_t>(N);
+}
+
+// ---- scratch memory (scratch.cpp) ---------------------------------------------------------
+// Split-K exchange slots (zero between launches) and the prefill X workspace. Eager
+// launches use the set of their (device, stream); inside a ScratchScope (graph capture,
+// decode engine) the scope's set. Growth under stream capture fails with kHipFailed;
+// a fixed set answers a request beyond its preset buffers with kTooLarge.
+struct ScratchSet;
+int scratch_split_slots(hipStream_t s, size_t nslots, unsigned long long **slots);
+int scratch_prefill(hipStream_t s, size_t bytes, void **ws);
+ScratchSet *scratch_set_new();
+ScratchSet *scratch_set_fixed(void *xws, size_t xws_bytes);
+void scratch_set_free(ScratchSet *set);  // the caller has synchronised every launch that used it
+void scratch_forget_stream(hipStream_t s);  // the stream is being destroyed (synchronised)
+class ScratchScope {
+  public:
+    explicit ScratchScope(ScratchSet *set);
+    ~ScratchScope();
+    ScratchScope(const ScratchScope &) = delete;
+    ScratchScope &operator=(const ScratchScope &) = delete;
+
+  private:
+    ScratchSet *prev_;
+};
+struct ScratchStats {
+    size_t split_bytes, prefill_bytes;
+    int split_captured, prefill_captured, retired;
+};
+ScratchStats scratch_stats(hipStream_t s);  // the set a launch on s would use now
 
 }  // namespace tqhip

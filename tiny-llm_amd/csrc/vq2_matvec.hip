@@ -237,10 +237,11 @@ __global__ __launch_bounds__(64 * kVq2Waves) void vq2_matvec_copies(const uint8_
 int device_cus_vq2() {
     static int cus = 0;
     if (cus == 0) {
-        int dev = 0;
-        TQ_HIP_CHECK(hipGetDevice(&dev));
-        TQ_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        if (cus < 1) cus = 1;
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            return 1;  // no device: the launch that follows fails and reports it
+        cus = n;
     }
     return cus;
 }
