@@ -51,6 +51,7 @@ extern "C" {
 #define TQHIP_ELAUNCH (-4)      /* the kernel launch failed */
 #define TQHIP_EFILE (-5)        /* a .tqwen file was unreadable, invalid or of an unsupported kind */
 #define TQHIP_EHIP (-6)         /* a HIP allocation or copy failed */
+#define TQHIP_ENOSCRATCH (-7)   /* tqhip_matmul_i4_noalloc_dev: the call needs more than the static scratch */
 
 /* ---- 1. host-pointer entry points (the "hip" variants) ------------------ */
 
@@ -95,6 +96,20 @@ int tqhip_matvec_qkv_i4_dev(const uint8_t *wq, const uint8_t *wk, const uint8_t 
                             float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size, void *stream);
 int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                         void *stream);
+/* tqhip_matmul_i4_dev without any allocation. No counterpart in the reference: this is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same kernels and results as
+ * tqhip_matmul_i4_dev, bit for bit. X's fp16 copy and the per-token scales go to a
+ * static device array of TQHIP_NOALLOC_SCRATCH_BYTES (16 MiB) that every GPU the library
+ * runs on holds until the process ends; a call needing more
+ * (((ceil(K/64)*64*2*N + 255) & ~255) + 4*N bytes, e.g. above 3274 tokens at K = 2560)
+ * returns TQHIP_ENOSCRATCH before launching anything. Group sizes that are not a
+ * multiple of 32 run one matvec per token, with kernels that need no scratch. All calls
+ * on one GPU share the array: calls that overlap on one GPU (two streams, or two host
+ * threads) race and must be ordered by the caller. */
+#define TQHIP_NOALLOC_SCRATCH_BYTES (16u << 20)
+int tqhip_matmul_i4_noalloc_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                                void *stream);
 /* Compact-i4 embedding lookup: out[t][0..dim) = dequant_i4_row(embed, rows[t],
  * dim, group_size, .) for t < n (kernels/ref_ops.h:183-205, called per prompt
  * token by runtime/qwen_forward_prefill.cpp:180); rows is a device array of

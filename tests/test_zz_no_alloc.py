@@ -1,0 +1,57 @@
+"""The allocation-free prefill entry point (tqhip_matmul_i4_noalloc_dev) against
+tqhip_matmul_i4_dev, through the C ABI.
+
+Both run the same kernels; the only difference is where X's fp16 copy lives (the
+library's static device array instead of a stream's grow-only buffer), so the
+outputs must agree bit for bit, call after call, with the second call of each
+pair smaller than the first (the array keeps the previous call's contents). The
+results are also held to the prefill bar against the oracle, and a call that
+needs more than the static array is refused before anything is launched.
+"""
+import numpy as np
+import pytest
+
+from conftest import max_abs_rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def run_pair(gpu, w, x, M, K, N, G, stream):
+    dw, dx = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x)
+    ya, yb = gpu.DeviceBuffer(4 * M * N), gpu.DeviceBuffer(4 * M * N)
+    gpu.lib().tqhip_memset(yb.ptr, 0xFF, 4 * M * N)  # the no-alloc call must write every output
+    gpu.matmul_i4_dev(dw, dx, ya, M, K, N, G, stream=stream)
+    st = gpu.matmul_i4_noalloc_dev(dw, dx, yb, M, K, N, G, stream=stream)
+    assert st == gpu.OK, st
+    stream.synchronize()
+    return ya.download(np.float32, M * N), yb.download(np.float32, M * N)
+
+
+@pytest.mark.parametrize("G", [64, 40])
+def test_noalloc_matches_dev_entry_point(gpu, orc, G):
+    stream = gpu.Stream()
+    # G = 64: the MFMA GEMM (512 tokens at K = 2560 uses 10.5 MB of the 16 MiB), then a
+    # smaller call over the same array; G = 40: one matvec per token column, no scratch.
+    cases = [(9728, 2560, 512), (896, 896, 40)] if G == 64 else [(640, 520, 9), (200, 280, 3)]
+    for i, (M, K, N) in enumerate(cases):
+        print(f"[no-alloc] G={G} call {i}: M={M} K={K} N={N}", flush=True)
+        w = gpu.synth_i4(M, K, G, seed=700 + 10 * i + G)
+        x = gpu.synth_normal(K * N, seed=701 + 10 * i + G)
+        want, got = run_pair(gpu, w, x, M, K, N, G, stream)
+        assert np.array_equal(got, want), f"call {i}: no-alloc result differs from tqhip_matmul_i4_dev"
+        if M * N <= 896 * 40:  # the oracle at sizes it finishes in seconds
+            ref = orc.matmul_i4(w, x, M, K, N, G, threads=16)
+        else:  # sampled rows of the 9728x2560x512 call
+            rows = np.arange(0, M, 97)
+            rb = gpu.i4_row_bytes(K, G)
+            wr = w.reshape(M, rb)[rows].ravel()
+            ref = orc.matmul_i4(wr, x, rows.size, K, N, G, threads=16)
+            got = got.reshape(N, M)[:, rows].ravel()
+        assert rel_l2(got, ref) <= 2e-3 and max_abs_rel(got, ref) <= 1e-3, i
+
+
+def test_noalloc_refuses_calls_beyond_the_static_array(gpu):
+    K = 2560
+    assert gpu.matmul_i4_noalloc_dev(None, None, None, 9728, K, 3275, 64) == gpu.ENOSCRATCH
+    assert gpu.matmul_i4_noalloc_dev(None, None, None, 9728, K, 100000, 64) == gpu.ENOSCRATCH
+    assert gpu.matmul_i4_noalloc_dev(None, None, None, 0, K, 8, 64) == gpu.EBADSHAPE

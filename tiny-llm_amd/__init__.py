@@ -21,7 +21,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtqhip.so")
 
-OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH, EFILE, EHIP = 0, -1, -2, -3, -4, -5, -6
+OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH, EFILE, EHIP, ENOSCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
+NOALLOC_SCRATCH_BYTES = 16 << 20  # TQHIP_NOALLOC_SCRATCH_BYTES
 OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV, OP_BIIP_ROTATE = 1, 2, 3, 4, 5, 6
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -69,6 +70,7 @@ _SIGS = {
     "tqhip_matvec_pair_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "tqhip_matvec_qkv_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matmul_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "tqhip_matmul_i4_noalloc_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_biip_rotate_dev": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp]),
     "tqhip_dequant_i4_rows_dev": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     # registry
@@ -403,6 +405,12 @@ def matmul_i4_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None)
     _check(lib().tqhip_matmul_i4_dev(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size, _stream(stream)),
            "tqhip_matmul_i4_dev")
 
+
+def matmul_i4_noalloc_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None) -> int:
+    """tqhip_matmul_i4_noalloc_dev: the prefill GEMM with X's fp16 copy in the library's static
+    device array (no allocation). Returns the status (ENOSCRATCH when the call needs more than
+    NOALLOC_SCRATCH_BYTES)."""
+    return int(lib().tqhip_matmul_i4_noalloc_dev(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size, _stream(stream)))
 
 
 class Stream:

@@ -266,6 +266,11 @@ int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K
                         void *stream) {
     return launch_i4_matmul(w, x, y, M, K, N, group_size, static_cast<hipStream_t>(stream));
 }
+int tqhip_matmul_i4_noalloc_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                                void *stream) {
+    static_assert(TQHIP_NOALLOC_SCRATCH_BYTES == kNoAllocScratchBytes, "header and library agree on the size");
+    return launch_i4_matmul_noalloc(w, x, y, M, K, N, group_size, static_cast<hipStream_t>(stream));
+}
 
 int tqhip_set_matvec_i4_impl_by_name(const char *name) { return tinyqwen::set_matvec_i4_impl_by_name(name) ? 1 : 0; }
 const char *tqhip_matvec_i4_impl_name(void) { return tinyqwen::matvec_i4_impl_name(); }

@@ -24,6 +24,7 @@
 #include "tq_common.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace tqhip {
@@ -771,7 +772,52 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
     return launch_tiles<1, 3, 0>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
 }
 
+// ---- allocation-free variant --------------------------------------------------------------
+// `scratch` holds X's fp16 copy and the per-token scales for callers that cannot
+// allocate (code under graph capture, serving loops). Every GPU the library runs on
+// holds its own copy for the life of the process; all calls on one GPU share it, so
+// calls that overlap on one GPU race. Nothing in it has to start at zero: x_to_f16
+// writes every byte the GEMM reads (the padding columns included).
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, once looked up
+
+// The device address of `scratch` on the current device. The host-side name is only a
+// handle for the lookup; kernels get this address.
+int noalloc_scratch(unsigned char **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return kHipFailed;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return kHipFailed;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<unsigned char *>(g_scratch_ptr[dev]);
+    return kOk;
+}
+
 }  // namespace
+
+int launch_i4_matmul_noalloc(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                             hipStream_t stream) {
+    if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+    const bool mfma = mfma_applies(M, K, N, group_size);
+    if (mfma && prefill_scratch_bytes(K, N) > kNoAllocScratchBytes) return kNoScratch;
+    unsigned char *ws = nullptr;
+    if (mfma) {
+        const int st = noalloc_scratch(&ws);
+        if (st != kOk) return st;
+        return matmul_mfma(w, x, y, M, K, N, group_size, ws, stream);
+    }
+    // One matvec per token column under a scratch set with no buffers: a kernel that would
+    // need split-K slots is not chosen, and nothing is allocated.
+    static ScratchSet *none = scratch_set_fixed(nullptr, 0);
+    ScratchScope scope(none);
+    return matmul_by_columns(w, x, y, M, K, N, group_size, stream);
+}
 
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                      hipStream_t stream) {

@@ -51,6 +51,7 @@ enum Status : int {
     kLaunchFailed = -4,  // hipGetLastError after the launch was not hipSuccess
     kBadFile = -5,       // a .tqwen file was unreadable, invalid or of an unsupported kind
     kHipFailed = -6,     // a HIP allocation or copy failed
+    kNoScratch = -7,     // the allocation-free entry point's static scratch is too small for the call
     kNotFused = 1,       // a fused path does not apply to these operands; nothing was launched
 };
 
@@ -72,6 +73,11 @@ int launch_biip_rotate_n(int n, const float *x, float *const *y, int dim, const 
                          const float *const *sign, int block_size, hipStream_t stream);
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                      hipStream_t stream);
+// The same without any allocation: X's fp16 copy goes to the library's static
+// device array (kNoAllocScratchBytes per device); kNoScratch when it does not fit.
+int launch_i4_matmul_noalloc(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
+                             hipStream_t stream);
+constexpr size_t kNoAllocScratchBytes = size_t{16} << 20;
 // Bytes of prefill scratch (fp16 X rows padded to 64 elements, 256-byte aligned, then one
 // float per token) a matmul of K x N takes.
 inline size_t prefill_scratch_bytes(int K, int N) {
