@@ -96,6 +96,24 @@ int tqhip_matvec_qkv_i4_dev(const uint8_t *wq, const uint8_t *wk, const uint8_t 
                             float *yk, float *yv, int q_dim, int kv_dim, int in_dim, int group_size, void *stream);
 int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                         void *stream);
+/* One matrix of a matvec set: its weights, activations, output and shape. */
+typedef struct tqhip_i4_mat {
+    const uint8_t *w;
+    const float *x;
+    float *y;
+    int out_dim, in_dim;
+} tqhip_i4_mat;
+/* n independent i4 matvecs y_i = W_i x_i of one group size, each with its own activation
+ * vector and shape, for instance a decoder layer's q/k/v/o/gate/up/down (four activation
+ * vectors). No counterpart in the reference, whose runtime issues a layer as separate
+ * registry calls (runtime/qwen_forward_token.cpp:401, 458, 639, 658 through
+ * kernels/dispatch.h:151-175): this is the "matvec set per layer" as one launch. Every
+ * matrix with group_size 64, in_dim % 4 == 0, in_dim <= 10240 and x 16-byte aligned goes
+ * into one launch per 8 such matrices; any other runs through tqhip_matvec_i4_dev's
+ * kernels. Each output has the same bits as the lane kernels of tqhip_matvec_i4_dev give
+ * it where those run (rows up to 1024 wide on small grids, up to 6144 wide on very small
+ * ones). mats is read during the call. */
+int tqhip_matvec_i4_set_dev(const tqhip_i4_mat *mats, int n, int group_size, void *stream);
 /* tqhip_matmul_i4_dev without any allocation. No counterpart in the reference: this is
  * for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). Same kernels and results as
@@ -191,6 +209,7 @@ typedef struct tqhip_op {
 #define TQHIP_OP_I4_PAIR 4
 #define TQHIP_OP_I4_QKV 5
 #define TQHIP_OP_BIIP_ROTATE 6   /* x -> y, in_dim = dim, group_size = block_size, w2 = scale (or NULL), w3 = sign */
+#define TQHIP_OP_I4_SET 7        /* w = const tqhip_i4_mat * (n matrices, read when the op runs or is captured), group_size */
 int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream);
 /* As tqhip_run_ops, with a HIP event pair around every call; op_ms[i] gets the
  * mean event-to-event time of call i over the repeats (kernel duration as the

@@ -54,9 +54,9 @@ SHAPES = [
     # with one three-window tile per workgroup
     (151936, 896, 64), (16384, 1536, 64), (20000, 2560, 64), (40000, 520, 40), (60000, 2560, 64),
     (20000, 4096, 64), (9728, 2560, 64), (4096, 2560, 64),
-    # the fp32 lane kernel (G = 64, K % 4 == 0, K <= 1024): every lane of a
-    # half-wave live (K = 1024), a partial last group (K = 964), rows shorter
-    # than a group, one and two rows per half-wave (up to 4 tiles per CU)
+    # the set kernel (G = 64, K % 4 == 0, x 16-byte aligned, small grids): every
+    # lane of a half-wave live (K = 1024), a partial last group (K = 964), rows
+    # shorter than a group, one and two rows per half-wave
     (40, 1024, 64), (3000, 964, 64), (9, 36, 64), (16000, 512, 64),
 ]
 
@@ -113,8 +113,8 @@ def test_bad_shapes_return_codes(gpu):
 
 
 def test_misaligned_activations_take_another_kernel(gpu, orc):
-    """x 4 bytes past a 16-byte boundary: the lane kernel needs 16-byte aligned
-    activations, so this launch goes to the register path; same results as
+    """x 4 bytes past a 16-byte boundary: the set kernel needs 16-byte aligned
+    activations, so this launch goes to the MFMA register path; same results as
     the oracle either way."""
     M, K, G = 896, 896, 64
     w = gpu.synth_i4(M, K, G, seed=77)
@@ -133,15 +133,15 @@ def test_misaligned_activations_take_another_kernel(gpu, orc):
 # length and tile count, and a row's sum does not depend on where in the grid
 # it is computed), else within 1e-6 of the output scale (the fused launch has
 # more tiles than the single one and can take another kernel, which adds the
-# same terms in another order: e.g. 6144 fused rows at K = 2560 run the MFMA
-# kernels, a single 1024-row matrix the wave-per-row lane kernel).
+# same terms in another order: e.g. 19456 fused rows at K = 2560 run the MFMA
+# kernels, a single 9728-row matrix the set kernel).
 def same_as_single(got, single, exact):
     if exact:
         return np.array_equal(got, single)
     return float(np.max(np.abs(got - single))) <= 1e-6 * max(float(np.max(np.abs(single))), 1e-30)
 
 
-@pytest.mark.parametrize("q,kv,K,G,exact", [(896, 128, 896, 64, True), (4096, 1024, 2560, 64, False),
+@pytest.mark.parametrize("q,kv,K,G,exact", [(896, 128, 896, 64, True), (4096, 1024, 2560, 64, True),
                                             (100, 17, 520, 40, True), (64, 16, 4864, 64, True),
                                             (40, 8, 1000, 128, True), (24, 24, 200, 6, True)])
 def test_qkv_dev_one_launch_matches_single_and_oracle(gpu, orc, q, kv, K, G, exact):
@@ -194,27 +194,32 @@ def test_run_ops_pair_and_qkv_kinds(gpu, orc):
 
 # Split-K path (long rows, few tiles; rows a multiple of 16 bytes): several
 # workgroups per 16-row tile, partial sums meeting in exchange slots that every
-# launch leaves empty. (At G = 64 and K <= 6144 grids of at most 64 tiles run
-# the wave-per-row lane kernel instead: 896x4864, 100x4864 and 17x1792 cover
-# that one here; 1600x4864, 2560x4096 and 2560x9728 run split-K.)
+# launch leaves empty. At G = 64 the set kernel takes these shapes when x is
+# 16-byte aligned, so each runs twice: aligned (set kernel) and with x 4 bytes
+# off (1600x4864, 2560x4096, 2560x9728 and 1030x2688 then run split-K, the
+# smaller ones the MFMA kernels); G = 128 runs split-K either way.
 @pytest.mark.parametrize("M,K,G", [(896, 4864, 64), (1600, 4864, 64), (2560, 9728, 64), (2560, 4096, 64),
                                    (100, 4864, 64), (300, 8192, 128), (17, 1792, 64), (64, 3072, 128),
                                    (1030, 2688, 64)])
 def test_split_k_matches_oracle_and_repeats(gpu, orc, M, K, G):
     w = gpu.synth_i4(M, K, G, seed=M * 7 + K)
-    x = gpu.synth_normal(K, seed=K)
+    x = gpu.synth_normal(K + 4, seed=K)
     dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
-    outs = []
-    for _ in range(3):  # the tile counters must come back to zero after every launch
-        gpu.matvec_i4_dev(dw, dx, dy, M, K, G)
-        outs.append(dy.download(np.float32, M))
-    assert all(np.array_equal(outs[0], o) for o in outs[1:]), "split-K result changed between launches"
-    assert_close(outs[0], orc.matvec_i4(w, x, M, K, G, threads=16), f"split {M}x{K} G{G}")
+    for off in (0, 1):  # x at a 16-byte boundary, then 4 bytes past one
+        xs = x[off:off + K]
+        outs = []
+        for _ in range(3):  # the tile counters must come back to zero after every launch
+            assert gpu.lib().tqhip_matvec_i4_dev(dw.ptr, dx.ptr + 4 * off, dy.ptr, M, K, G, None) == 0
+            gpu.synchronize()
+            outs.append(dy.download(np.float32, M))
+        assert all(np.array_equal(outs[0], o) for o in outs[1:]), "result changed between launches"
+        assert_close(outs[0], orc.matvec_i4(w, np.ascontiguousarray(xs), M, K, G, threads=16),
+                     f"{M}x{K} G{G} x offset {4 * off}")
 
 
 def test_split_k_on_two_streams(gpu, orc):
     """Launches on different streams use different scratch buffers."""
-    M, K, G = 1600, 4864, 64  # split-K (100 tiles), with its per-stream scratch
+    M, K, G = 1600, 4864, 128  # split-K (100 tiles), with its per-stream scratch
     ws = [gpu.synth_i4(M, K, G, seed=s) for s in (1, 2)]
     xs = [gpu.synth_normal(K, seed=s) for s in (3, 4)]
     dws = [gpu.DeviceBuffer.from_array(w) for w in ws]

@@ -23,7 +23,7 @@ LIB_PATH = os.path.join(HERE, "libtqhip.so")
 
 OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH, EFILE, EHIP, ENOSCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
 NOALLOC_SCRATCH_BYTES = 16 << 20  # TQHIP_NOALLOC_SCRATCH_BYTES
-OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV, OP_BIIP_ROTATE = 1, 2, 3, 4, 5, 6
+OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV, OP_BIIP_ROTATE, OP_I4_SET = 1, 2, 3, 4, 5, 6, 7
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -37,6 +37,21 @@ class Op(ctypes.Structure):
     _fields_ = [("kind", _i), ("w", _vp), ("x", _vp), ("y", _vp),
                 ("out_dim", _i), ("in_dim", _i), ("n", _i), ("group_size", _i),
                 ("w2", _vp), ("w3", _vp), ("y2", _vp), ("y3", _vp), ("out_dim2", _i)]
+
+
+class I4Mat(ctypes.Structure):
+    """tqhip_i4_mat: one matrix of a matvec set (device pointers)."""
+    _fields_ = [("w", _vp), ("x", _vp), ("y", _vp), ("out_dim", _i), ("in_dim", _i)]
+
+
+def i4_set(mats: list) -> "ctypes.Array":
+    """A tqhip_i4_mat array from (w, x, y, out_dim, in_dim) tuples (DeviceBuffers or addresses)."""
+    return (I4Mat * len(mats))(*[I4Mat(_ptr(w), _ptr(x), _ptr(y), m, k) for w, x, y, m, k in mats])
+
+
+def set_op(mats: "ctypes.Array", group_size: int) -> Op:
+    """A TQHIP_OP_I4_SET op over a tqhip_i4_mat array; keep the array alive while the op is used."""
+    return Op(OP_I4_SET, ctypes.addressof(mats), None, None, 0, 0, len(mats), group_size)
 
 
 class TensorInfo(ctypes.Structure):
@@ -71,6 +86,7 @@ _SIGS = {
     "tqhip_matvec_qkv_i4_dev": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matmul_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matmul_i4_noalloc_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "tqhip_matvec_i4_set_dev": (_i, [_vp, _i, _i, _vp]),
     "tqhip_biip_rotate_dev": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp]),
     "tqhip_dequant_i4_rows_dev": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     # registry
@@ -404,6 +420,13 @@ def matvec_qkv_i4_dev(wq, wk, wv, x, yq, yk, yv, q_dim: int, kv_dim: int, in_dim
 def matmul_i4_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None) -> None:
     _check(lib().tqhip_matmul_i4_dev(_ptr(w), _ptr(x), _ptr(y), M, K, N, group_size, _stream(stream)),
            "tqhip_matmul_i4_dev")
+
+
+def matvec_i4_set_dev(mats, group_size: int, stream=None) -> None:
+    """tqhip_matvec_i4_set_dev over a tqhip_i4_mat array (see i4_set) or a list of tuples."""
+    arr = mats if isinstance(mats, ctypes.Array) else i4_set(mats)
+    _check(lib().tqhip_matvec_i4_set_dev(ctypes.addressof(arr), len(arr), group_size, _stream(stream)),
+           "tqhip_matvec_i4_set_dev")
 
 
 def matmul_i4_noalloc_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None) -> int:

@@ -20,7 +20,7 @@ REPO = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libtqhip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["i4_matvec.hip", "vq2_matvec.hip", "i4_matmul.hip", "biip_rotate.hip", "i4_embed.hip", "decode_engine.hip", "tqwen_model.cpp", "dispatch.cpp",
+SOURCES = ["i4_matvec.hip", "i4_set.hip", "vq2_matvec.hip", "i4_matmul.hip", "biip_rotate.hip", "i4_embed.hip", "decode_engine.hip", "tqwen_model.cpp", "dispatch.cpp",
            "capi.cpp", "synth.cpp", "scratch.cpp"]
 ARCH = os.environ.get("TQHIP_ARCH", "gfx950")
 

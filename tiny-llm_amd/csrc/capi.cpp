@@ -266,6 +266,9 @@ int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K
                         void *stream) {
     return launch_i4_matmul(w, x, y, M, K, N, group_size, static_cast<hipStream_t>(stream));
 }
+int tqhip_matvec_i4_set_dev(const tqhip_i4_mat *mats, int n, int group_size, void *stream) {
+    return launch_i4_matvec_set(n, reinterpret_cast<const I4Mat *>(mats), group_size, static_cast<hipStream_t>(stream));
+}
 int tqhip_matmul_i4_noalloc_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                                 void *stream) {
     static_assert(TQHIP_NOALLOC_SCRATCH_BYTES == kNoAllocScratchBytes, "header and library agree on the size");
@@ -379,6 +382,8 @@ static int launch_op(const tqhip_op &op, hipStream_t s) {
         }
         case TQHIP_OP_VQ2_MATVEC: return launch_vq2_matvec(w, op.x, op.y, op.out_dim, op.in_dim, s);
         case TQHIP_OP_I4_MATMUL: return launch_i4_matmul(w, op.x, op.y, op.out_dim, op.in_dim, op.n, op.group_size, s);
+        case TQHIP_OP_I4_SET:
+            return launch_i4_matvec_set(op.n, static_cast<const I4Mat *>(op.w), op.group_size, s);
         case TQHIP_OP_BIIP_ROTATE:
             return launch_biip_rotate(op.x, op.y, op.in_dim, static_cast<const float *>(op.w2),
                                       static_cast<const float *>(op.w3), op.group_size, s);
@@ -492,6 +497,12 @@ int tqhip_ops_graph_destroy(void *graph) {
 }
 
 }  // extern "C"
+
+static_assert(sizeof(tqhip_i4_mat) == sizeof(I4Mat) && offsetof(tqhip_i4_mat, w) == offsetof(I4Mat, w) &&
+                  offsetof(tqhip_i4_mat, x) == offsetof(I4Mat, x) && offsetof(tqhip_i4_mat, y) == offsetof(I4Mat, y) &&
+                  offsetof(tqhip_i4_mat, out_dim) == offsetof(I4Mat, M) &&
+                  offsetof(tqhip_i4_mat, in_dim) == offsetof(I4Mat, K),
+              "tqhip_i4_mat is the library's I4Mat");
 
 // Self-registration as the "hip" variants (kernels/dispatch.h:459-474 idiom).
 TINYQWEN_MATVEC_I4_VARIANT(tqhip_matvec_i4, "hip");

@@ -26,33 +26,21 @@
 //     from the start; the MFMA operands (codes and group headers) are read
 //     back from LDS. The row windows are split over the waves and the
 //     per-wave partial sums are added in a fixed order (deterministic).
-//     (i4_matvec_lds is the same scheme staged through VGPRs instead.)
 //   * Rows longer than 48 windows use the register-only variant, which loads
 //     the operands straight from HBM.
 // Portable path (any even G): one wave per row, fp32 accumulation.
 
-#include "tq_common.h"
+#include "i4_lane.h"
 
 #include <algorithm>
 
 namespace tqhip {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
 constexpr int kChunk = 64;     // bytes of one weight row covered by one MFMA pair ("window")
 constexpr int kTile = 16;      // weight rows per MFMA tile
 constexpr int kPiece = 1024;   // bytes one wave streams per 16-byte-per-lane load
-constexpr unsigned kNibbles = 0x0F0F0F0Fu;
-constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family word 3)
 constexpr int kCachePolicyStream = 2;     // buffer-load cache-policy bits: nt (non-temporal)
-#ifndef TQ_LDS_DEPTH
-#define TQ_LDS_DEPTH 1  // tiles in flight per workgroup beyond the one in LDS
-#endif
-#ifndef TQ_WAVES_PER_CU
-#define TQ_WAVES_PER_CU 16  // resident waves per CU the staged kernel's grid aims for
-#endif
-constexpr int kWavesPerCu = TQ_WAVES_PER_CU;
 #ifndef TQ_DMA_INFLIGHT_KB
 #define TQ_DMA_INFLIGHT_KB 96  // weight bytes in flight per CU the DMA ring aims for
 #endif
@@ -70,53 +58,15 @@ constexpr int kPipeWgsPerCu = 2;         // register-path kernel: workgroups per
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
 constexpr int kMaxDepth = 8;              // DMA ring slots at most
 constexpr int kMaxGroup = 3;              // matrices sharing x in one DMA-staged launch (qkv)
-#ifndef TQ_USE_DMA
-#define TQ_USE_DMA 1  // stage tiles with global->LDS DMA (else through VGPRs)
-#endif
-
-// DPP controls (gfx9): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_ror:8, row_shr:n.
-constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppRor8 = 0x128;
-constexpr int kDppShr1 = 0x111, kDppShr2 = 0x112, kDppShr4 = 0x114, kDppShr8 = 0x118;
-
-__device__ inline float half_bits(uint32_t h) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xFFFFu)));
-}
 
 __device__ inline float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
 }
 
-// a[l] + a[l^16], then + the same of lane l^32: the four 16-lane rows of the
-// wave summed in every lane, in the order of two xor-shuffle steps (16, then
-// 32). gfx950's row swaps move the values in registers, where a shuffle is an
-// LDS permute round trip. v_permlane16_swap(d, s) exchanges the odd rows of d
-// with the even rows of s, so with d = s = a the two results hold rows
-// (0,0,2,2) and (1,1,3,3) and their sum is a[l] + a[l^16] in every lane (fp
-// addition commutes); v_permlane32_swap does the same for the wave halves.
-__device__ __forceinline__ float sum_rows4(float a) {
-    const unsigned u = __builtin_bit_cast(unsigned, a);
-    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    const float b = __builtin_bit_cast(float, static_cast<unsigned>(p[0])) +
-                    __builtin_bit_cast(float, static_cast<unsigned>(p[1]));
-    const unsigned v = __builtin_bit_cast(unsigned, b);
-    const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return __builtin_bit_cast(float, static_cast<unsigned>(q[0])) +
-           __builtin_bit_cast(float, static_cast<unsigned>(q[1]));
-}
-
 __device__ inline float wave_sum(float v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
     return v;
-}
-
-template <int CTRL>
-__device__ inline float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-__device__ inline int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 
 // Position of element i of a group inside its 8-element block, in the order
@@ -164,12 +114,6 @@ struct TileRef {
     float *y;
     int M, tile;
 };
-
-// A store of one output through a global-memory pointer. A pointer rebuilt
-// from an integer (TileMap) has lost its address space, and a plain store
-// through it becomes a flat store, which also counts against the LDS wait
-// counter: every later LDS barrier would then wait for the store to complete.
-__device__ inline void store_y(float *p, float v) { *(__attribute__((address_space(1))) float *)p = v; }
 
 // Tile -> matrix lookup for the 1..3 matrices of gm (tiles numbered one
 // matrix after the other): the base values plus differences added under the
@@ -586,206 +530,8 @@ __device__ __forceinline__ float window_step(float a, const v4i &d, unsigned h, 
     return fmaf(s, fmaf(V, E, -z * C), a);
 }
 
-__device__ inline __amdgpu_buffer_rsrc_t rows_rsrc(const uint8_t *w, int M, int row_bytes, int row0) {
-    const size_t rem = row0 < M ? static_cast<size_t>(M - row0) * row_bytes : 0;  // past the end: every load reads 0
-    const int nrec = rem > 0xFFFFFFFFull ? -1 : static_cast<int>(static_cast<unsigned>(rem));
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w) + static_cast<size_t>(row0) * row_bytes,
-                                             static_cast<short>(0), nrec, kBufferFlags);
-}
-
 // ============================================================================================
-// LDS-staged kernel (rows of up to 48 windows).
-//   GT: compile-time group size (0 = run time). CPW: windows per wave.
-//   PW: 1 KB pieces per wave per tile. NWMAX: waves per workgroup bound.
-template <int GT, int CPW, int PW, int NWMAX, int DEPTH>
-__global__ __launch_bounds__(64 * NWMAX, kWavesPerCu / 4) void i4_matvec_lds(const uint8_t *__restrict__ w,
-                                                               const float *__restrict__ x, float *__restrict__ y,
-                                                               Geom gm) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int NW = gm.NW;
-    const int M = gm.M, rb = gm.row_bytes, rbp = gm.rbp;
-    const int G = GT ? GT : gm.G;
-    const int Kp = gm.Gr * G;
-    const int NWP = (NW + 3) & ~3;
-    const int tbuf = kTile * rbp + kChunk;  // bytes of one staged tile (slack for the last window)
-
-    unsigned char *stage = smem;                                         // [2][tbuf]
-    float *part = reinterpret_cast<float *>(smem + 2 * tbuf);            // [2][16][NWP]
-    // The activation set-up lives in stage buffer 1 (free until tile 1 is
-    // stashed after the first barrier of the loop), or after part if too big.
-    // G = 64 / 128: each wave converts just the groups its windows touch into
-    // its own 2 KB slice; otherwise the workgroup converts the whole vector.
-    constexpr bool kWaveLocal = GT == 64 || GT == 128;
-    const int t0 = (gm.T * wave) / NW;
-    const int nch = (gm.T * (wave + 1)) / NW - t0;  // 1..CPW by construction on the host
-    const int gfirst = (kChunk * t0) / (GT ? kI4Header + GT / 2 : gm.gb);
-    XPlanes xp;
-    XFirst xf;
-    if constexpr (kWaveLocal) {
-        xp.pl = reinterpret_cast<int8_t *>(smem + gm.xoff + wave * kWaveXBytes);
-        xp.stride = 64 * 8;
-        xp.pre = reinterpret_cast<int *>(xp.pl + 3 * xp.stride);
-        xp.gexp = reinterpret_cast<float *>(xp.pre + 64);
-        xp.gbase = gfirst;
-        xp.ngroups = 64 / (G / 8);
-        load_x_wave<GT>(xf, x, gm.K, gm.Gr, gfirst);
-    } else {
-        xp.pl = reinterpret_cast<int8_t *>(smem + gm.xoff);
-        xp.stride = Kp;
-        xp.pre = reinterpret_cast<int *>(xp.pl + 3 * Kp);
-        xp.gexp = reinterpret_cast<float *>(xp.pre + Kp / 8);
-        xp.gbase = 0;
-        xp.ngroups = gm.Gr;
-        load_x_first<GT>(xf, x, gm.K, Kp);
-    }
-
-    // Tiles are dealt round-robin (tile = blockIdx.x + i*gridDim.x): at any
-    // moment the whole grid streams one neighbourhood of the matrix, which
-    // HBM serves markedly faster than one distant range per workgroup.
-    const int tiles = (M + kTile - 1) / kTile;
-    const int ntile = blockIdx.x < static_cast<unsigned>(tiles) ? (tiles - 1 - blockIdx.x) / gridDim.x + 1 : 0;
-    auto tile_of = [&](int i) { return static_cast<int>(blockIdx.x + static_cast<unsigned>(i) * gridDim.x); };
-
-    // Pieces of a tile this lane moves: tile-relative byte offset and its LDS
-    // destination (row-padded). Identical for every tile.
-    int poff[PW], pdst[PW];
-    bool pown[PW];
-#pragma unroll
-    for (int s = 0; s < PW; ++s) {
-        const int j = wave + s * NW;
-        const int o = kPiece * j + 16 * lane;
-        // o and the tile size 16*rb are multiples of 16: a 16-byte piece lies
-        // entirely inside the tile or entirely past it (the last piece's tail).
-        pown[s] = j < gm.pieces && o < kTile * rb;
-        poff[s] = o;
-        const int row = o / rb;
-        pdst[s] = row * rbp + (o - row * rb);
-    }
-    const bool aligned16 = (rb & 15) == 0;  // a 16-byte piece never straddles two rows
-
-    auto issue = [&](v4i (&v)[PW], int tile) {
-        const __amdgpu_buffer_rsrc_t rs = rows_rsrc(w, M, rb, tile * kTile);
-#pragma unroll
-        for (int s = 0; s < PW; ++s)
-            if (pown[s]) v[s] = __builtin_amdgcn_raw_buffer_load_b128(rs, poff[s], 0, 0);
-    };
-    auto stash = [&](const v4i (&v)[PW], unsigned char *buf) {
-#pragma unroll
-        for (int s = 0; s < PW; ++s) {
-            if (!pown[s]) continue;
-            if (aligned16) {
-                *reinterpret_cast<v4i *>(buf + pdst[s]) = v[s];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int o = poff[s] + 4 * e;
-                    const int row = o / rb;
-                    *reinterpret_cast<int *>(buf + row * rbp + (o - row * rb)) = v[s][e];
-                }
-            }
-        }
-    };
-
-    // The first tiles start streaming before the activation set-up.
-    v4i V0[PW], V1[PW];
-    if (ntile > 0) issue(V0, tile_of(0));
-    if (DEPTH == 2 && ntile > 1) issue(V1, tile_of(1));
-
-    if constexpr (kWaveLocal) {
-        prepare_x_wave<GT>(xp, x, gm.K, gm.Gr, xf);
-    } else {
-        prepare_x<GT>(xp, x, gm.K, gm.Gr, Kp, xf);
-        __syncthreads();
-    }
-
-    v4i A0[CPW], A1[CPW];
-    float E[CPW], C[CPW];
-    int HO[CPW];
-    unsigned HM[CPW];
-    build_operands<GT, CPW>(xp, gm, t0, nch, A0, A1, E, C, HO, HM);
-    // LDS offsets of this lane's operand column and headers within a staged tile
-    const int bn = lane & 15, kq = lane >> 4;
-    int RO[CPW], RH[CPW];
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-        const int t = t0 + min(c, nch - 1);
-        RO[c] = bn * rbp + kChunk * t + 16 * kq;
-        RH[c] = bn * rbp + HO[c];
-    }
-
-    if (ntile > 0) stash(V0, stage);
-    if (DEPTH == 2 && ntile > 2) issue(V0, tile_of(2));
-    if (DEPTH == 1 && ntile > 1) issue(V0, tile_of(1));
-
-    auto reduce_prev = [&](int i) {  // partial sums of tile i (written before the last barrier)
-        const float *pb = part + (i & 1) * (kTile * NWP);
-        if (threadIdx.x < kTile) {
-            const float4 *pr = reinterpret_cast<const float4 *>(pb + threadIdx.x * NWP);
-            float s = 0.f;
-            for (int q = 0; q < NWP / 4; ++q) {  // fixed order; padding slots hold 0
-                const float4 v = pr[q];
-                s += v.x;
-                s += v.y;
-                s += v.z;
-                s += v.w;
-            }
-            const int row = tile_of(i) * kTile + threadIdx.x;
-            if (row < M) y[row] = s;
-        }
-    };
-    auto compute = [&](int i) {
-        const unsigned char *buf = stage + (i & 1) * tbuf;
-        float a = 0.f;
-#pragma unroll
-        for (int c = 0; c < CPW; ++c) {
-            const v4i d = *reinterpret_cast<const v4i *>(buf + RO[c]);
-            const unsigned h = *reinterpret_cast<const unsigned *>(buf + RH[c]) & HM[c];
-            a = window_step(a, d, h, A0[c], A1[c], E[c], C[c]);
-        }
-        a = sum_rows4(a);  // the four group slots of each row
-        float *pb = part + (i & 1) * (kTile * NWP);
-        if (lane < kTile) pb[lane * NWP + wave] = a;
-    };
-
-    for (int i = threadIdx.x; i < 2 * kTile * NWP; i += blockDim.x) part[i] = 0.f;
-
-    if constexpr (DEPTH == 1) {
-        // tile i in LDS buffer i&1, tile i+1 in flight into V0
-        for (int i = 0; i < ntile; ++i) {
-            __syncthreads();
-            if (i + 1 < ntile) stash(V0, stage + ((i + 1) & 1) * tbuf);
-            if (i + 2 < ntile) issue(V0, tile_of(i + 2));
-            compute(i);
-            if (i > 0) reduce_prev(i - 1);
-        }
-        __syncthreads();
-        if (ntile > 0) reduce_prev(ntile - 1);
-        return;
-    }
-    // DEPTH 2: tile i is in LDS buffer i&1, tile i+1 in VGPRs (V1/V0 by parity),
-    // tile i+2 being fetched.
-    for (int i = 0; i < ntile; i += 2) {
-        __syncthreads();
-        if (i + 1 < ntile) stash(V1, stage + tbuf);
-        if (i + 3 < ntile) issue(V1, tile_of(i + 3));
-        compute(i);
-        if (i > 0) reduce_prev(i - 1);
-        if (i + 1 >= ntile) break;
-        __syncthreads();
-        if (i + 2 < ntile) stash(V0, stage);
-        if (i + 4 < ntile) issue(V0, tile_of(i + 4));
-        compute(i + 1);
-        reduce_prev(i);
-    }
-    __syncthreads();
-    if (ntile > 0) reduce_prev(ntile - 1);
-}
-
-// ============================================================================================
-// DMA-staged kernel (rows of up to 48 windows): like i4_matvec_lds, but tiles
-// go global -> LDS directly (buffer_load ... lds, 16 bytes per lane) into a
+// DMA-staged kernel (rows of up to 48 windows): tiles go global -> LDS directly (buffer_load ... lds, 16 bytes per lane) into a
 // ring of D tile buffers (D = gm.depth, 3..8, picked on the host from the LDS
 // budget), so D tiles are in flight while the activation set-up runs and
 // D - 1 while a tile is contracted, without spending VGPRs on the staging.
@@ -1374,241 +1120,7 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     }
 }
 
-// ============================================================================================
-// Lane kernel (G = 64, K % 4 == 0, rows of at most 32 half-groups: K <= 1024) for grids of
-// up to four 16-row tiles per CU (the decode-size launches): fp32 VALU, no LDS, no barrier.
-// Each wave owns 2 * R rows, one per half-wave and round; lane u of a half-wave takes
-// half-group u of the row (32 weights: 16 code bytes plus the group's header) and the 32
-// activations it multiplies, which stay in VGPRs for all R rows. Per half-group,
-// scale * (sum(q * x) - zero * sum(x)) in fp32; the 32 lanes of a half-wave are added with
-// DPP and one gfx950 row swap in a fixed order. One load round trip, about 100 VALU and
-// the reduction lie between the launch and the store, where the MFMA path also converts
-// the activations, builds operands and synchronises its waves twice through LDS.
-constexpr int kLaneWaves = 4;  // waves per workgroup
-constexpr int kDppMirror = 0x140;
-
-template <int B>
-__device__ inline float ubyte_float(unsigned v) {
-    float f;
-    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
-    if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
-    if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
-    if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
-    return f;
-}
-
-template <int R, bool GROUP>
-__global__ __launch_bounds__(64 * kLaneWaves) void i4_matvec_lane(const uint8_t *__restrict__ w,
-                                                                  const float *__restrict__ x,
-                                                                  float *__restrict__ y, Geom gm) {
-    const int lane = threadIdx.x & 63;
-    const int half = lane >> 5, u = lane & 31;
-    const int job = blockIdx.x * kLaneWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (job >= gm.tile_end[gm.nmat - 1]) return;  // (whole waves)
-    TileRef r;
-    if constexpr (GROUP) {
-        r = TileMap(gm).at(job);
-    } else {
-        r.w = w;
-        r.y = y;
-        r.M = gm.M;
-        r.tile = job;
-    }
-    const int rb = gm.row_bytes;
-    const bool live = u < 2 * gm.Gr;
-    const int row0 = r.tile * (2 * R);
-    const __amdgpu_buffer_rsrc_t wr = rows_rsrc(r.w, r.M, rb, row0);  // rows past the matrix read 0
-    unsigned hd[R];
-    v4i cd[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        const int off = (2 * i + half) * rb + (kI4Header + 32) * (u >> 1);
-        hd[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
-        cd[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + kI4Header + 16 * (u & 1), 0, 0);
-    }
-    // the 32 activations of half-group u (zeros past K; K % 4 == 0 and x is
-    // 16-byte aligned, so a float4 lies wholly inside or outside x), and their
-    // sum. (Plain loads: with a buffer load of 16 bytes whose elements are used
-    // as floats, this compiler shrank the load to its first dword and reused
-    // that dword for the other three elements.)
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    float xv[32];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int e = 32 * u + 4 * q;
-        const float4 v = e < gm.K ? x4[e >> 2] : make_float4(0.f, 0.f, 0.f, 0.f);
-        xv[4 * q] = v.x;
-        xv[4 * q + 1] = v.y;
-        xv[4 * q + 2] = v.z;
-        xv[4 * q + 3] = v.w;
-    }
-    float sx = 0.f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) sx += xv[e];
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const unsigned d = static_cast<unsigned>(cd[i][j]);
-            const unsigned lo = d & kNibbles, hi = (d >> 4) & kNibbles;  // elements 8j + 2b and 8j + 2b + 1 in byte b
-            acc = fmaf(ubyte_float<0>(lo), xv[8 * j], acc);
-            acc = fmaf(ubyte_float<0>(hi), xv[8 * j + 1], acc);
-            acc = fmaf(ubyte_float<1>(lo), xv[8 * j + 2], acc);
-            acc = fmaf(ubyte_float<1>(hi), xv[8 * j + 3], acc);
-            acc = fmaf(ubyte_float<2>(lo), xv[8 * j + 4], acc);
-            acc = fmaf(ubyte_float<2>(hi), xv[8 * j + 5], acc);
-            acc = fmaf(ubyte_float<3>(lo), xv[8 * j + 6], acc);
-            acc = fmaf(ubyte_float<3>(hi), xv[8 * j + 7], acc);
-        }
-        const float sc = half_bits(hd[i]), z = half_bits(hd[i] >> 16);
-        float p = live ? sc * fmaf(-z, sx, acc) : 0.f;
-        p += dpp_f<kDppXor1>(p);
-        p += dpp_f<kDppXor2>(p);
-        p += dpp_f<kDppHalfMirror>(p);
-        p += dpp_f<kDppMirror>(p);
-        const unsigned pu = __builtin_bit_cast(unsigned, p);
-        const auto sw = __builtin_amdgcn_permlane16_swap(pu, pu, false, false);  // rows (0,0,2,2) and (1,1,3,3)
-        p = __builtin_bit_cast(float, static_cast<unsigned>(sw[0])) + __builtin_bit_cast(float, static_cast<unsigned>(sw[1]));
-        const int row = row0 + 2 * i + half;
-        if (u == 0 && row < r.M) store_y(r.y + row, p);
-    }
-}
-
-// Long rows (32 < half-groups <= 64 S): the same arithmetic with one wave per
-// row; lane u takes half-groups u, u + 64, ..., and the 64 lanes are added
-// with DPP and the two gfx950 row swaps (sum_rows4).
-template <int S, bool GROUP>
-__global__ __launch_bounds__(64 * kLaneWaves) void i4_matvec_lanew(const uint8_t *__restrict__ w,
-                                                                   const float *__restrict__ x,
-                                                                   float *__restrict__ y, Geom gm) {
-    const int u = threadIdx.x & 63;
-    const int job = blockIdx.x * kLaneWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if (job >= gm.tile_end[gm.nmat - 1]) return;  // (whole waves)
-    TileRef r;
-    if constexpr (GROUP) {
-        r = TileMap(gm).at(job);
-    } else {
-        r.w = w;
-        r.y = y;
-        r.M = gm.M;
-        r.tile = job;
-    }
-    const int rb = gm.row_bytes, U = 2 * gm.Gr;
-    const __amdgpu_buffer_rsrc_t wr = rows_rsrc(r.w, r.M, rb, r.tile);  // one row; past the matrix: reads 0
-    unsigned hd[S];
-    v4i cd[S];
-#pragma unroll
-    for (int sl = 0; sl < S; ++sl) {
-        const int unit = u + 64 * sl;
-        const int off = (kI4Header + 32) * (unit >> 1);
-        hd[sl] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
-        cd[sl] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + kI4Header + 16 * (unit & 1), 0, 0);
-    }
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    float p = 0.f;
-#pragma unroll
-    for (int sl = 0; sl < S; ++sl) {
-        const int unit = u + 64 * sl;
-        float xv[32];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int e = 32 * unit + 4 * q;
-            const float4 v = e < gm.K ? x4[e >> 2] : make_float4(0.f, 0.f, 0.f, 0.f);
-            xv[4 * q] = v.x;
-            xv[4 * q + 1] = v.y;
-            xv[4 * q + 2] = v.z;
-            xv[4 * q + 3] = v.w;
-        }
-        float sx = 0.f, acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) sx += xv[e];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const unsigned d = static_cast<unsigned>(cd[sl][j]);
-            const unsigned lo = d & kNibbles, hi = (d >> 4) & kNibbles;
-            acc = fmaf(ubyte_float<0>(lo), xv[8 * j], acc);
-            acc = fmaf(ubyte_float<0>(hi), xv[8 * j + 1], acc);
-            acc = fmaf(ubyte_float<1>(lo), xv[8 * j + 2], acc);
-            acc = fmaf(ubyte_float<1>(hi), xv[8 * j + 3], acc);
-            acc = fmaf(ubyte_float<2>(lo), xv[8 * j + 4], acc);
-            acc = fmaf(ubyte_float<2>(hi), xv[8 * j + 5], acc);
-            acc = fmaf(ubyte_float<3>(lo), xv[8 * j + 6], acc);
-            acc = fmaf(ubyte_float<3>(hi), xv[8 * j + 7], acc);
-        }
-        const float sc = half_bits(hd[sl]), z = half_bits(hd[sl] >> 16);
-        if (unit < U) p += sc * fmaf(-z, sx, acc);
-    }
-    p += dpp_f<kDppXor1>(p);
-    p += dpp_f<kDppXor2>(p);
-    p += dpp_f<kDppHalfMirror>(p);
-    p += dpp_f<kDppMirror>(p);
-    p = sum_rows4(p);
-    if (u == 0 && r.tile < r.M) store_y(r.y + r.tile, p);
-}
-
-template <int S>
-int launch_lanew(const uint8_t *w, const float *x, float *y, Geom gm, const int *rows, hipStream_t stream) {
-    int end = 0;
-    for (int j = 0; j < kMaxGroup; ++j) {
-        if (j < gm.nmat) end += rows[j];
-        gm.tile_end[j] = end;  // jobs (rows) of matrices 0..j
-    }
-    const int grid = (end + kLaneWaves - 1) / kLaneWaves;
-    if (gm.nmat > 1)
-        hipLaunchKernelGGL((i4_matvec_lanew<S, true>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
-    else
-        hipLaunchKernelGGL((i4_matvec_lanew<S, false>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
-    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
-}
-
-template <int R>
-int launch_lane(const uint8_t *w, const float *x, float *y, Geom gm, const int *rows, hipStream_t stream) {
-    int end = 0;
-    for (int j = 0; j < kMaxGroup; ++j) {
-        if (j < gm.nmat) end += (rows[j] + 2 * R - 1) / (2 * R);
-        gm.tile_end[j] = end;  // jobs (2 R rows) of matrices 0..j
-    }
-    const int grid = (end + kLaneWaves - 1) / kLaneWaves;
-    if (gm.nmat > 1)
-        hipLaunchKernelGGL((i4_matvec_lane<R, true>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
-    else
-        hipLaunchKernelGGL((i4_matvec_lane<R, false>), dim3(grid), dim3(64 * kLaneWaves), 0, stream, w, x, y, gm);
-    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
-}
-
 int device_cus();
-
-// The lane kernel runs for short rows on grids of at most kLaneMaxTilesPerCu
-// 16-row tiles per CU (everything at K = 896 but lm_head): G = 64, K % 4 == 0
-// and x 16-byte aligned (whole float4 activation loads), K <= 1024.
-constexpr int kLaneMaxTilesPerCu = 4;
-inline bool lane_fits(const float *x, int K, int G, int tiles) {
-    return G == 64 && K % 4 == 0 && K <= 1024 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
-           tiles <= kLaneMaxTilesPerCu * device_cus();
-}
-// Rows per half-wave: one while the grid is at most one tile per CU (more
-// waves, shorter chains: 896x896 2.99 vs 3.18 us), two above (the activations
-// reused over twice the rows: the 2x4864x896 gate/up pair 5.52 us, against
-// 5.84 on the register path).
-inline int lane_rows(int tiles) { return tiles <= device_cus() ? 1 : 2; }
-
-// Long rows (1024 < K <= 64 * 3 * 32) on grids of at most one 16-row tile per
-// four CUs (one wave per row): 896x4864 4.8 vs 5.6 us on split-K, 300x2560 3.6
-// vs 5.3 us; at 160 and 256 tiles the MFMA kernels win (8.2 vs 7.6 us at
-// 2560x4096, 8.0 vs 5.4 us at 4096x2560).
-inline int lanew_slots(const float *x, int K, int G, int tiles) {
-    if (G != 64 || K % 4 != 0 || K <= 1024 || K > 3 * 64 * 32 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 ||
-        4 * tiles > device_cus())
-        return 0;
-    return (K + 64 * 32 - 1) / (64 * 32);  // 64-half-group slots per lane: 1..3
-}
-int launch_lanew_for(const uint8_t *w, const float *x, float *y, const Geom &gm, const int *rows, int slots,
-                     hipStream_t stream) {
-    return slots == 1 ? launch_lanew<1>(w, x, y, gm, rows, stream)
-           : slots == 2 ? launch_lanew<2>(w, x, y, gm, rows, stream)
-                        : launch_lanew<3>(w, x, y, gm, rows, stream);
-}
 
 // ============================================================================================
 // Register-only kernel (rows of 49..96 windows): operands straight from HBM.
@@ -1651,7 +1163,7 @@ __global__ __launch_bounds__(1024, 4) void i4_matvec_reg(const uint8_t *__restri
 #pragma unroll
     for (int c = 0; c < CPW; ++c) DO[c] = kChunk * (t0 + min(c, nch - 1)) + 16 * kq;
 
-    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {  // round-robin, as in i4_matvec_lds
+    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {  // round-robin, as in i4_matvec_dma
         const int row0 = tile * kTile;
         const __amdgpu_buffer_rsrc_t rs = rows_rsrc(w, M, rb, row0);
         const int lb = (min(row0 + bn, M - 1) - row0) * rb;
@@ -1853,24 +1365,6 @@ int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     return launch_with_lds(i4_matvec_dma<GT, CPW, PW, NWMAX>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, limit);
 }
 
-template <int GT, int CPW, int PW, int NWMAX, int DEPTH = TQ_LDS_DEPTH>
-int launch_lds(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
-    if (TQ_USE_DMA) return launch_dma<GT, CPW, PW, NWMAX>(w, x, y, gm, stream);
-    static size_t limit = 0;
-    const int tiles = (gm.M + kTile - 1) / kTile;
-    const int NWP = (gm.NW + 3) & ~3;
-    const size_t tbuf = static_cast<size_t>(kTile) * gm.rbp + kChunk;
-    const size_t base = 2 * tbuf + static_cast<size_t>(2 * kTile * NWP) * 4;
-    Geom g2 = gm;
-    const size_t xbytes = (GT == 64 || GT == 128) ? static_cast<size_t>(gm.NW) * kWaveXBytes : xplanes_bytes(gm);
-    const bool inside = xbytes <= tbuf;
-    g2.xoff = static_cast<int>(inside ? tbuf : base);
-    const size_t lds = (inside ? base : base + xbytes) + 16;
-    const int by_waves = std::max(1, kWavesPerCu / NWMAX);
-    const int by_lds = std::max(1, static_cast<int>((160 * 1024) / lds));
-    const int grid = std::max(1, std::min(tiles, device_cus() * std::min(by_waves, by_lds)));
-    return launch_with_lds(i4_matvec_lds<GT, CPW, PW, NWMAX, DEPTH>, grid, 64 * gm.NW, lds, w, x, y, g2, stream, limit);
-}
 
 template <int GT, int CPW, int PW, int NWMAX>
 int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int Tmax, hipStream_t stream) {
@@ -1939,29 +1433,29 @@ int launch_mfma_for(const uint8_t *w, const float *x, float *y, Geom gm, hipStre
     if (T <= 8) {
         gm.NW = T;
         switch (pw_of(gm.NW)) {
-            case 1: return launch_lds<GT, 1, 1, 8>(w, x, y, gm, stream);
-            case 2: return launch_lds<GT, 1, 2, 8>(w, x, y, gm, stream);
-            case 3: return launch_lds<GT, 1, 3, 8>(w, x, y, gm, stream);
-            default: return launch_lds<GT, 1, 4, 8>(w, x, y, gm, stream);
+            case 1: return launch_dma<GT, 1, 1, 8>(w, x, y, gm, stream);
+            case 2: return launch_dma<GT, 1, 2, 8>(w, x, y, gm, stream);
+            case 3: return launch_dma<GT, 1, 3, 8>(w, x, y, gm, stream);
+            default: return launch_dma<GT, 1, 4, 8>(w, x, y, gm, stream);
         }
     }
     if (T <= 16) {
         gm.NW = (T + 1) / 2;
         switch (pw_of(gm.NW)) {
-            case 1: case 2: return launch_lds<GT, 2, 2, 8>(w, x, y, gm, stream);
-            case 3: return launch_lds<GT, 2, 3, 8>(w, x, y, gm, stream);
-            default: return launch_lds<GT, 2, 4, 8>(w, x, y, gm, stream);
+            case 1: case 2: return launch_dma<GT, 2, 2, 8>(w, x, y, gm, stream);
+            case 3: return launch_dma<GT, 2, 3, 8>(w, x, y, gm, stream);
+            default: return launch_dma<GT, 2, 4, 8>(w, x, y, gm, stream);
         }
     }
     if (T <= 24) {
         gm.NW = (T + 2) / 3;
-        return pw_of(gm.NW) <= 3 ? launch_lds<GT, 3, 3, 8>(w, x, y, gm, stream)
-                                 : launch_lds<GT, 3, 4, 8>(w, x, y, gm, stream);
+        return pw_of(gm.NW) <= 3 ? launch_dma<GT, 3, 3, 8>(w, x, y, gm, stream)
+                                 : launch_dma<GT, 3, 4, 8>(w, x, y, gm, stream);
     }
     if (T <= 48) {
         gm.NW = (T + 2) / 3;
-        return pw_of(gm.NW) <= 3 ? launch_lds<GT, 3, 3, 16>(w, x, y, gm, stream)
-                                 : launch_lds<GT, 3, 4, 16>(w, x, y, gm, stream);
+        return pw_of(gm.NW) <= 3 ? launch_dma<GT, 3, 3, 16>(w, x, y, gm, stream)
+                                 : launch_dma<GT, 3, 4, 16>(w, x, y, gm, stream);
     }
     if (T <= 64) {
         gm.NW = (T + 3) / 4;
@@ -2023,12 +1517,12 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
     }
     gm.ksplit = 1;
     int st;
-    if (lane_fits(x, in_dim, group_size, gm.tile_end[0]))
-        return lane_rows(gm.tile_end[0]) == 1 ? launch_lane<1>(w, x, y, gm, &out_dim, stream)
-                                              : launch_lane<2>(w, x, y, gm, &out_dim, stream);
-    if (const int sl = lanew_slots(x, in_dim, group_size, gm.tile_end[0]))
-        return launch_lanew_for(w, x, y, gm, &out_dim, sl, stream);
-    if (TQ_USE_DMA && (group_size == 64 || group_size == 128)) {
+    {
+        const I4Mat m{w, x, y, out_dim, in_dim};
+        st = launch_i4_matvec_set_fit(1, &m, group_size, stream);
+        if (st != kNotFused) return st;
+    }
+    if ((group_size == 64 || group_size == 128)) {
         st = group_size == 64 ? launch_split_for<64>(w, x, y, gm, stream) : launch_split_for<128>(w, x, y, gm, stream);
         if (st != kTooLarge) return st;
     }
@@ -2053,7 +1547,13 @@ int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, cons
         if (out_dim[j] < 1) return kBadShape;
     const size_t rb = i4_row_bytes(in_dim, group_size);
     const int T = static_cast<int>((rb + kChunk - 1) / kChunk);
-    const bool grouped = n > 1 && TQ_USE_DMA && (group_size % 8 == 0) && group_size >= 40 && T <= 48 &&
+    {  // the set kernel takes all n in one launch where it applies (rows sharing x)
+        I4Mat m[kMaxGroup];
+        for (int j = 0; j < n; ++j) m[j] = I4Mat{w[j], x, y[j], out_dim[j], in_dim};
+        const int st = launch_i4_matvec_set_fit(n, m, group_size, stream);
+        if (st != kNotFused) return st;
+    }
+    const bool grouped = n > 1 && (group_size % 8 == 0) && group_size >= 40 && T <= 48 &&
                          rb * kTile * 2 < (1ull << 31);
     if (!grouped) {
         for (int j = 0; j < n; ++j) {
@@ -2087,11 +1587,6 @@ int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, cons
         gm.mw[j] = w[jj];
         gm.my[j] = y[jj];
     }
-    if (lane_fits(x, in_dim, group_size, end))
-        return lane_rows(end) == 1 ? launch_lane<1>(w[0], x, y[0], gm, out_dim, stream)
-                                   : launch_lane<2>(w[0], x, y[0], gm, out_dim, stream);
-    if (const int sl = lanew_slots(x, in_dim, group_size, end))
-        return launch_lanew_for(w[0], x, y[0], gm, out_dim, sl, stream);
     const int st = group_size == 64    ? launch_mfma_for<64>(w[0], x, y[0], gm, stream)
                    : group_size == 128 ? launch_mfma_for<128>(w[0], x, y[0], gm, stream)
                                        : launch_mfma_for<0>(w[0], x, y[0], gm, stream);

@@ -1,0 +1,362 @@
+// i4_set.hip -- one launch over a set of i4 HQQ@64 matvecs, each with its own
+// activation vector, output, row count and row length.
+//
+// A decoder layer's matvec set (q, k, v, o, gate, up, down: four distinct
+// activation vectors) is about 8 MB at Qwen2.5-0.5B scale, a microsecond or two
+// of HBM time, while every separate launch costs a few microseconds of dispatch
+// and load latency. This kernel covers the whole set with one grid:
+//   * Every workgroup belongs to one matrix (the matrices' workgroups are
+//     numbered one after the other, the longest rows first so they start
+//     first); the matrix is found with a few scalar compares against the
+//     kernel argument.
+//   * The workgroup's activation loads are issued first, then every weight load
+//     of its rows; while the weights arrive, the activations are turned into
+//     exact integer operands in LDS (one power-of-two exponent per group of 64),
+//     and one barrier later every wave reads its slices from LDS.
+//   * Rows of up to 32 half-groups (K <= 1024) take one half-wave each (two rows
+//     per half-wave on larger sets), longer rows (K <= 10240) one wave each over
+//     1..5 slots of 64 half-groups; lane u computes half-group u (32 weights: 16
+//     code bytes and the group header) with v_dot4 on the code nibbles and the
+//     activation digits, exact before a per-half-group fp32 epilogue.
+// The same kernel serves single-matrix and pair / qkv launches of decode size
+// (launch_i4_matvec_set_fit), so a matrix gives the same bits alone or in a set.
+// Numerics: the only rounding before the epilogue is x -> X (relative 2^-23 of the
+// group's largest |x|); measured rel L2 ~4e-7 against the double-accumulating reference
+// (kernels/matvec/matvec_i4_ref.cpp:45-103).
+#include "i4_lane.h"
+
+#include <algorithm>
+
+namespace tqhip {
+namespace {
+
+#ifndef TQ_SET_WAVES
+#define TQ_SET_WAVES 8
+#endif
+constexpr int kSetWaves = TQ_SET_WAVES;     // waves per workgroup
+constexpr int kSetThreads = 64 * kSetWaves;
+constexpr int kSetMaxSlots = 5;   // wave-per-row slots of 64 half-groups: K <= 5 * 64 * 32
+
+struct SetMat {
+    const uint8_t *w;
+    const float *x;
+    float *y;
+    int M, K;
+    int blk0;   // first workgroup of this matrix
+    int shape;  // 0: one row per half-wave (K <= 1024); s = 1..5: one row per wave over s slots
+};
+struct SetArgs {
+    SetMat m[kSetMaxMats];
+    int n;
+};
+
+// ---- activations as exact integers -------------------------------------------------------
+// Every group of 64 activations is scaled by its own power of two 2^f (its largest |x|
+// lands in [2^21, 2^22)) and rounded to the nearest integer: X = x * 2^f rounded,
+// |X| <= 2^22, the only rounding before the epilogue. X's two's-complement bytes are its
+// digits, X = b0 + 256 b1 + 65536 s2 with b0, b1 unsigned and s2 the signed third byte
+// (exact while |X| < 2^23). They go to LDS as the byte operands of v_dot4: per 8-element
+// block six dwords [byte p][even | odd], "even" holding elements 0, 2, 4, 6 and "odd" 1,
+// 3, 5, 7 -- the order in which a code dword's low and high nibbles present the weights.
+// Per half-group (32 elements) LDS also holds sum(X) (as a float) and 2^-f.
+constexpr int kBlockBytes = 24;  // one 8-element block: 3 digit planes x (even, odd) dwords
+
+__device__ inline int group_exponent(float m) {
+    if (!(m > 0.f)) return 0;
+    int e;
+    frexpf(m, &e);  // m in [2^(e-1), 2^e)
+    return min(22 - e, 149);
+}
+
+// Round to nearest (ties upward: floor(v + 0.5)), one instruction.
+__device__ inline int round_int(float v) {
+    int r;
+    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// Thread t converts 16-byte chunk c = t + kSetThreads i (elements 4c .. 4c + 3) of every chunk
+// the rows read (c < C): the 16 chunks of a group are one DPP row (16 lanes), the 8
+// chunks of a half-group half of one.
+__device__ __forceinline__ void stage_x(float4 q, int c, int Kc, int C, unsigned char *xp, float2 *hs) {
+    if (c >= Kc) q = make_float4(0.f, 0.f, 0.f, 0.f);  // past K: zeros
+    float m = fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w)));
+    m = fmaxf(m, dpp_f<kDppXor1>(m));
+    m = fmaxf(m, dpp_f<kDppXor2>(m));
+    m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
+    m = fmaxf(m, dpp_f<kDppMirror>(m));  // the group's largest |x|, in all 16 lanes
+    const int f = group_exponent(m);
+    const float up = ldexpf(1.f, f);     // exact power of two (f <= 149)
+    const unsigned X0 = round_int(q.x * up), X1 = round_int(q.y * up);
+    const unsigned X2 = round_int(q.z * up), X3 = round_int(q.w * up);
+    int sum = static_cast<int>(X0 + X1 + X2 + X3);
+    sum += dpp_i<kDppXor1>(sum);
+    sum += dpp_i<kDppXor2>(sum);
+    sum += dpp_i<kDppHalfMirror>(sum);  // the half-group's sum(X), in its 8 lanes
+    if (c >= C) return;
+    // elements 4c + 0, 2 are "even" bytes 2 (c & 1) + 0, 1 of the block; 4c + 1, 3 "odd"
+    unsigned char *blk = xp + (c >> 1) * kBlockBytes + 2 * (c & 1);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const unsigned sel = 0x0C0C0000u | ((4u + p) << 8) | p;  // byte p of the second, byte p of the first
+        *reinterpret_cast<unsigned short *>(blk + 8 * p) = static_cast<unsigned short>(__builtin_amdgcn_perm(X2, X0, sel));
+        *reinterpret_cast<unsigned short *>(blk + 8 * p + 4) =
+            static_cast<unsigned short>(__builtin_amdgcn_perm(X3, X1, sel));
+    }
+    if ((c & 7) == 0) hs[c >> 3] = make_float2(static_cast<float>(sum), ldexpf(1.f, -f));
+}
+
+// scale * 2^-f * (sum(q * X) - zero * sum(X)) over one half-group: the 16 code bytes cd,
+// the group header hd, the half-group's 24 operand dwords xv (4 blocks) and its
+// (sum(X), 2^-f). The digit sums are exact integers (v_dot4: unsigned for b0 and b1,
+// signed for s2); sum(q * X) = (a0 + 256 a1) + 65536 a2 is formed in fp32.
+__device__ __forceinline__ float half_group_int(const v4i &cd, unsigned hd, const unsigned (&xv)[24], float2 hs) {
+    unsigned a0 = 0, a1 = 0;
+    int a2 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const unsigned d = static_cast<unsigned>(cd[j]);
+        const unsigned lo = d & kNibbles, hi = (d >> 4) & kNibbles;
+        a0 = __builtin_amdgcn_udot4(lo, xv[6 * j + 0], a0, false);
+        a0 = __builtin_amdgcn_udot4(hi, xv[6 * j + 1], a0, false);
+        a1 = __builtin_amdgcn_udot4(lo, xv[6 * j + 2], a1, false);
+        a1 = __builtin_amdgcn_udot4(hi, xv[6 * j + 3], a1, false);
+        a2 = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(xv[6 * j + 4]), a2, false);
+        a2 = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xv[6 * j + 5]), a2, false);
+    }
+    const float V = fmaf(static_cast<float>(a2), 65536.f, static_cast<float>(a0 + a1 * 256u));
+    const float sc = half_bits(hd), z = half_bits(hd >> 16);
+    return (sc * hs.y) * fmaf(-z, hs.x, V);
+}
+
+// Rows of at most 32 half-groups (S = 0): R rows per half-wave, 2R per wave, 8R per
+// workgroup. Rows of more: one per wave over S slots, 4 per workgroup.
+template <int S, int R>
+__device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char *lds) {
+    // 16-byte activation loads per thread: the chunks of the widest row of this shape
+    constexpr int NX = ((S == 0 ? 256 : 512 * S) + kSetThreads - 1) / kSetThreads;
+    constexpr int NR = S == 0 ? R : 1;      // rows per lane
+    constexpr int NS = S == 0 ? 1 : S;      // half-group slots per lane
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int U = 2 * ((m.K + 63) / 64), rb = 18 * U;  // half-groups and bytes per row
+    const int C = 8 * U;                                 // 16-byte activation chunks the rows read
+    unsigned char *xp = lds;                                              // C / 2 blocks of operands
+    float2 *hs = reinterpret_cast<float2 *>(lds + (C / 2) * kBlockBytes);  // U (sum(X), 2^-f)
+
+    // 1. the activations first: chunk t + kSetThreads i, clamped to the last one (zeroed past K
+    // in stage_x). (Plain 16-byte loads: with a 16-byte buffer load whose elements are used
+    // as floats, this compiler shrinks the load to its first dword and reuses that dword.)
+    const float4 *x4 = reinterpret_cast<const float4 *>(m.x);
+    const int Kc = m.K / 4;
+    float4 xq[NX];
+#pragma unroll
+    for (int i = 0; i < NX; ++i) xq[i] = x4[min(t + kSetThreads * i, Kc - 1)];
+
+    // 2. the weights: lane u of a row takes half-group u (+ 64 per slot)
+    const int half = S == 0 ? lane >> 5 : 0, u = S == 0 ? lane & 31 : lane;
+    // the wave's first row (uniform, so the buffer resource stays in scalar registers); the
+    // half-wave's row goes into the per-lane offset
+    const int base = S == 0 ? (blk * kSetWaves + wave) * 2 * R : blk * kSetWaves + wave;
+    const __amdgpu_buffer_rsrc_t wr = rows_rsrc(m.w, m.M, rb, base);  // rows past the matrix read 0
+    unsigned hd[NR * NS];
+    v4i cd[NR * NS];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+#pragma unroll
+        for (int sl = 0; sl < NS; ++sl) {
+            const int unit = u + 64 * sl;
+            const int off = (2 * r + half) * rb + (kI4Header + 32) * (unit >> 1);
+            hd[r * NS + sl] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
+            cd[r * NS + sl] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + kI4Header + 16 * (unit & 1), 0, 0);
+        }
+    }
+    // every weight load is issued before the wait for the activations below
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. activations to integer operands in LDS, while the weights arrive. Every iteration
+    // runs (stage_x writes only chunks below C): a loop that stopped early would let the
+    // compiler sink the later activation loads behind the weight loads.
+#pragma unroll
+    for (int i = 0; i < NX; ++i) stage_x(xq[i], t + kSetThreads * i, Kc, C, xp, hs);
+    __syncthreads();
+
+    // 4. the row sums; lanes past the row's half-groups read the last one (ignored)
+    float p[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) p[r] = 0.f;
+#pragma unroll
+    for (int sl = 0; sl < NS; ++sl) {
+        const int unit = u + 64 * sl;
+        const int ru = min(unit, U - 1);
+        unsigned xv[24];
+        const v4i *src = reinterpret_cast<const v4i *>(xp + ru * 4 * kBlockBytes);
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const v4i v = src[k];
+            xv[4 * k] = v[0];
+            xv[4 * k + 1] = v[1];
+            xv[4 * k + 2] = v[2];
+            xv[4 * k + 3] = v[3];
+        }
+        const float2 h = hs[ru];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const float v = half_group_int(cd[r * NS + sl], hd[r * NS + sl], xv, h);
+            if (unit < U) p[r] += v;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int row = base + 2 * r + half;
+        const float sum = S == 0 ? sum_half_wave(p[r]) : sum_wave(p[r]);
+        if (u == 0 && row < m.M) store_y(m.y + row, sum);
+    }
+}
+
+// SMAX: the largest shape in the launch (the register budget follows it); R: rows per
+// half-wave for the short rows.
+template <int SMAX, int R>
+__global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int b = blockIdx.x;
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < kSetMaxMats; ++i) j = (i < a.n && b >= a.m[i].blk0) ? i : j;
+    SetMat m = a.m[0];
+#pragma unroll
+    for (int i = 1; i < kSetMaxMats; ++i)
+        if (i == j) m = a.m[i];
+    const int blk = b - m.blk0;
+    if (m.shape == 0) {
+        set_rows<0, R>(m, blk, lds);
+    } else if (SMAX <= 1 || m.shape == 1) {
+        set_rows<1, 1>(m, blk, lds);
+    } else if (SMAX <= 2 || m.shape == 2) {
+        set_rows<2, 1>(m, blk, lds);
+    } else if (SMAX <= 3 || m.shape == 3) {
+        set_rows<3, 1>(m, blk, lds);
+    } else if (SMAX <= 4 || m.shape == 4) {
+        set_rows<4, 1>(m, blk, lds);
+    } else {
+        set_rows<5, 1>(m, blk, lds);
+    }
+}
+
+// Shape of a matrix in the set kernel, or -1 when the kernel does not take it:
+// G = 64, K % 4 == 0 and x 16-byte aligned (whole 16-byte activation loads), K <= 10240.
+int set_shape(const I4Mat &mt, int group_size) {
+    if (group_size != 64 || mt.K % 4 != 0 || mt.K > kSetMaxSlots * 64 * 32 ||
+        (reinterpret_cast<uintptr_t>(mt.x) & 15) != 0)
+        return -1;
+    return mt.K <= 1024 ? 0 : (mt.K + 64 * 32 - 1) / (64 * 32);
+}
+
+int device_cus_set() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            return 1;  // no device: the launch that follows fails and reports it
+        cus = n;
+    }
+    return cus;
+}
+
+template <int R>
+void launch_r(int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream, const SetArgs &a) {
+    switch (smax) {
+        case 0: hipLaunchKernelGGL((i4_matvec_set<0, R>), grid, block, lds, stream, a); break;
+        case 1: hipLaunchKernelGGL((i4_matvec_set<1, R>), grid, block, lds, stream, a); break;
+        case 2: hipLaunchKernelGGL((i4_matvec_set<2, R>), grid, block, lds, stream, a); break;
+        case 3: hipLaunchKernelGGL((i4_matvec_set<3, R>), grid, block, lds, stream, a); break;
+        case 4: hipLaunchKernelGGL((i4_matvec_set<4, R>), grid, block, lds, stream, a); break;
+        default: hipLaunchKernelGGL((i4_matvec_set<5, R>), grid, block, lds, stream, a); break;
+    }
+}
+
+int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream) {
+    SetArgs a{};
+    int order[kSetMaxMats];
+    for (int i = 0; i < n; ++i) order[i] = i;
+    // longest rows first: their workgroups are dispatched first
+    std::stable_sort(order, order + n, [&](int p, int q) { return shape[p] > shape[q]; });
+    // Two short rows per half-wave once they fill more than one 16-row tile per CU: the
+    // activations read from LDS and summed once serve both rows.
+    long short_rows = 0;
+    for (int k = 0; k < n; ++k)
+        if (shape[k] == 0) short_rows += mats[k].M;
+    const int R = short_rows > 16L * device_cus_set() ? 2 : 1;
+    int blocks = 0, smax = 0, umax = 0;
+    for (int k = 0; k < n; ++k) {
+        const I4Mat &mt = mats[order[k]];
+        const int s = shape[order[k]];
+        a.m[k] = SetMat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, s};
+        const int per = s == 0 ? 2 * R * kSetWaves : kSetWaves;  // rows per workgroup
+        blocks += (mt.M + per - 1) / per;
+        smax = std::max(smax, s);
+        umax = std::max(umax, 2 * ((mt.K + 63) / 64));
+    }
+    for (int k = n; k < kSetMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
+    a.n = n;
+    const size_t lds = static_cast<size_t>(umax) * (4 * kBlockBytes + 8);  // the widest row's operands
+    const dim3 grid(blocks), block(kSetThreads);
+    if (R == 2)
+        launch_r<2>(smax, grid, block, lds, stream, a);
+    else
+        launch_r<1>(smax, grid, block, lds, stream, a);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+// Single-matrix and fused (pair / qkv) launches go through the set kernel while its grid
+// stays within this many workgroups per CU: measured on MI355X against the MFMA kernels,
+// 9728x2560 7.6 vs 8.5 us, 2560x9728 8.5 vs 13.0 us, 896x4864 4.0 vs 5.5 us; at
+// 151936x896 (4748 workgroups) both take 19 us and at 151936x2560 the DMA ring wins
+// (39 vs 69 us).
+constexpr int kSetMaxBlocksPerCu = 8;
+
+}  // namespace
+
+int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream_t stream) {
+    if (n < 1 || n > kSetMaxMats) return kNotFused;
+    int shape[kSetMaxMats];
+    long blocks = 0;
+    for (int i = 0; i < n; ++i) {
+        shape[i] = set_shape(mats[i], group_size);
+        if (shape[i] < 0 || mats[i].M < 1) return kNotFused;
+        blocks += shape[i] == 0 ? (mats[i].M + 4 * kSetWaves - 1) / (4 * kSetWaves)
+                                : (mats[i].M + kSetWaves - 1) / kSetWaves;
+    }
+    if (blocks > static_cast<long>(kSetMaxBlocksPerCu) * device_cus_set()) return kNotFused;
+    return launch_set(mats, shape, n, stream);
+}
+
+int launch_i4_matvec_set(int n, const I4Mat *mats, int group_size, hipStream_t stream) {
+    if (n < 0 || (n > 0 && !mats)) return kBadShape;
+    if (group_size < 2 || (group_size & 1)) return kBadGroup;
+    for (int i = 0; i < n; ++i)
+        if (mats[i].M < 1 || mats[i].K < 1) return kBadShape;
+    // the matrices the set kernel takes, in launches of up to kSetMaxMats; the others alone
+    I4Mat batch[kSetMaxMats];
+    int shape[kSetMaxMats], nb = 0;
+    for (int i = 0; i < n; ++i) {
+        const int s = set_shape(mats[i], group_size);
+        if (s < 0) {
+            const int st = launch_i4_matvec(mats[i].w, mats[i].x, mats[i].y, mats[i].M, mats[i].K, group_size, stream);
+            if (st != kOk) return st;
+            continue;
+        }
+        batch[nb] = mats[i];
+        shape[nb++] = s;
+        if (nb == kSetMaxMats) {
+            const int st = launch_set(batch, shape, nb, stream);
+            if (st != kOk) return st;
+            nb = 0;
+        }
+    }
+    return nb > 0 ? launch_set(batch, shape, nb, stream) : kOk;
+}
+
+}  // namespace tqhip

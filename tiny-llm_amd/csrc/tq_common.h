@@ -63,6 +63,20 @@ int launch_i4_matvec_generic(const uint8_t *w, const float *x, float *y, int out
 // n (1..3) matrices sharing x, in_dim and group_size (pair / qkv), one launch where possible.
 int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, const int *out_dim, const float *x,
                            int in_dim, int group_size, hipStream_t stream);
+// One matrix of a matvec set (tqhip_i4_mat): its own activations, output and shape.
+struct I4Mat {
+    const uint8_t *w;
+    const float *x;
+    float *y;
+    int M, K;
+};
+constexpr int kSetMaxMats = 8;  // matrices per set launch
+// n independent matvecs sharing a group size: one launch per kSetMaxMats matrices the set
+// kernel takes (G = 64, K % 4 == 0, K <= 10240, x 16-byte aligned), the others one by one.
+int launch_i4_matvec_set(int n, const I4Mat *mats, int group_size, hipStream_t stream);
+// The set kernel for a single or fused launch when every matrix takes it and its grid is small
+// enough to beat the MFMA kernels; kNotFused (nothing launched) otherwise.
+int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream_t stream);
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
 int launch_i4_embed_rows(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
                          hipStream_t stream);
