@@ -2,6 +2,9 @@
 
 Usage: python tiny-llm_amd/build.py   (or tiny_llm_amd.build() from Python)
 
+Also builds libtqceil.so from csrc/ceilings.hip: the machine-ceiling probes (stream
+read, empty launch, dense MFMA) that bench.py reports beside the kernels.
+
 Every HIP translation unit is compiled with packed-fp32 instructions disabled
 (-Xclang -target-feature -Xclang -packed-fp32-ops); hipcc's host pass warns
 that it does not know the feature, which is harmless.
@@ -18,6 +21,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 REPO = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libtqhip.so")
+CEIL_LIB = os.path.join(HERE, "libtqceil.so")  # machine-ceiling probes, loaded by bench.py only
 BUILD_DIR = os.path.join(HERE, "_build")
 
 SOURCES = ["i4_matvec.hip", "i4_set.hip", "vq2_matvec.hip", "i4_matmul.hip", "biip_rotate.hip", "i4_embed.hip", "decode_engine.hip", "tqwen_model.cpp", "dispatch.cpp",
@@ -68,8 +72,15 @@ def build(verbose: bool = False) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB)
+    # the machine-ceiling probes bench.py reports beside the kernels (not part of the product)
+    tmp = CEIL_LIB + ".tmp"
+    cmd = [_hipcc(), *_flags(), "-shared", os.path.join(CSRC, "ceilings.hip"), "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, CEIL_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {CEIL_LIB}")
     return LIB
 
 

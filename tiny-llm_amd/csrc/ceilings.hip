@@ -1,0 +1,130 @@
+// ceilings.hip -- machine-ceiling probes for bench.py (libtqceil.so, not part of the
+// product library): what one MI355X actually sustains next to its published peaks.
+//
+//   tqceil_stream_read  every byte of a buffer read once with 16-byte loads (grid-stride,
+//                       4 or 8 loads in flight per thread, optionally non-temporal), one
+//                       value stored per workgroup:
+//                       the achievable HBM read rate when the buffer is larger than the
+//                       256 MB MALL.
+//   tqceil_empty        an empty kernel: back-to-back launches measure the per-launch floor.
+//   tqceil_mfma_f16     dense fp16 MFMA from registers (v_mfma_f32_32x32x16_f16 with four
+//                       independent accumulators per wave, or v_mfma_f32_16x16x32_f16 with
+//                       eight; no memory traffic): the sustained fp16 MFMA rate.
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace {
+
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+// U 16-byte loads in flight per thread; NT: non-temporal loads (the data is read once).
+template <int U, bool NT>
+__global__ __launch_bounds__(256) void stream_read(const u4 *__restrict__ p, size_t n16, unsigned *__restrict__ out) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    unsigned acc = 0;
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        u4 v[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) v[k] = NT ? __builtin_nontemporal_load(p + i + k * stride) : p[i + k * stride];
+#pragma unroll
+        for (int k = 0; k < U; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    for (; i < n16; i += stride) {
+        const u4 a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    __shared__ unsigned red[256];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned v = 0;
+        for (int t = 0; t < 256; ++t) v ^= red[t];
+        out[blockIdx.x] = v;
+    }
+}
+
+__global__ void empty_kernel(int *p) {
+    if (p && threadIdx.x == 0x7fffffff) p[0] = 0;  // never true: keeps the argument live
+}
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void mfma_f16(int iters, float *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    h8 a, b;
+    for (int j = 0; j < 8; ++j) {
+        a[j] = static_cast<_Float16>(0.001f * (lane + j));
+        b[j] = static_cast<_Float16>(0.002f * (lane - j));
+    }
+    f16v c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int it = 0; it < iters; ++it) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c3, 0, 0, 0);
+    }
+    float s = 0.f;
+    for (int j = 0; j < 16; ++j) s += c0[j] + c1[j] + c2[j] + c3[j];
+    if (s == 12345.678f) out[blockIdx.x] = s;  // practically never: keeps the work live
+}
+
+// The same with v_mfma_f32_16x16x32_f16 (16384 flops): twice the instructions for the work.
+__global__ __launch_bounds__(256) void mfma_f16_16(int iters, float *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    h8 a, b;
+    for (int j = 0; j < 8; ++j) {
+        a[j] = static_cast<_Float16>(0.001f * (lane + j));
+        b[j] = static_cast<_Float16>(0.002f * (lane - j));
+    }
+    f4v c[8] = {};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) c[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c[k], 0, 0, 0);
+    }
+    float s = 0.f;
+    for (int k = 0; k < 8; ++k) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
+    if (s == 12345.678f) out[blockIdx.x] = s;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Reads `bytes` (a multiple of 16) at p with `blocks` workgroups of 256 threads; out gets one
+// word per workgroup.
+// variant: 0 = 4 loads in flight, 1 = 8, 2 = 8 non-temporal.
+int tqceil_stream_read(const void *p, size_t bytes, unsigned *out, int blocks, int variant, void *stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const u4 *q = static_cast<const u4 *>(p);
+    if (variant == 0)
+        hipLaunchKernelGGL((stream_read<4, false>), dim3(blocks), dim3(256), 0, s, q, bytes / 16, out);
+    else if (variant == 1)
+        hipLaunchKernelGGL((stream_read<8, false>), dim3(blocks), dim3(256), 0, s, q, bytes / 16, out);
+    else
+        hipLaunchKernelGGL((stream_read<8, true>), dim3(blocks), dim3(256), 0, s, q, bytes / 16, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int tqceil_empty(int blocks, int threads, int launches, void *stream) {
+    for (int i = 0; i < launches; ++i)
+        hipLaunchKernelGGL(empty_kernel, dim3(blocks), dim3(threads), 0, static_cast<hipStream_t>(stream), nullptr);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// blocks workgroups of four waves, each wave doing 4 * iters * 32768 flops: variant 0 as
+// 4 * iters v_mfma_f32_32x32x16_f16, variant 1 as 8 * iters v_mfma_f32_16x16x32_f16.
+int tqceil_mfma_f16(int blocks, int iters, int variant, float *out, void *stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (variant == 0)
+        hipLaunchKernelGGL(mfma_f16, dim3(blocks), dim3(256), 0, s, iters, out);
+    else
+        hipLaunchKernelGGL(mfma_f16_16, dim3(blocks), dim3(256), 0, s, iters, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // extern "C"
