@@ -252,6 +252,8 @@ def ceilings(tq, stream):
                                        ctypes.c_void_p]
     lib.tqceil_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.tqceil_mfma_f16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.tqceil_shared_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_void_p]
     sp = ctypes.c_void_p(stream.ptr)
 
     def timed(fn, reps=1, batches=5):
@@ -278,6 +280,15 @@ def ceilings(tq, stream):
             read[f"{names[variant]}, {blocks} wg"] = nb / (ms * 1e-3) / 1e9
     buf.free()
     best = max(read, key=read.get)
+    # one L2-resident buffer (32 tokens x 2560 fp32, the few-token GEMM's X) read whole by every workgroup
+    sb = 32 * 2560 * 4
+    sbuf = tq.DeviceBuffer(sb)
+    tq.lib().tqhip_memset(sbuf.ptr, 1, sb)
+    shared = {}
+    for blocks, threads in ((256, 1024), (256, 512), (512, 512), (1024, 256)):
+        ms = timed(lambda: lib.tqceil_shared_read(sbuf.ptr, sb, out.ptr, blocks, threads, sp))
+        shared[f"{blocks}x{threads}"] = {"us": round(ms * 1e3, 2), "gbs_per_cu": round(blocks * sb / 256 / (ms * 1e-3) / 1e9, 1)}
+    sbuf.free()
     empty = {}
     for blocks, threads in ((1, 64), (1024, 256)):
         empty[f"{blocks}x{threads}"] = round(timed(lambda: lib.tqceil_empty(blocks, threads, 200, sp), 1) * 1e3 / 200, 3)
@@ -292,6 +303,8 @@ def ceilings(tq, stream):
     return {"stream_read_gbs": round(read[best], 1), "stream_read_frac": round(read[best] / PEAK_GBS, 4),
             "stream_read": {"bytes": nb, "best": best, "gbs": {k: round(v, 1) for k, v in read.items()}},
             "empty_launch_us": empty,
+            "shared_read": {"bytes": sb, "note": "every workgroup reads the same buffer; GB/s per CU of 256",
+                            "runs": shared},
             "mfma_f16_tflops": round(tflops, 1), "mfma_f16_frac": round(tflops / PEAK_MFMA_TFLOPS, 4),
             "mfma": {"best": best_mf, "tflops": {k: round(v, 1) for k, v in mf.items()}}}
 

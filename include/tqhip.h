@@ -117,10 +117,12 @@ int tqhip_matvec_i4_set_dev(const tqhip_i4_mat *mats, int n, int group_size, voi
 /* tqhip_matmul_i4_dev without any allocation. No counterpart in the reference: this is
  * for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). Same kernels and results as
- * tqhip_matmul_i4_dev, bit for bit. X's fp16 copy and the per-token scales go to a
- * static device array of TQHIP_NOALLOC_SCRATCH_BYTES (16 MiB) that every GPU the library
- * runs on holds until the process ends; a call needing more
- * (((ceil(K/64)*64*2*N + 255) & ~255) + 4*N bytes, e.g. above 3274 tokens at K = 2560)
+ * tqhip_matmul_i4_dev, bit for bit. X's fp16 copy and the per-token scales (or, at up to
+ * 32 tokens with group_size 64, the few-token kernel's partial products) go to a static
+ * device array of TQHIP_NOALLOC_SCRATCH_BYTES (16 MiB) that every GPU the library runs on
+ * holds until the process ends; its last 64 KiB hold the few-token kernel's tile counters
+ * (zero between calls). A call whose fp16 copy needs more than the rest
+ * (((ceil(K/64)*64*2*N + 255) & ~255) + 4*N bytes, e.g. above 3261 tokens at K = 2560)
  * returns TQHIP_ENOSCRATCH before launching anything. Group sizes that are not a
  * multiple of 32 run one matvec per token, with kernels that need no scratch. All calls
  * on one GPU share the array: calls that overlap on one GPU (two streams, or two host

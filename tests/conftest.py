@@ -76,3 +76,42 @@ def max_abs_rel(got, ref):
     ref = np.asarray(ref, dtype=np.float64)
     scale = np.max(np.abs(ref))
     return float(np.max(np.abs(got - ref)) / (scale if scale > 0 else 1.0))
+
+
+def extreme_x(K, seed):
+    """Per group of 64: one activation 1e4 times larger, one 1e6 times smaller; group 2 all zero."""
+    x = np.random.default_rng(seed).standard_normal(K).astype(np.float32)
+    x[::64] *= 1e4
+    x[1::64] *= 1e-6
+    x[2 * 64:3 * 64] = 0.0
+    return x
+
+
+def special_headers(w, M, K, seed, G=64):
+    """Overwrites about 3% of the group headers with special finite fp16 values."""
+    w = w.copy()
+    groups = (K + G - 1) // G
+    hdr = w.reshape(M, groups, 4 + G // 2)[:, :, 0:4].view(np.uint16)  # [..., 0] scale, [..., 1] zero
+    rng = np.random.default_rng(seed)
+    pick = rng.random((M, groups)) < 0.03
+    specials = [(0x0001, 0x4700), (0x03FF, 0x0000), (0x8000 | 0x2148, 0x4880), (0x0000, 0x4B00),
+                (0x2148, 0xC200), (0x2148, 0x5640), (0x0400, 0x0001)]
+    # (smallest subnormal scale, zero 7), (largest subnormal, 0), (negative scale, 9), (zero scale, 14),
+    # (0.01, zero -3), (0.01, zero 100), (smallest normal, subnormal zero)
+    kinds = rng.integers(0, len(specials), size=(M, groups))
+    for i, (sc, z) in enumerate(specials):
+        sel = pick & (kinds == i)
+        hdr[..., 0][sel] = sc
+        hdr[..., 1][sel] = z
+    return w
+
+
+def fp16_operand_bound_ok(got, want, orc, w, x, M, K, N, G):
+    """Every output of an i4 matmul with fp16 operands within 1e-3 of the size of its own terms,
+    sum_k |w_mk * x_nk| (rounding both operands to fp16 moves a product by at most 2 * 2^-11 of
+    itself): the check for a handful of outputs, where one near-cancelled output decides the
+    relative L2 and max measures."""
+    wd = np.abs(orc.dequant_i4_matrix_f64(w, M, K, G))
+    bound = 1e-3 * (np.abs(np.asarray(x, np.float64)).reshape(N, K) @ wd.T).reshape(-1)
+    err = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
+    return bool(np.all(err <= bound))

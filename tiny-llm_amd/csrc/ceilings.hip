@@ -6,6 +6,8 @@
 //                       value stored per workgroup:
 //                       the achievable HBM read rate when the buffer is larger than the
 //                       256 MB MALL.
+//   tqceil_shared_read  every workgroup reads the same L2-resident buffer: what one CU pulls
+//                       from L2 (the few-token GEMM's X operand is such a buffer).
 //   tqceil_empty        an empty kernel: back-to-back launches measure the per-launch floor.
 //   tqceil_mfma_f16     dense fp16 MFMA from registers (v_mfma_f32_32x32x16_f16 with four
 //                       independent accumulators per wave, or v_mfma_f32_16x16x32_f16 with
@@ -46,6 +48,27 @@ __global__ __launch_bounds__(256) void stream_read(const u4 *__restrict__ p, siz
         for (int t = 0; t < 256; ++t) v ^= red[t];
         out[blockIdx.x] = v;
     }
+}
+
+// Every workgroup reads the same `n16` 16-byte words (an L2-resident buffer shared by all):
+// what one CU can pull from L2.
+__global__ __launch_bounds__(1024) void shared_read(const u4 *__restrict__ p, size_t n16, unsigned *__restrict__ out) {
+    constexpr int U = 8;
+    const size_t stride = blockDim.x;
+    size_t i = threadIdx.x;
+    unsigned acc = 0;
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        u4 v[U];
+#pragma unroll
+        for (int k = 0; k < U; ++k) v[k] = p[i + k * stride];
+#pragma unroll
+        for (int k = 0; k < U; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    for (; i < n16; i += stride) {
+        const u4 a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;  // practically never: keeps the loads live
 }
 
 __global__ void empty_kernel(int *p) {
@@ -107,6 +130,13 @@ int tqceil_stream_read(const void *p, size_t bytes, unsigned *out, int blocks, i
         hipLaunchKernelGGL((stream_read<8, false>), dim3(blocks), dim3(256), 0, s, q, bytes / 16, out);
     else
         hipLaunchKernelGGL((stream_read<8, true>), dim3(blocks), dim3(256), 0, s, q, bytes / 16, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// `blocks` workgroups of `threads` (<= 1024) threads each read all `bytes` (a multiple of 16) at p.
+int tqceil_shared_read(const void *p, size_t bytes, unsigned *out, int blocks, int threads, void *stream) {
+    hipLaunchKernelGGL(shared_read, dim3(blocks), dim3(threads), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const u4 *>(p), bytes / 16, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -19,8 +19,11 @@
 //      contracts with v_mfma_f32_32x32x16_f16 (fp32 accumulation).
 //      fp16 and bf16 MFMA run at the same rate on gfx950; fp16 keeps 8x
 //      finer rounding of both operands.
+// Up to 32 tokens at G = 64 (16-byte aligned X, K % 4 == 0): one launch that converts X
+// itself and splits K over workgroups (section 5 below).
 // Other group sizes: one i4 matvec per token column.
 
+#include "i4_lane.h"
 #include "tq_common.h"
 
 #include <algorithm>
@@ -36,7 +39,6 @@ typedef unsigned u4v __attribute__((ext_vector_type(4)));
 
 constexpr int kStepK = 64;             // K elements per main-loop step
 constexpr int kThreads = 256;
-constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
 
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, size_t bytes) {
     const int nrec = bytes > 0xFFFFFFFFull ? -1 : static_cast<int>(static_cast<unsigned>(bytes));
@@ -637,6 +639,232 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
     }
 }
 
+// ---- 5. Few tokens (N <= 32, G = 64): one launch
+//   A kernel launch costs a few microseconds on this GPU whatever it does, so at a few
+//   tokens a separate X conversion pass would cost as much as the GEMM. Here every
+//   workgroup converts the X it needs itself. The grid is (128-row tile) x (K slice):
+//   workgroup (tile, ks) forms the partial product of its 128 rows over the slice's
+//   steps for all tokens; the last workgroup of a tile to finish adds the KS partials in
+//   slice order (fixed, whatever the arrival order) and stores Y. One CU reads only some
+//   50-90 GB/s from L2, so the fp32 X of a whole row of K per workgroup would take
+//   several microseconds: the slices spread it over the CUs.
+//   - X: the slice of the 32 token rows is read once (fp32, 16-byte loads), scaled per
+//     token by the power of two that puts the token's largest |x| in the slice into
+//     [2^13, 2^14), and stored to LDS as fp16, [step][token][64 elements] with the
+//     16-byte chunks of token n at positions c ^ (n & 7).
+//   - W: each row's slice (9 dwords a step, contiguous) comes in with one DMA into LDS at
+//     an odd dword pitch. (A load per lane and row touches a cache line per lane; the
+//     DMA touches the 2-3 lines the slice spans.) Wave w then takes rows 32 w .. 32 w + 31:
+//     lane (row r, half h) reads the group header and code dwords 1 + 4 h .. 4 + 4 h of each
+//     step, so MFMA k-slot 8 h + p of k-block j holds element 32 h + 8 j + p of the step,
+//     on the A (W) and on the B (X) side.
+//   - Partials: [tile][slice][4 waves x 4 float4 x 64 lanes] fp32 (the MFMA's register
+//     order: every store and load instruction moves 1 KB in one piece), written at device
+//     scope. The slices of a tile are 8 workgroups apart and workgroups are dealt to the 8
+//     XCDs in turn, so a tile normally stays on one XCD and the last arrival reads the
+//     other partials from that XCD's L2; the arrival counter (zero between launches: the
+//     last arrival resets it) carries each writer's XCD, so a partial written elsewhere is
+//     read at device scope instead.
+constexpr int kSkRows = 128;
+constexpr int kDeviceScope = 16;  // buffer cache policy: sc1 (device-scope coherent)
+constexpr int kL1Bypass = 1;      // buffer cache policy: sc0 (misses in the CU's L1, served by the XCD's L2)
+constexpr int kSkXccSlots = 14;   // slices whose writer's XCD the arrival counter carries
+constexpr int kSkReduceBatch = 6; // partials the last arrival has in flight at once
+typedef float f4v __attribute__((ext_vector_type(4)));
+constexpr int kSkTile = kSkRows * 32;  // floats of one partial
+constexpr int kSkMaxSteps = 7;  // a row's slice (9 dwords a step) within one 64-lane DMA
+
+template <int SMAX>
+__global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                                        float *__restrict__ y, int M, int K, int N, int row_bytes,
+                                                        int T, int KS, float *__restrict__ part,
+                                                        unsigned long long *__restrict__ arrivals) {
+    __shared__ __align__(16) unsigned char xs[SMAX * 4096];
+    __shared__ __align__(16) unsigned char ws_lds[kSkRows * (9 * SMAX + 1) * 4];
+    __shared__ float inv_s[32];
+    __shared__ int last_s;
+    __shared__ unsigned long long writers_s;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // workgroup b -> tile 8 (b / (8 KS)) + b % 8, slice (b / 8) % KS: the slices of a tile are
+    // 8 workgroups apart, so with workgroups dealt to the 8 XCDs in turn they share one XCD
+    const int tile = (blockIdx.x / (8 * KS)) * 8 + (blockIdx.x & 7), ks = (blockIdx.x >> 3) % KS;
+    const int m0 = tile * kSkRows;
+    if (m0 >= M) return;  // a padding tile (the tile count rounded up to 8)
+    const int s0 = (ks * T) / KS, ns = ((ks + 1) * T) / KS - s0;  // steps [s0, s0 + ns), 1 <= ns <= SMAX
+
+    // 1. X: thread t takes token n = t / 8 and float4s (t % 8) + 8 q of the token's slice
+    const int n = threadIdx.x >> 3, sub = threadIdx.x & 7;
+    const int k0 = 64 * s0;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + static_cast<size_t>(n < N ? n : 0) * K + k0);
+    float4 xv[2 * SMAX];
+    unsigned okm = 0;  // bit q: float4 q lies in the matrix (masked to zero after the loads land)
+#pragma unroll
+    for (int q = 0; q < 2 * SMAX; ++q) {
+        const int f = sub + 8 * q;
+        const bool ok = n < N && q < 2 * ns && k0 + 4 * f < K;  // K % 4 == 0: a float4 is all in or all out
+        okm |= static_cast<unsigned>(ok) << q;
+        xv[q] = xr[ok ? f : 0];
+    }
+    // 2. W: the slice of each of the tile's 128 rows is 9 ns contiguous dwords; one DMA per row
+    //    (wave w: rows 32 w .. 32 w + 31, lane i: dword i) lands it at LDS dword r * P, with
+    //    the odd pitch P = 9 ns | 1, so the 32 rows a wave reads in step j (dword r P + 9 j + c)
+    //    fall in 32 different banks
+    const int P = (9 * ns) | 1;
+    const int li = lane & 31, h = lane >> 5;
+    if (lane < 9 * ns) {  // only the slice's lanes: a DMA lane writes LDS dword (base + lane), and
+                          // lanes past 9 ns would land in the next row's dwords
+        const __amdgpu_buffer_rsrc_t wr = rows_rsrc(w, M, row_bytes, m0);
+#pragma unroll 4
+        for (int i = 0; i < 32; ++i) {
+            const int r = 32 * wave + i;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wr, (__attribute__((address_space(3))) void *)(ws_lds + 4 * r * P), 4, r * row_bytes + 4 * lane,
+                36 * s0, 0, 0);
+        }
+    }
+
+    // 3. the slice's X to fp16 in LDS, scaled per token
+    wait_vm(0);
+#pragma unroll
+    for (int q = 0; q < 2 * SMAX; ++q) {
+        const bool ok = (okm >> q) & 1u;
+        xv[q].x = ok ? xv[q].x : 0.f;
+        xv[q].y = ok ? xv[q].y : 0.f;
+        xv[q].z = ok ? xv[q].z : 0.f;
+        xv[q].w = ok ? xv[q].w : 0.f;
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int q = 0; q < 2 * SMAX; ++q)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[q].x), fabsf(xv[q].y)), fmaxf(fabsf(xv[q].z), fabsf(xv[q].w))));
+    m = fmaxf(m, dpp_f<kDppXor1>(m));
+    m = fmaxf(m, dpp_f<kDppXor2>(m));
+    m = fmaxf(m, dpp_f<kDppHalfMirror>(m));  // the 8 lanes of token n
+    int e = 0;  // zero or non-finite: unscaled (inf and NaN carry through)
+    if (m > 0.f && m <= 3.0e38f) e = min(14 - __builtin_amdgcn_frexp_expf(m), 126);
+    const float sc = ldexpf(1.f, e);
+    if (sub == 0) inv_s[n] = ldexpf(1.f, -e);
+#pragma unroll
+    for (int q = 0; q < 2 * SMAX; ++q) {
+        const int c = (sub >> 1) + 4 * (q & 1);  // 16-byte chunk of step q / 2
+        uint2 pk;
+        pk.x = fma_pair_f16(xv[q].x, xv[q].y, sc, 0.f);
+        pk.y = fma_pair_f16(xv[q].z, xv[q].w, sc, 0.f);
+        *reinterpret_cast<uint2 *>(xs + 4096 * (q >> 1) + 128 * n + 16 * (c ^ (n & 7)) + 8 * (sub & 1)) = pk;
+    }
+    lds_barrier();
+
+    // 4. the slice's steps: lane (row 32 w + li, half h) takes the header and code dwords
+    //    1 + 4 h .. 4 + 4 h of the step's group
+    f16x acc = {};
+    const unsigned *wl = reinterpret_cast<const unsigned *>(ws_lds) + (32 * wave + li) * P;
+#pragma unroll
+    for (int j = 0; j < SMAX; ++j) {
+        if (j < ns) {
+            const unsigned hd = wl[9 * j];
+            unsigned cd[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) cd[kk] = wl[9 * j + 1 + 4 * h + kk];
+            const float s = half_bits_f(hd);
+            const float zs = -(half_bits_f(hd >> 16) * s);
+            h8 b[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                b[kk] = *reinterpret_cast<const h8 *>(xs + 4096 * j + 128 * li + 16 * ((4 * h + kk) ^ (li & 7)));
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(dequant8(cd[kk], s, zs), b[kk], acc, 0, 0, 0);
+        }
+    }
+
+    // 5. the partial, stored as the MFMA leaves it: float4 r4 of lane l of wave w at index
+    //    (4 w + r4) * 64 + l (rows 32 w + 8 r4 + 4 h + 0..3 of token l % 32, h = l / 32), so
+    //    every store and load instruction moves 1 KB in one piece. Partials are stored at
+    //    device scope (sc1: written through this XCD's L2 to the level where all XCDs meet),
+    //    so a store that has completed is visible everywhere and the counter needs no cache
+    //    write-back or invalidation (both act on a whole L2). The counter add carries the
+    //    writer's XCD (slices < kSkXccSlots): the last arrival reads a partial written on its
+    //    own XCD from that L2 (which the write went through) and any other one at device
+    //    scope (its own L2 may hold an older copy of the line).
+    const float iv = inv_s[li];
+    const int xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 7;  // HW_REG_XCC_ID bits 0..3
+    f4v own[4];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+        own[r4] = f4v{acc[4 * r4] * iv, acc[4 * r4 + 1] * iv, acc[4 * r4 + 2] * iv, acc[4 * r4 + 3] * iv};
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(part + static_cast<size_t>(tile) * KS * kSkTile,
+                                                static_cast<size_t>(KS) * kSkTile * sizeof(float));
+    const int lo = 16 * (256 * wave + lane);  // byte offset of the lane's float4 r4 = 0 in a partial
+    if (KS > 1) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, own[r4]), pr,
+                                                   lo + 4 * (ks * kSkTile) + 1024 * r4, 0, kDeviceScope);
+        wait_vm(0);       // this wave's partial stores have completed
+        __syncthreads();  // and every other wave's
+        if (threadIdx.x == 0) {
+            // bits 56..63: arrivals; bits 4 p .. 4 p + 3: 1 + the XCD of slice p's writer
+            const unsigned long long mine =
+                (1ull << 56) | (ks < kSkXccSlots ? static_cast<unsigned long long>(xcc + 1) << (4 * ks) : 0ull);
+            const unsigned long long prev =
+                __hip_atomic_fetch_add(arrivals + tile, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = (prev >> 56) == static_cast<unsigned long long>(KS - 1);
+            if (last) __hip_atomic_store(arrivals + tile, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_s = last;
+            writers_s = prev;
+        }
+        __syncthreads();
+        if (!last_s) return;
+    }
+    const unsigned long long writers = writers_s;
+
+    // 6. the last arrival: Y = the KS partials added in slice order (its own from registers,
+    //    the others loaded kSkReduceBatch at a time)
+    f4v sum[4] = {};
+    for (int p0 = 0; p0 < KS; p0 += kSkReduceBatch) {
+        f4v v[kSkReduceBatch][4];
+#pragma unroll
+        for (int u = 0; u < kSkReduceBatch; ++u) {
+            const int p = min(p0 + u, KS - 1);
+            if (p == ks) continue;
+            const bool here = p < kSkXccSlots && ((writers >> (4 * p)) & 15) == static_cast<unsigned>(xcc + 1);
+            if (here) {
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    v[u][r4] = __builtin_bit_cast(
+                        f4v, __builtin_amdgcn_raw_buffer_load_b128(pr, lo + 4 * (p * kSkTile) + 1024 * r4, 0, kL1Bypass));
+            } else {
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    v[u][r4] = __builtin_bit_cast(
+                        f4v, __builtin_amdgcn_raw_buffer_load_b128(pr, lo + 4 * (p * kSkTile) + 1024 * r4, 0, kDeviceScope));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kSkReduceBatch; ++u) {
+            if (p0 + u >= KS) break;
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const f4v t = p0 + u == ks ? own[r4] : v[u][r4];
+                sum[r4][0] += t[0];
+                sum[r4][1] += t[1];
+                sum[r4][2] += t[2];
+                sum[r4][3] += t[3];
+            }
+        }
+    }
+    if (li >= N) return;
+    float *yc = y + static_cast<size_t>(li) * M;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int m = m0 + 32 * wave + 8 * r4 + 4 * h + c;
+            if (m < M) yc[m] = sum[r4][c];
+        }
+}
+
 // Raises fn's dynamic-LDS limit to what the CU's 160 KB leaves beside its static LDS
 // (once per kernel; `limit` caches the figure).
 int raise_lds_limit(const void *fn, size_t &limit) {
@@ -703,6 +931,51 @@ int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
     hipLaunchKernelGGL((i4_matmul_g64<WN, S, NWV>), grid, dim3(64 * NWV), lds, stream, w, xh, xinv, y, M, N, K, Kp,
                        rb);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+// The few-token kernel applies: G = 64, at most 32 tokens, whole 16-byte X loads (K % 4 == 0,
+// X 16-byte aligned) and the byte offsets of 128 rows within 31 bits.
+bool skinny_applies(const float *x, int K, int N, int group_size) {
+    return group_size == 64 && N <= 32 && K % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+           static_cast<size_t>(kSkRows) * i4_row_bytes(K, 64) < (1ull << 31);
+}
+
+struct SkinnyGeom {
+    int tiles, T, KS, smax;
+    size_t part_bytes;  // the partial products
+};
+
+// About 1.9 workgroups per CU (all resident at once; measured on MI355X at 9728x2560x32: 6
+// slices of 6-7 steps beat 8 of 5, the reduction of fewer partials outweighing the longer
+// slices), at most kSkMaxSteps steps per slice and at most one slice per step.
+SkinnyGeom skinny_geom(int M, int K) {
+    SkinnyGeom g;
+    g.tiles = (M + kSkRows - 1) / kSkRows;
+    g.T = (K + 63) / 64;
+    const int cus = device_cu_count();
+    const int ks = std::max((19 * cus + 5 * g.tiles) / (10 * g.tiles), (g.T + kSkMaxSteps - 1) / kSkMaxSteps);
+    g.KS = std::max(1, std::min(ks, g.T));
+    g.smax = (g.T + g.KS - 1) / g.KS;
+    g.part_bytes = static_cast<size_t>(g.tiles) * g.KS * kSkTile * sizeof(float);
+    return g;
+}
+
+int launch_skinny(const uint8_t *w, const float *x, float *y, int M, int K, int N, const SkinnyGeom &g, float *part,
+                  unsigned long long *arrivals, hipStream_t stream) {
+    const int rb = static_cast<int>(i4_row_bytes(K, 64));
+    const dim3 grid((g.tiles + 7) / 8 * 8 * g.KS), block(256);
+    switch (g.smax) {
+#define TQ_SKINNY(S)                                                                                             \
+    case S:                                                                                                      \
+        hipLaunchKernelGGL(i4_matmul_skinny<S>, grid, block, 0, stream, w, x, y, M, K, N, rb, g.T, g.KS, part, \
+                           arrivals);                                                                            \
+        break;
+        TQ_SKINNY(1) TQ_SKINNY(2) TQ_SKINNY(3) TQ_SKINNY(4) TQ_SKINNY(5) TQ_SKINNY(6) TQ_SKINNY(7)
+#undef TQ_SKINNY
+        default:
+            return kBadShape;
+    }
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -778,7 +1051,11 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
 // holds its own copy for the life of the process; all calls on one GPU share it, so
 // calls that overlap on one GPU race. Nothing in it has to start at zero: x_to_f16
 // writes every byte the GEMM reads (the padding columns included).
+// The last kNoAllocArrivalBytes are the few-token kernel's arrival counters: zero when the
+// code object is loaded and after every launch, and never written by anything else.
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr size_t kNoAllocArrivalBytes = size_t{64} << 10;
+constexpr size_t kNoAllocWorkBytes = kNoAllocScratchBytes - kNoAllocArrivalBytes;
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
@@ -804,8 +1081,18 @@ int noalloc_scratch(unsigned char **out) {
 int launch_i4_matmul_noalloc(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                              hipStream_t stream) {
     if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+    if (skinny_applies(x, K, N, group_size)) {
+        const SkinnyGeom g = skinny_geom(M, K);
+        if (g.part_bytes <= kNoAllocWorkBytes && static_cast<size_t>(g.tiles) * 8 <= kNoAllocArrivalBytes) {
+            unsigned char *ws = nullptr;
+            const int st = noalloc_scratch(&ws);
+            if (st != kOk) return st;
+            return launch_skinny(w, x, y, M, K, N, g, reinterpret_cast<float *>(ws),
+                                 reinterpret_cast<unsigned long long *>(ws + kNoAllocWorkBytes), stream);
+        }
+    }
     const bool mfma = mfma_applies(M, K, N, group_size);
-    if (mfma && prefill_scratch_bytes(K, N) > kNoAllocScratchBytes) return kNoScratch;
+    if (mfma && prefill_scratch_bytes(K, N) > kNoAllocWorkBytes) return kNoScratch;
     unsigned char *ws = nullptr;
     if (mfma) {
         const int st = noalloc_scratch(&ws);
@@ -822,6 +1109,16 @@ int launch_i4_matmul_noalloc(const uint8_t *w, const float *x, float *y, int M, 
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                      hipStream_t stream) {
     if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+    if (skinny_applies(x, K, N, group_size)) {
+        const SkinnyGeom g = skinny_geom(M, K);
+        unsigned long long *slots = nullptr;  // zero between launches: the arrival counters
+        int st = scratch_split_slots(stream, static_cast<size_t>(g.tiles), &slots);
+        if (st != kOk) return st;
+        void *part = nullptr;
+        st = scratch_prefill(stream, g.part_bytes, &part);
+        if (st != kOk) return st;
+        return launch_skinny(w, x, y, M, K, N, g, static_cast<float *>(part), slots, stream);
+    }
     if (!mfma_applies(M, K, N, group_size)) return matmul_by_columns(w, x, y, M, K, N, group_size, stream);
     void *ws = nullptr;
     const int st = scratch_prefill(stream, prefill_scratch_bytes(K, N), &ws);  // the stream's (or scope's) buffer

@@ -1120,7 +1120,6 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
     }
 }
 
-int device_cus();
 
 // ============================================================================================
 // Register-only kernel (rows of 49..96 windows): operands straight from HBM.
@@ -1225,18 +1224,6 @@ __global__ __launch_bounds__(256) void i4_matvec_rowwave(const uint8_t *__restri
     }
 }
 
-int device_cus() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
-            return 1;  // no device: whatever is launched next fails and reports it
-        cus = n;
-    }
-    return cus;
-}
-
 // Lets `fn` take `lds` bytes of dynamic LDS. Above the default 64 KB the
 // limit is raised once per kernel, to what the CU's 160 KB leaves beside the
 // kernel's static LDS; `limit` caches that figure (0: not raised yet).
@@ -1273,7 +1260,7 @@ int launch_pipe(const uint8_t *w, const float *x, float *y, const Geom &gm, hipS
     const int tiles = gm.tile_end[gm.nmat - 1];
     const int NWP = (gm.NW + 3) & ~3;
     const size_t lds = static_cast<size_t>(2 * kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
-    const int grid = std::max(1, std::min(tiles, device_cus() * kPipeWgsPerCu));
+    const int grid = std::max(1, std::min(tiles, device_cu_count() * kPipeWgsPerCu));
     // one tile per workgroup: nothing to load ahead (a second register slot
     // would only add a round of zero-length loads and an idle iteration)
     const bool one = tiles <= grid;
@@ -1303,7 +1290,7 @@ int launch_seg(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     static_assert(kChunk * CPW + 48 <= 16 * PD * 4, "segment fits the slot");
     const int tiles = gm.tile_end[gm.nmat - 1];
     const int NWP = (gm.NW + 3) & ~3;
-    const int cus = device_cus();
+    const int cus = device_cu_count();
     const int wgs = tiles <= 8 * cus ? 1 : 2, depth = wgs == 1 ? 3 : 2;
     const int grid = std::max(1, std::min(tiles, cus * wgs));
     const int per_wg = (tiles + grid - 1) / grid;
@@ -1341,19 +1328,19 @@ int launch_dma(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
         const size_t lds2 = 2 * tbuf + fixed;
         int wgs2 = wgs;
         while (wgs2 > 1 && static_cast<size_t>(wgs2) * lds2 > kLdsBytes) --wgs2;
-        const int slots = device_cus() * wgs2;
-        const bool pipe_one_round = CPW != 3 || tiles <= device_cus() * kPipeWgsPerCu;
+        const int slots = device_cu_count() * wgs2;
+        const bool pipe_one_round = CPW != 3 || tiles <= device_cu_count() * kPipeWgsPerCu;
         if (CPW == 1 || (tiles <= 2 * slots && pipe_one_round)) return launch_pipe<GT, CPW, NWMAX>(w, x, y, gm, stream);
     }
     if constexpr (CPW == 3) {
-        if (gm.T > 24 || tiles < 32 * device_cus()) {
+        if (gm.T > 24 || tiles < 32 * device_cu_count()) {
             const int st = launch_seg<GT, CPW, NWMAX>(w, x, y, gm, stream);
             if (st != kTooLarge) return st;
         }
     }
     while (wgs > 1 && static_cast<size_t>(wgs) * (3 * tbuf + fixed) > kLdsBytes) --wgs;
     if (3 * tbuf + fixed > kLdsBytes) return kTooLarge;
-    const int grid = std::max(1, std::min(tiles, device_cus() * wgs));
+    const int grid = std::max(1, std::min(tiles, device_cu_count() * wgs));
     const int per_wg = (tiles + grid - 1) / grid;
     const size_t lds_cap = kLdsBytes / wgs;
     int depth = static_cast<int>(std::min<size_t>(kMaxDepth, (lds_cap - fixed) / tbuf));
@@ -1394,7 +1381,7 @@ int launch_split(const uint8_t *w, const float *x, float *y, Geom gm, int S, int
 template <int GT>
 int launch_split_for(const uint8_t *w, const float *x, float *y, Geom gm, hipStream_t stream) {
     const int tiles = (gm.M + kTile - 1) / kTile;
-    const int slots = 2 * device_cus();
+    const int slots = 2 * device_cu_count();
     if (gm.T < 24 || 2 * tiles > slots || gm.row_bytes % 16 != 0) return kTooLarge;
     const int S = std::min({4, slots / tiles, gm.T / 8});
     if (S < 2) return kTooLarge;
@@ -1421,7 +1408,7 @@ int launch_reg(const uint8_t *w, const float *x, float *y, const Geom &gm, hipSt
     const int tiles = (gm.M + kTile - 1) / kTile;
     const int NWP = (gm.NW + 3) & ~3;
     const size_t lds = static_cast<size_t>(kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
-    const int grid = std::max(1, std::min(tiles, device_cus()));
+    const int grid = std::max(1, std::min(tiles, device_cu_count()));
     return launch_with_lds(i4_matvec_reg<GT, CPW>, grid, 64 * gm.NW, lds, w, x, y, gm, stream, limit);
 }
 
@@ -1478,7 +1465,7 @@ int launch_i4_matvec_generic(const uint8_t *w, const float *x, float *y, int out
     const int Gr = i4_groups(in_dim, group_size);
     const unsigned long long rb = i4_row_bytes(in_dim, group_size);
     const int waves_per_block = 4;
-    const int grid = std::max(1, std::min((out_dim + waves_per_block - 1) / waves_per_block, device_cus() * 8));
+    const int grid = std::max(1, std::min((out_dim + waves_per_block - 1) / waves_per_block, device_cu_count() * 8));
     hipLaunchKernelGGL(i4_matvec_rowwave, dim3(grid), dim3(64 * waves_per_block), 0, stream, w, x, y, out_dim,
                        in_dim, group_size, gb, Gr, rb);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;

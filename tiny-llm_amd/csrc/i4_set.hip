@@ -253,18 +253,6 @@ int set_shape(const I4Mat &mt, int group_size) {
     return mt.K <= 1024 ? 0 : (mt.K + 64 * 32 - 1) / (64 * 32);
 }
 
-int device_cus_set() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
-            return 1;  // no device: the launch that follows fails and reports it
-        cus = n;
-    }
-    return cus;
-}
-
 template <int R>
 void launch_r(int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream, const SetArgs &a) {
     switch (smax) {
@@ -288,7 +276,7 @@ int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream) {
     long short_rows = 0;
     for (int k = 0; k < n; ++k)
         if (shape[k] == 0) short_rows += mats[k].M;
-    const int R = short_rows > 16L * device_cus_set() ? 2 : 1;
+    const int R = short_rows > 16L * device_cu_count() ? 2 : 1;
     int blocks = 0, smax = 0, umax = 0;
     for (int k = 0; k < n; ++k) {
         const I4Mat &mt = mats[order[k]];
@@ -329,7 +317,7 @@ int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream
         blocks += shape[i] == 0 ? (mats[i].M + 4 * kSetWaves - 1) / (4 * kSetWaves)
                                 : (mats[i].M + kSetWaves - 1) / kSetWaves;
     }
-    if (blocks > static_cast<long>(kSetMaxBlocksPerCu) * device_cus_set()) return kNotFused;
+    if (blocks > static_cast<long>(kSetMaxBlocksPerCu) * device_cu_count()) return kNotFused;
     return launch_set(mats, shape, n, stream);
 }
 

@@ -1,6 +1,7 @@
 // scratch.cpp -- device scratch of the launches: the split-K exchange slots of
-// the matvec (all zero between launches) and the fp16 copy of X of the prefill
-// GEMM.
+// the matvec and the tile arrival counters of the few-token prefill kernel (all
+// zero between launches), and the prefill workspace (the fp16 copy of X of the
+// prefill GEMM, or the few-token kernel's partial products).
 //
 // Who owns which buffer:
 //   * Eager calls use the set of their (device, stream): launches on one stream
@@ -36,8 +37,8 @@ struct ScratchBuf {
 
 struct ScratchSet {
     std::mutex mu;
-    ScratchBuf split;  // split-K exchange slots: zero between launches
-    ScratchBuf xws;    // prefill fp16 X + per-token scale
+    ScratchBuf split;  // split-K exchange slots / arrival counters: zero between launches
+    ScratchBuf xws;    // prefill workspace
     std::vector<void *> retired;
     bool fixed = false;  // preset buffers, no growth (allocation-free entry point)
 };

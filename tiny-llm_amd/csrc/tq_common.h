@@ -99,6 +99,10 @@ inline size_t prefill_scratch_bytes(int K, int N) {
     return (Kp * 2 * static_cast<size_t>(N) + 255) / 256 * 256 + 4 * static_cast<size_t>(N);
 }
 
+// Compute units of the current device, looked up once (1 when there is no device: the launch
+// that follows fails and reports it). Defined in device.cpp.
+int device_cu_count();
+
 // ---- scratch memory (scratch.cpp) ---------------------------------------------------------
 // Split-K exchange slots (zero between launches) and the prefill X workspace. Eager
 // launches use the set of their (device, stream); inside a ScratchScope (graph capture,

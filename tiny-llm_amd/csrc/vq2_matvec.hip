@@ -234,23 +234,11 @@ __global__ __launch_bounds__(64 * kVq2Waves) void vq2_matvec_copies(const uint8_
     }
 }
 
-int device_cus_vq2() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
-            return 1;  // no device: the launch that follows fails and reports it
-        cus = n;
-    }
-    return cus;
-}
-
 }  // namespace
 
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream) {
     if (out_dim < 1 || in_dim < kVq2Dim || in_dim % kVq2Dim) return kBadShape;
-    const int cus = device_cus_vq2();
+    const int cus = device_cu_count();
     if ((in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0) {
         // index rows dword-aligned: the conflict-free kernel (16 waves x 4-row
         // tiles measured fastest at 3072..16384 rows, within 4% of the best at
