@@ -107,15 +107,6 @@ __device__ inline float half_bits_f(unsigned h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h & 0xFFFFu)));
 }
 
-// fp16 pair {q0 * s + c, q1 * s + c}: each computed exactly and rounded once
-// to fp16 (v_fma_mix with fp32 operands).
-__device__ inline unsigned fma_pair_f16(float q0, float q1, float s, float c) {
-    unsigned r;
-    asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,0,0]" : "=v"(r) : "v"(q0), "v"(s), "v"(c));
-    asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel_hi:[0,0,0]" : "+v"(r) : "v"(q1), "v"(s), "v"(c));
-    return r;
-}
-
 // 8 consecutive elements (one code dword, low nibble first) of one group as
 // the fp16 MFMA operand: q * scale - zero * scale, rounded once (within one
 // fp16 rounding of the reference's fp32 (q - zero) * scale).
@@ -130,19 +121,40 @@ __device__ inline float ubyte_f(unsigned v) {
     return f;
 }
 
+// q * s + nzs in fp32 is exact (q has 4 bits, s and the zero 11: q * s and nzs = -zero * s
+// are exact products and their sum needs at most 24 bits), so rounding it to fp16 with
+// v_cvt_pk_f16_f32 (round to nearest even) rounds once, as v_fma_mix would; measured on
+// MI355X v_fma_mix issues at a third to a quarter of the rate of v_fma_f32.
+// (asm: left to itself the compiler folds the fp32 FMA and the conversion back into v_fma_mix)
+__device__ inline unsigned pair_f16(float a, float b) {
+    unsigned r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// The group's scale and -zero * scale as plain fp32 registers: the compiler would otherwise fold
+// their fp16 -> fp32 conversion into every FMA as a v_fma_mix_f32 (the slow mixed-precision
+// form).
+__device__ inline void opaque_f32(float &s, float &nzs) { asm("" : "+v"(s), "+v"(nzs)); }
+
 __device__ inline h8 dequant8(unsigned c, float s, float nzs) {
     const unsigned lo = c & 0x0F0F0F0Fu;         // elements 0, 2, 4, 6
     const unsigned hi = (c >> 4) & 0x0F0F0F0Fu;  // elements 1, 3, 5, 7
     u4v pk;
-    pk[0] = fma_pair_f16(ubyte_f<0>(lo), ubyte_f<0>(hi), s, nzs);
-    pk[1] = fma_pair_f16(ubyte_f<1>(lo), ubyte_f<1>(hi), s, nzs);
-    pk[2] = fma_pair_f16(ubyte_f<2>(lo), ubyte_f<2>(hi), s, nzs);
-    pk[3] = fma_pair_f16(ubyte_f<3>(lo), ubyte_f<3>(hi), s, nzs);
+    pk[0] = pair_f16(fmaf(ubyte_f<0>(lo), s, nzs), fmaf(ubyte_f<0>(hi), s, nzs));
+    pk[1] = pair_f16(fmaf(ubyte_f<1>(lo), s, nzs), fmaf(ubyte_f<1>(hi), s, nzs));
+    pk[2] = pair_f16(fmaf(ubyte_f<2>(lo), s, nzs), fmaf(ubyte_f<2>(hi), s, nzs));
+    pk[3] = pair_f16(fmaf(ubyte_f<3>(lo), s, nzs), fmaf(ubyte_f<3>(hi), s, nzs));
     return __builtin_bit_cast(h8, pk);
 }
 
+// s_waitcnt vmcnt(n), expcnt / lgkmcnt untouched (gfx9 encoding). The count assumes the loads
+// issued before it in program order: the sched_barriers keep the machine scheduler from
+// moving a load across it (scheduling groups would otherwise carry a step's interleaved loads
+// past the next step's wait, and vmcnt(n) would then let that step's own loads still be in
+// flight).
 __device__ __forceinline__ void wait_vm(int n) {
-    // s_waitcnt vmcnt(n), expcnt / lgkmcnt untouched (gfx9 encoding)
+    __builtin_amdgcn_sched_barrier(0);
     switch (n) {
 #define TQ_VMWAIT(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); break;
         TQ_VMWAIT(0) TQ_VMWAIT(1) TQ_VMWAIT(2) TQ_VMWAIT(3) TQ_VMWAIT(4) TQ_VMWAIT(5) TQ_VMWAIT(6) TQ_VMWAIT(7)
@@ -152,15 +164,20 @@ __device__ __forceinline__ void wait_vm(int n) {
 #undef TQ_VMWAIT
         default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break;
     }
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Workgroup barrier that waits for this wave's LDS operations only (global ->
-// LDS transfers of later steps stay in flight).
+// LDS transfers of later steps stay in flight). The sched_barriers keep the machine
+// scheduler from moving anything across it (a memory clobber binds only the compiler's
+// IR passes: scheduling groups would otherwise hoist the step's LDS reads above it).
 __device__ inline void lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 constexpr int kWDwords = 10;                    // per row and step
@@ -512,13 +529,19 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma2(const uint8_t *__res
 
 // ---- 4. G = 64: W straight into registers
 //   At G = 64 a step's 64 elements of a row are one group: 36 contiguous bytes
-//   [scale | zero | 32 code bytes] at 36 s. Each lane loads its row's record
-//   with three loads (16 + 16 + 4 bytes) into VGPRs, S - 1 steps ahead, so W
+//   [scale | zero | 32 code bytes] at 36 s. Lane (row, half h) loads the group
+//   header and the 16 code bytes of its half into VGPRs, S - 1 steps ahead, so W
 //   never passes through LDS (measured: the dword-granular W staging of
 //   i4_matmul_mfma2 was 40% of its time). X is staged as in i4_matmul_mfma2.
 //   The loop is unrolled by S so that every register slot index is a
 //   constant; steps past the last are loaded (never consumed) and not
 //   computed, which keeps every wait one constant s_waitcnt.
+//   Measured per wave on MI355X at 512 tokens (cycle counters around the loop
+//   phases): about a third of the time went to issuing a step's loads (the CU's
+//   memory pipeline takes some 64 bytes a clock, and a step of two workgroups
+//   per CU asks for ~40 KB), half to the dequantization and MFMAs, and the
+//   waits for data and the barrier took under a tenth. Hence 20 bytes of W per
+//   lane (not the whole 36-byte record) and the fp32 dequantization.
 __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char *st, const int *xvo, int nx, int xso,
                                         int wave) {
 #pragma unroll
@@ -527,16 +550,16 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char
             xr, (__attribute__((address_space(3))) void *)(st + 1024 * (nx * wave + q)), 16, xvo[q], xso, 0, 0);
 }
 
-template <int WN, int S, int NWV>
+template <int WM, int WN, int S, int NWV>
 __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restrict__ w,
                                                           const _Float16 *__restrict__ xh,
                                                           const float *__restrict__ xinv, float *__restrict__ y, int M,
                                                           int N, int K, int Kp, int row_bytes) {
     constexpr int BN = 32 * WN;
-    constexpr int BM = 32 * NWV;
+    constexpr int BM = 32 * WM * NWV;
     constexpr int XStage = BN * 128;
     constexpr int XD = 4 * WN / NWV;  // X DMAs per wave per step
-    constexpr int P = 3 + XD;         // loads per wave per step: W 16 + 16 + 4 bytes, the X DMAs
+    constexpr int P = 2 * WM + XD;    // loads per wave per step: per row block W 4 + 16 bytes, the X DMAs
     static_assert(4 * WN % NWV == 0, "X DMAs split evenly over the waves");
     constexpr int kGroupBytes = 36;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -550,8 +573,13 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
                                                 static_cast<size_t>(M - m0) * row_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh + static_cast<size_t>(n0) * Kp,
                                                 static_cast<size_t>(N - n0) * Kp * 2);
-    const int li = lane & 31, kq = lane >> 5;
-    const int wvo = (32 * wave + li) * row_bytes;
+    // Lane (row li of each of the wave's row blocks, half h) takes elements 32 h .. 32 h + 31 of
+    // every step: the group header and code bytes 16 h .. 16 h + 15; MFMA k-slot 8 h + p of
+    // k-block kk holds element 32 h + 8 kk + p on the A (W) and the B (X) side.
+    const int li = lane & 31, h = lane >> 5;
+    int wvo[WM];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) wvo[i] = (32 * (WM * wave + i) + li) * row_bytes;
     int xvo[XD];
 #pragma unroll
     for (int q = 0; q < XD; ++q) {
@@ -565,22 +593,26 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
             const int r = 32 * j + li;
-            xro[kk][j] = 16 * (8 * r + ((2 * kk + kq) ^ ((r >> 1) & 7)));
+            xro[kk][j] = 16 * (8 * r + ((4 * h + kk) ^ ((r >> 1) & 7)));
         }
 
-    u4v wa[S], wb[S];
-    unsigned wc[S];
+    unsigned hd[S][WM];
+    u4v cd[S][WM];
     auto issue = [&](auto uc, int s) {  // step s into register slot and X stage u = s % S
         constexpr int u = decltype(uc)::value;
         const int so = kGroupBytes * min(s, groups - 1);  // (past the last step: in-row bytes, never used)
-        wa[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo, so, 0));
-        wb[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo + 16, so, 0));
-        wc[u] = __builtin_amdgcn_raw_buffer_load_b32(wr, wvo + 32, so, 0);
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            hd[u][i] = __builtin_amdgcn_raw_buffer_load_b32(wr, wvo[i], so, 0);
+            cd[u][i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo[i] + 4 + 16 * h, so, 0));
+        }
         issue_x(xr, smem + u * XStage, xvo, XD, s * kStepK * 2, wave);
     };
-    f16x acc[WN];
+    f16x acc[WM][WN];
 #pragma unroll
-    for (int j = 0; j < WN; ++j) acc[j] = f16x{};
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = f16x{};
     auto compute = [&](auto uc) {
         constexpr int u = decltype(uc)::value;
         const unsigned char *st = smem + u * XStage;
@@ -589,40 +621,55 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
         for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
             for (int j = 0; j < WN; ++j) b[kk][j] = *reinterpret_cast<const h8 *>(st + xro[kk][j]);
-        // code dword i of the group: 0..2 in wa.yzw, 3..6 in wb, 7 in wc; lane half kq takes i = 2 kk' + kq
-        const unsigned c[4] = {kq ? wa[u].z : wa[u].y, kq ? wb[u].x : wa[u].w, kq ? wb[u].z : wb[u].y,
-                               kq ? wc[u] : wb[u].w};
-        const unsigned hd = wa[u].x;
-        const float sc = half_bits_f(hd);
-        const float zs = -(half_bits_f(hd >> 16) * sc);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const h8 a = dequant8(c[kk], sc, zs);
+        for (int i = 0; i < WM; ++i) {
+            float sc = half_bits_f(hd[u][i]);
+            float zs = -(half_bits_f(hd[u][i] >> 16) * sc);
+            opaque_f32(sc, zs);
 #pragma unroll
-            for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[kk][j], acc[j], 0, 0, 0);
+            for (int kk = 0; kk < 4; ++kk) {
+                const h8 a = dequant8(cd[u][i][kk], sc, zs);
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[kk][j], acc[i][j], 0, 0, 0);
+            }
         }
     };
-    auto round_step = [&](auto uc, int s) {
+    // full: the step is below `steps` (no branch: the loads of step s + S - 1 and the MFMAs of
+    // step s share one block for the scheduler)
+    auto round_step = [&](auto uc, int s, auto full) {
         constexpr int u = decltype(uc)::value;
         wait_vm((S - 2) * P);  // this wave's loads of step s have landed
         lds_barrier();         // every wave's X part has; step s - 1's stage is free
         issue(std::integral_constant<int, (u + S - 1) % S>{}, s + S - 1);
-        if (s < steps) compute(uc);
+        if constexpr (decltype(full)::value)
+            compute(uc);
+        else if (s < steps)
+            compute(uc);
     };
 
     issue(std::integral_constant<int, 0>{}, 0);
     if constexpr (S > 2) issue(std::integral_constant<int, 1>{}, 1);
     if constexpr (S > 3) issue(std::integral_constant<int, 2>{}, 2);
     static_assert(S >= 2 && S <= 4, "register slots 0..3");
-    for (int s0 = 0; s0 < steps; s0 += S) {
-        round_step(std::integral_constant<int, 0>{}, s0);
-        round_step(std::integral_constant<int, 1>{}, s0 + 1);
-        if constexpr (S > 2) round_step(std::integral_constant<int, 2>{}, s0 + 2);
-        if constexpr (S > 3) round_step(std::integral_constant<int, 3>{}, s0 + 3);
+    const std::true_type full;
+    const std::false_type tail;
+    int s0 = 0;
+    for (; s0 + S <= steps; s0 += S) {
+        round_step(std::integral_constant<int, 0>{}, s0, full);
+        round_step(std::integral_constant<int, 1>{}, s0 + 1, full);
+        if constexpr (S > 2) round_step(std::integral_constant<int, 2>{}, s0 + 2, full);
+        if constexpr (S > 3) round_step(std::integral_constant<int, 3>{}, s0 + 3, full);
+    }
+    if (s0 < steps) {
+        round_step(std::integral_constant<int, 0>{}, s0, tail);
+        round_step(std::integral_constant<int, 1>{}, s0 + 1, tail);
+        if constexpr (S > 2) round_step(std::integral_constant<int, 2>{}, s0 + 2, tail);
+        if constexpr (S > 3) round_step(std::integral_constant<int, 3>{}, s0 + 3, tail);
     }
     wait_vm(0);
 
-    // epilogue: lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32
+    // epilogue: lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32 of each block
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
         const int n = n0 + 32 * j + li;
@@ -630,12 +677,14 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
         const float sc = xinv[n];
         float *yc = y + static_cast<size_t>(n) * M;
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-            const int m = m0 + 32 * wave + 8 * r4 + 4 * kq;
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (m + q < M) yc[m + q] = acc[j][4 * r4 + q] * sc;
-        }
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int m = m0 + 32 * (WM * wave + i) + 8 * r4 + 4 * h;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (m + q < M) yc[m + q] = acc[i][j][4 * r4 + q] * sc;
+            }
     }
 }
 
@@ -749,8 +798,8 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
     for (int q = 0; q < 2 * SMAX; ++q) {
         const int c = (sub >> 1) + 4 * (q & 1);  // 16-byte chunk of step q / 2
         uint2 pk;
-        pk.x = fma_pair_f16(xv[q].x, xv[q].y, sc, 0.f);
-        pk.y = fma_pair_f16(xv[q].z, xv[q].w, sc, 0.f);
+        pk.x = pair_f16(xv[q].x * sc, xv[q].y * sc);  // exact scaling, one rounding
+        pk.y = pair_f16(xv[q].z * sc, xv[q].w * sc);
         *reinterpret_cast<uint2 *>(xs + 4096 * (q >> 1) + 128 * n + 16 * (c ^ (n & 7)) + 8 * (sub & 1)) = pk;
     }
     lds_barrier();
@@ -766,8 +815,9 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
             unsigned cd[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) cd[kk] = wl[9 * j + 1 + 4 * h + kk];
-            const float s = half_bits_f(hd);
-            const float zs = -(half_bits_f(hd >> 16) * s);
+            float s = half_bits_f(hd);
+            float zs = -(half_bits_f(hd >> 16) * s);
+            opaque_f32(s, zs);
             h8 b[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
@@ -916,21 +966,21 @@ int launch_tiles2(const uint8_t *w, const _Float16 *xh, const float *xinv, float
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
-template <int WN, int S, int NWV>
+template <int WM, int WN, int S, int NWV>
 int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y, int M, int N, int K, int Kp, int rb,
                hipStream_t stream) {
-    constexpr int BN = 32 * WN, BM = 32 * NWV;
+    constexpr int BN = 32 * WN, BM = 32 * WM * NWV;
     const size_t lds = static_cast<size_t>(S) * BN * 128;
     static size_t limit = 0;
     if (lds > 64 * 1024 && limit == 0) {
-        const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WN, S, NWV>);
+        const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WM, WN, S, NWV>);
         if (raise_lds_limit(fn, limit) != kOk) return kLaunchFailed;
     }
     if (lds > 64 * 1024 && lds > limit) return kTooLarge;
     if (static_cast<size_t>(BM) * rb + static_cast<size_t>(Kp) * 2 * BN >= (1ull << 31)) return kTooLarge;
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
-    hipLaunchKernelGGL((i4_matmul_g64<WN, S, NWV>), grid, dim3(64 * NWV), lds, stream, w, xh, xinv, y, M, N, K, Kp,
-                       rb);
+    hipLaunchKernelGGL((i4_matmul_g64<WM, WN, S, NWV>), grid, dim3(64 * NWV), lds, stream, w, xh, xinv, y, M, N, K,
+                       Kp, rb);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -1022,9 +1072,12 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
     if (group_size == 64) {
         // one-wave workgroups of 32 rows for a single token block: four times
         // the workgroups (304 at 9728 rows), each with a wave-private X ring
-        st = wn == 1   ? launch_g64<1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-             : wn == 2 ? launch_g64<2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-                       : launch_g64<3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
+        // one row block per wave: measured on MI355X at 9728x2560, two (a 256-row tile, one
+        // wave per SIMD) ran 512 tokens in 63 us against 55, and staging W through LDS in
+        // 3-step chunks did not beat the loads straight into registers
+        st = wn == 1   ? launch_g64<1, 1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+             : wn == 2 ? launch_g64<1, 2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+                       : launch_g64<1, 3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
         if (st != kTooLarge) return st;
         st = wn == 1   ? launch_tiles2<1, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
              : wn == 2 ? launch_tiles2<2, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
