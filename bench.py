@@ -278,6 +278,25 @@ def ceilings(tq, stream):
         for blocks in (2048, 4096, 8192):
             ms = timed(lambda: lib.tqceil_stream_read(buf.ptr, nb, out.ptr, blocks, variant, sp))
             read[f"{names[variant]}, {blocks} wg"] = nb / (ms * 1e-3) / 1e9
+    # cold reads of one matrix's size (the configs[2] and VQ2 shapes), one launch each at offsets
+    # rotating through the 1 GiB buffer, back to back: the floor a single matvec launch of that
+    # many bytes can reach here (launch cost and the ramp to full bandwidth included)
+    sized = {}
+    for size in (804864, 5924864, 14057472, 34647040):
+        step = (size + 4095) // 4096 * 4096
+        offs = [(i * step) % (nb - step) for i in range(60)]
+        best_s = None
+        for variant in (1, 2):
+            for blocks in (256, 512, 1024, 2048):
+                def batch():
+                    for o in offs:
+                        lib.tqceil_stream_read(buf.ptr + o, size // 16 * 16, out.ptr, blocks, variant, sp)
+                ms = timed(batch, 1, batches=5) / len(offs)
+                if best_s is None or ms < best_s[0]:
+                    best_s = (ms, variant, blocks)
+        sized[str(size)] = {"us": round(best_s[0] * 1e3, 2), "gbs": round(size / (best_s[0] * 1e-3) / 1e9, 1),
+                            "frac": round(size / (best_s[0] * 1e-3) / 1e9 / PEAK_GBS, 4),
+                            "best": f"{names[best_s[1]]}, {best_s[2]} wg"}
     buf.free()
     best = max(read, key=read.get)
     # one L2-resident buffer (32 tokens x 2560 fp32, the few-token GEMM's X) read whole by every workgroup
@@ -303,6 +322,8 @@ def ceilings(tq, stream):
     return {"stream_read_gbs": round(read[best], 1), "stream_read_frac": round(read[best] / PEAK_GBS, 4),
             "stream_read": {"bytes": nb, "best": best, "gbs": {k: round(v, 1) for k, v in read.items()}},
             "empty_launch_us": empty,
+            "cold_read_one_launch": {"note": "one launch reading N cold bytes, back to back (bytes -> us)",
+                                     "sizes": sized},
             "shared_read": {"bytes": sb, "note": "every workgroup reads the same buffer; GB/s per CU of 256",
                             "runs": shared},
             "mfma_f16_tflops": round(tflops, 1), "mfma_f16_frac": round(tflops / PEAK_MFMA_TFLOPS, 4),

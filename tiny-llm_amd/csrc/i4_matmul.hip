@@ -45,6 +45,17 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void *base, size_t byte
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), nrec, kBufferFlags);
 }
 
+// q * s + nzs in fp32 is exact (q has 4 bits, s and the zero 11: q * s and nzs = -zero * s
+// are exact products and their sum needs at most 24 bits), so rounding it to fp16 with
+// v_cvt_pk_f16_f32 (round to nearest even) rounds once, as v_fma_mix would; measured on
+// MI355X v_fma_mix issues at a third to a quarter of the rate of v_fma_f32.
+// (asm: left to itself the compiler folds the fp32 FMA and the conversion back into v_fma_mix)
+__device__ inline unsigned pair_f16(float a, float b) {
+    unsigned r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // ---- 1. X (fp32, column n = token) -> fp16 * 2^e_n, rows padded to Kp.
 // One workgroup per token; the column is read once into registers (Kp <= 256 *
 // kXRegs), its max taken, then converted and stored. Longer columns: two passes.
@@ -119,17 +130,6 @@ __device__ inline float ubyte_f(unsigned v) {
     if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
     if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
     return f;
-}
-
-// q * s + nzs in fp32 is exact (q has 4 bits, s and the zero 11: q * s and nzs = -zero * s
-// are exact products and their sum needs at most 24 bits), so rounding it to fp16 with
-// v_cvt_pk_f16_f32 (round to nearest even) rounds once, as v_fma_mix would; measured on
-// MI355X v_fma_mix issues at a third to a quarter of the rate of v_fma_f32.
-// (asm: left to itself the compiler folds the fp32 FMA and the conversion back into v_fma_mix)
-__device__ inline unsigned pair_f16(float a, float b) {
-    unsigned r;
-    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
 }
 
 // The group's scale and -zero * scale as plain fp32 registers: the compiler would otherwise fold
@@ -550,16 +550,16 @@ __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char
             xr, (__attribute__((address_space(3))) void *)(st + 1024 * (nx * wave + q)), 16, xvo[q], xso, 0, 0);
 }
 
-template <int WM, int WN, int S, int NWV>
+template <int WN, int S, int NWV>
 __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restrict__ w,
                                                           const _Float16 *__restrict__ xh,
                                                           const float *__restrict__ xinv, float *__restrict__ y, int M,
                                                           int N, int K, int Kp, int row_bytes) {
     constexpr int BN = 32 * WN;
-    constexpr int BM = 32 * WM * NWV;
+    constexpr int BM = 32 * NWV;
     constexpr int XStage = BN * 128;
     constexpr int XD = 4 * WN / NWV;  // X DMAs per wave per step
-    constexpr int P = 2 * WM + XD;    // loads per wave per step: per row block W 4 + 16 bytes, the X DMAs
+    constexpr int P = 2 + XD;         // loads per wave per step: W 4 + 16 bytes, the X DMAs
     static_assert(4 * WN % NWV == 0, "X DMAs split evenly over the waves");
     constexpr int kGroupBytes = 36;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -573,13 +573,11 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
                                                 static_cast<size_t>(M - m0) * row_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(xh + static_cast<size_t>(n0) * Kp,
                                                 static_cast<size_t>(N - n0) * Kp * 2);
-    // Lane (row li of each of the wave's row blocks, half h) takes elements 32 h .. 32 h + 31 of
-    // every step: the group header and code bytes 16 h .. 16 h + 15; MFMA k-slot 8 h + p of
-    // k-block kk holds element 32 h + 8 kk + p on the A (W) and the B (X) side.
+    // Lane (row li, half h) takes elements 32 h .. 32 h + 31 of every step: the group header
+    // and code bytes 16 h .. 16 h + 15; MFMA k-slot 8 h + p of k-block kk holds element
+    // 32 h + 8 kk + p on the A (W) and the B (X) side.
     const int li = lane & 31, h = lane >> 5;
-    int wvo[WM];
-#pragma unroll
-    for (int i = 0; i < WM; ++i) wvo[i] = (32 * (WM * wave + i) + li) * row_bytes;
+    const int wvo = (32 * wave + li) * row_bytes;
     int xvo[XD];
 #pragma unroll
     for (int q = 0; q < XD; ++q) {
@@ -596,56 +594,50 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
             xro[kk][j] = 16 * (8 * r + ((4 * h + kk) ^ ((r >> 1) & 7)));
         }
 
-    unsigned hd[S][WM];
-    u4v cd[S][WM];
+    unsigned hd[S];
+    u4v cd[S];
     auto issue = [&](auto uc, int s) {  // step s into register slot and X stage u = s % S
         constexpr int u = decltype(uc)::value;
         const int so = kGroupBytes * min(s, groups - 1);  // (past the last step: in-row bytes, never used)
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            hd[u][i] = __builtin_amdgcn_raw_buffer_load_b32(wr, wvo[i], so, 0);
-            cd[u][i] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo[i] + 4 + 16 * h, so, 0));
-        }
+        hd[u] = __builtin_amdgcn_raw_buffer_load_b32(wr, wvo, so, 0);
+        cd[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo + 4 + 16 * h, so, 0));
         issue_x(xr, smem + u * XStage, xvo, XD, s * kStepK * 2, wave);
     };
-    f16x acc[WM][WN];
+    f16x acc[WN];
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) acc[i][j] = f16x{};
-    auto compute = [&](auto uc) {
+    for (int j = 0; j < WN; ++j) acc[j] = f16x{};
+    // k-blocks k0 .. k1 - 1 of the step in register slot and X stage u
+    auto compute = [&](auto uc, int k0, int k1) {
         constexpr int u = decltype(uc)::value;
         const unsigned char *st = smem + u * XStage;
-        h8 b[4][WN];
+        float sc = half_bits_f(hd[u]);
+        float zs = -(half_bits_f(hd[u] >> 16) * sc);
+        opaque_f32(sc, zs);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
+        for (int kk = k0; kk < k1; ++kk) {
+            h8 b[WN];
 #pragma unroll
-            for (int j = 0; j < WN; ++j) b[kk][j] = *reinterpret_cast<const h8 *>(st + xro[kk][j]);
+            for (int j = 0; j < WN; ++j) b[j] = *reinterpret_cast<const h8 *>(st + xro[kk][j]);
+            const h8 a = dequant8(cd[u][kk], sc, zs);
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            float sc = half_bits_f(hd[u][i]);
-            float zs = -(half_bits_f(hd[u][i] >> 16) * sc);
-            opaque_f32(sc, zs);
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const h8 a = dequant8(cd[u][i][kk], sc, zs);
-#pragma unroll
-                for (int j = 0; j < WN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[kk][j], acc[i][j], 0, 0, 0);
-            }
+            for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[j], acc[j], 0, 0, 0);
         }
     };
-    // full: the step is below `steps` (no branch: the loads of step s + S - 1 and the MFMAs of
-    // step s share one block for the scheduler)
+    // full: the step is below `steps`. Its loads of step s + S - 1 go in between the first and
+    // the last two k-blocks' MFMAs (program order; no branch), so that a wave stalled on a full
+    // memory pipeline has MFMAs in flight.
     auto round_step = [&](auto uc, int s, auto full) {
         constexpr int u = decltype(uc)::value;
         wait_vm((S - 2) * P);  // this wave's loads of step s have landed
         lds_barrier();         // every wave's X part has; step s - 1's stage is free
-        issue(std::integral_constant<int, (u + S - 1) % S>{}, s + S - 1);
-        if constexpr (decltype(full)::value)
-            compute(uc);
-        else if (s < steps)
-            compute(uc);
+        if constexpr (decltype(full)::value) {
+            compute(uc, 0, 2);
+            issue(std::integral_constant<int, (u + S - 1) % S>{}, s + S - 1);
+            compute(uc, 2, 4);
+        } else {
+            issue(std::integral_constant<int, (u + S - 1) % S>{}, s + S - 1);
+            if (s < steps) compute(uc, 0, 4);
+        }
     };
 
     issue(std::integral_constant<int, 0>{}, 0);
@@ -669,7 +661,7 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
     }
     wait_vm(0);
 
-    // epilogue: lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32 of each block
+    // epilogue: lane holds rows (r/4)*8 + (lane/32)*4 + r%4 of column lane%32
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
         const int n = n0 + 32 * j + li;
@@ -677,14 +669,12 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
         const float sc = xinv[n];
         float *yc = y + static_cast<size_t>(n) * M;
 #pragma unroll
-        for (int i = 0; i < WM; ++i)
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int m = m0 + 32 * wave + 8 * r4 + 4 * h;
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int m = m0 + 32 * (WM * wave + i) + 8 * r4 + 4 * h;
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (m + q < M) yc[m + q] = acc[i][j][4 * r4 + q] * sc;
-            }
+            for (int q = 0; q < 4; ++q)
+                if (m + q < M) yc[m + q] = acc[j][4 * r4 + q] * sc;
+        }
     }
 }
 
@@ -966,21 +956,21 @@ int launch_tiles2(const uint8_t *w, const _Float16 *xh, const float *xinv, float
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
-template <int WM, int WN, int S, int NWV>
+template <int WN, int S, int NWV>
 int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y, int M, int N, int K, int Kp, int rb,
                hipStream_t stream) {
-    constexpr int BN = 32 * WN, BM = 32 * WM * NWV;
+    constexpr int BN = 32 * WN, BM = 32 * NWV;
     const size_t lds = static_cast<size_t>(S) * BN * 128;
     static size_t limit = 0;
     if (lds > 64 * 1024 && limit == 0) {
-        const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WM, WN, S, NWV>);
+        const void *fn = reinterpret_cast<const void *>(i4_matmul_g64<WN, S, NWV>);
         if (raise_lds_limit(fn, limit) != kOk) return kLaunchFailed;
     }
     if (lds > 64 * 1024 && lds > limit) return kTooLarge;
     if (static_cast<size_t>(BM) * rb + static_cast<size_t>(Kp) * 2 * BN >= (1ull << 31)) return kTooLarge;
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
-    hipLaunchKernelGGL((i4_matmul_g64<WM, WN, S, NWV>), grid, dim3(64 * NWV), lds, stream, w, xh, xinv, y, M, N, K,
-                       Kp, rb);
+    hipLaunchKernelGGL((i4_matmul_g64<WN, S, NWV>), grid, dim3(64 * NWV), lds, stream, w, xh, xinv, y, M, N, K, Kp,
+                       rb);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -1072,12 +1062,13 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
     if (group_size == 64) {
         // one-wave workgroups of 32 rows for a single token block: four times
         // the workgroups (304 at 9728 rows), each with a wave-private X ring
-        // one row block per wave: measured on MI355X at 9728x2560, two (a 256-row tile, one
-        // wave per SIMD) ran 512 tokens in 63 us against 55, and staging W through LDS in
-        // 3-step chunks did not beat the loads straight into registers
-        st = wn == 1   ? launch_g64<1, 1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-             : wn == 2 ? launch_g64<1, 2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-                       : launch_g64<1, 3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
+        // Tiles measured on MI355X at 9728x2560 (512 / 128 tokens): 128 x 96 52.9 / 33.0 us,
+        // 128 x 64 57.9 / 27.7, 128 x 128 58.7 / 38.9; two or more row blocks per wave
+        // (256 x 96, 256 x 64, 128 x 96 over 2 waves, ...) 66-82 / 40-72; and staging W
+        // through LDS in 3-step chunks did not beat the loads straight into registers.
+        st = wn == 1   ? launch_g64<1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+             : wn == 2 ? launch_g64<2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+                       : launch_g64<3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
         if (st != kTooLarge) return st;
         st = wn == 1   ? launch_tiles2<1, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
              : wn == 2 ? launch_tiles2<2, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
