@@ -1,8 +1,8 @@
 """The allocation-free prefill entry point (tqhip_matmul_i4_noalloc_dev) against
 tqhip_matmul_i4_dev, through the C ABI.
 
-Both run the same kernels; the only difference is where X's fp16 copy lives (the
-library's static device array instead of a stream's grow-only buffer), so the
+Both run the same kernels; the only difference is where their scratch lives (the
+library's static device array instead of a stream's grow-only buffers), so the
 outputs must agree bit for bit, call after call, with the second call of each
 pair smaller than the first (the array keeps the previous call's contents). The
 results are also held to the prefill bar against the oracle, and a call that
@@ -27,19 +27,29 @@ def run_pair(gpu, w, x, M, K, N, G, stream):
     return ya.download(np.float32, M * N), yb.download(np.float32, M * N)
 
 
-@pytest.mark.parametrize("G", [64, 40])
-def test_noalloc_matches_dev_entry_point(gpu, orc, G):
+# G = 64 above 32 tokens: the MFMA GEMM (512 tokens at K = 2560 uses 10.5 MB of the 16 MiB), then
+# a smaller call over the same array. G = 64 up to 32 tokens: the few-token kernel (partial
+# products in the array, tile counters in its last 64 KiB, which every launch must leave at
+# zero for the next: 32 tokens, a smaller call with fewer tiles, 32 tokens again). G = 40: one
+# matvec per token column, no scratch.
+NOALLOC_CASES = {
+    "gemm": (64, [(9728, 2560, 512), (896, 896, 40)]),
+    "few-token": (64, [(9728, 2560, 32), (4096, 2560, 7), (9728, 2560, 32)]),
+    "per-column": (40, [(640, 520, 9), (200, 280, 3)]),
+}
+
+
+@pytest.mark.parametrize("kind", list(NOALLOC_CASES))
+def test_noalloc_matches_dev_entry_point(gpu, orc, kind):
     stream = gpu.Stream()
-    # G = 64: the MFMA GEMM (512 tokens at K = 2560 uses 10.5 MB of the 16 MiB), then a
-    # smaller call over the same array; G = 40: one matvec per token column, no scratch.
-    cases = [(9728, 2560, 512), (896, 896, 40)] if G == 64 else [(640, 520, 9), (200, 280, 3)]
+    G, cases = NOALLOC_CASES[kind]
     for i, (M, K, N) in enumerate(cases):
-        print(f"[no-alloc] G={G} call {i}: M={M} K={K} N={N}", flush=True)
+        print(f"[no-alloc] {kind} call {i}: M={M} K={K} N={N} G={G}", flush=True)
         w = gpu.synth_i4(M, K, G, seed=700 + 10 * i + G)
         x = gpu.synth_normal(K * N, seed=701 + 10 * i + G)
         want, got = run_pair(gpu, w, x, M, K, N, G, stream)
         assert np.array_equal(got, want), f"call {i}: no-alloc result differs from tqhip_matmul_i4_dev"
-        if M * N <= 896 * 40:  # the oracle at sizes it finishes in seconds
+        if M * N <= 9728 * 32:  # the oracle at sizes it finishes in seconds
             ref = orc.matmul_i4(w, x, M, K, N, G, threads=16)
         else:  # sampled rows of the 9728x2560x512 call
             rows = np.arange(0, M, 97)
