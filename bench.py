@@ -588,7 +588,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
     ap.add_argument("--no-configs2", action="store_true", help="skip the configs[2] gate/up, down and attention matvecs")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the stream-read / launch / MFMA ceilings")
-    ap.add_argument("--only", choices=("prefill", "vq2", "headline", "configs2", "ceilings"),
+    ap.add_argument("--only", choices=("prefill", "vq2", "headline", "configs2", "ceilings", "engine"),
                     help="run just this section and print its JSON (for profiler runs; not the contract line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first run one device-to-device copy of MB MiB (a known-size kernel for counter runs)")
@@ -615,6 +615,9 @@ def main():
         a.free()
         b.free()
     if args.only:
+        if args.only == "engine":
+            print(json.dumps({"engine": engine(tq, args.steps, args.warmup)}), flush=True)
+            return
         fn = {"prefill": prefill, "vq2": vq2, "headline": headline, "configs2": configs2, "ceilings": ceilings}[args.only]
         print(json.dumps({args.only: fn(tq, stream)}), flush=True)
         return

@@ -690,7 +690,9 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
 //   - X: the slice of the 32 token rows is read once (fp32, 16-byte loads), scaled per
 //     token by the power of two that puts the token's largest |x| in the slice into
 //     [2^13, 2^14), and stored to LDS as fp16, [step][token][64 elements] with the
-//     16-byte chunks of token n at positions c ^ (n & 7).
+//     16-byte chunks of token n at positions c ^ ((n >> 1) & 7): the 16 rows a
+//     ds_read_b128 pass serves cover one 256-byte bank sweep exactly (rows n and n + 8 on
+//     the same chunk, as c ^ (n & 7) had them, share banks).
 //   - W: each row's slice (9 dwords a step, contiguous) comes in with one DMA into LDS at
 //     an odd dword pitch. (A load per lane and row touches a cache line per lane; the
 //     DMA touches the 2-3 lines the slice spans.) Wave w then takes rows 32 w .. 32 w + 31:
@@ -790,7 +792,7 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
         uint2 pk;
         pk.x = pair_f16(xv[q].x * sc, xv[q].y * sc);  // exact scaling, one rounding
         pk.y = pair_f16(xv[q].z * sc, xv[q].w * sc);
-        *reinterpret_cast<uint2 *>(xs + 4096 * (q >> 1) + 128 * n + 16 * (c ^ (n & 7)) + 8 * (sub & 1)) = pk;
+        *reinterpret_cast<uint2 *>(xs + 4096 * (q >> 1) + 128 * n + 16 * (c ^ ((n >> 1) & 7)) + 8 * (sub & 1)) = pk;
     }
     lds_barrier();
 
@@ -811,7 +813,7 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
             h8 b[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
-                b[kk] = *reinterpret_cast<const h8 *>(xs + 4096 * j + 128 * li + 16 * ((4 * h + kk) ^ (li & 7)));
+                b[kk] = *reinterpret_cast<const h8 *>(xs + 4096 * j + 128 * li + 16 * ((4 * h + kk) ^ ((li >> 1) & 7)));
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
                 acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(dequant8(cd[kk], s, zs), b[kk], acc, 0, 0, 0);
