@@ -59,7 +59,13 @@ __device__ inline unsigned pair_f16(float a, float b) {
 // ---- 1. X (fp32, column n = token) -> fp16 * 2^e_n, rows padded to Kp.
 // One workgroup per token; the column is read once into registers (Kp <= 256 *
 // kXRegs), its max taken, then converted and stored. Longer columns: two passes.
+// PERM: within every 8 elements, element e goes to position ((e & 3) << 1) | (e >> 2), the
+// k-slot order in which the packed-fp16 dequantization leaves a code dword's elements.
+__device__ __forceinline__ int x_pos(int k, bool perm) {
+    return perm ? (k & ~7) | ((k & 3) << 1) | ((k >> 2) & 1) : k;
+}
 constexpr int kXRegs = 16;
+template <bool PERM>
 __global__ __launch_bounds__(256) void x_to_f16(const float *__restrict__ x, int K, int Kp, _Float16 *__restrict__ xh,
                                                   float *__restrict__ xinv) {
     const int n = blockIdx.x;
@@ -87,11 +93,12 @@ __global__ __launch_bounds__(256) void x_to_f16(const float *__restrict__ x, int
 #pragma unroll
     for (int i = 0; i < kXRegs; ++i) {
         const int k = threadIdx.x + i * 256;
-        if (k < Kp) hc[k] = static_cast<_Float16>(ldexpf(v[i], e));
+        if (k < Kp) hc[x_pos(k, PERM)] = static_cast<_Float16>(ldexpf(v[i], e));
     }
     if (threadIdx.x == 0) xinv[n] = ldexpf(1.f, -e);
 }
 
+template <bool PERM>
 __global__ __launch_bounds__(256) void x_to_f16_long(const float *__restrict__ x, int K, int Kp,
                                                        _Float16 *__restrict__ xh, float *__restrict__ xinv) {
     const int n = blockIdx.x;
@@ -110,7 +117,8 @@ __global__ __launch_bounds__(256) void x_to_f16_long(const float *__restrict__ x
         e = min(max(15 - E, -120), 120);
     }
     _Float16 *hc = xh + static_cast<size_t>(n) * Kp;
-    for (int k = threadIdx.x; k < Kp; k += blockDim.x) hc[k] = static_cast<_Float16>(k < K ? ldexpf(xc[k], e) : 0.f);
+    for (int k = threadIdx.x; k < Kp; k += blockDim.x)
+        hc[x_pos(k, PERM)] = static_cast<_Float16>(k < K ? ldexpf(xc[k], e) : 0.f);
     if (threadIdx.x == 0) xinv[n] = ldexpf(1.f, -e);
 }
 
@@ -145,6 +153,55 @@ __device__ inline h8 dequant8(unsigned c, float s, float nzs) {
     pk[1] = pair_f16(fmaf(ubyte_f<1>(lo), s, nzs), fmaf(ubyte_f<1>(hi), s, nzs));
     pk[2] = pair_f16(fmaf(ubyte_f<2>(lo), s, nzs), fmaf(ubyte_f<2>(hi), s, nzs));
     pk[3] = pair_f16(fmaf(ubyte_f<3>(lo), s, nzs), fmaf(ubyte_f<3>(hi), s, nzs));
+    return __builtin_bit_cast(h8, pk);
+}
+
+// ---- packed-fp16 dequantization (the G = 64 GEMM)
+// A nibble q OR-ed into the mantissa of a fixed fp16 exponent reads as 1024 + q (bits 0..3 under
+// exponent 2^10) or 64 + q (bits 4..7 under 2^6), both exact; subtracting 1024 or 64 gives q
+// exactly, and fma(q, s, fp16(-z s)) rounds once. Eight elements cost 13 instructions (one shift,
+// four v_and_or_b32, four v_pk_add_f16, four v_pk_fma_f16) against 23 for the fp32 form. The
+// halves come out in the k-slot order (0, 4, 1, 5, 2, 6, 3, 7) of the code dword's elements, so
+// X is stored in that order within every 8 elements (x_to_f16 with kPermute).
+typedef _Float16 hf2 __attribute__((ext_vector_type(2)));
+__device__ inline hf2 as_h2(unsigned u) { return __builtin_bit_cast(hf2, u); }
+__device__ inline unsigned as_u(hf2 h) { return __builtin_bit_cast(unsigned, h); }
+// (v_and_or_b32 is a VOP3 instruction: its two constants cannot both be literals, so the magic
+// exponent comes in a VGPR and the mask in an SGPR)
+__device__ inline unsigned and_or(unsigned c, unsigned mask, unsigned magic) {
+    unsigned r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(c), "s"(mask), "v"(magic));
+    return r;
+}
+// element e of the code dword sits at k-slot ((e & 3) << 1) | (e >> 2)
+__device__ __host__ constexpr int pk_slot(int e) { return ((e & 3) << 1) | (e >> 2); }
+struct PkConst {
+    unsigned k64, k54;  // the two magic exponents, held in VGPRs
+};
+__device__ inline PkConst pk_const() {
+    PkConst k{0x64006400u, 0x54005400u};
+    asm volatile("" : "+v"(k.k64), "+v"(k.k54));
+    return k;
+}
+// The group's (s, s) and (-z s, -z s) from its header dword [scale | zero].
+__device__ inline void pk_header(unsigned hd, hf2 &s2, hf2 &c2) {
+    s2 = as_h2(__builtin_amdgcn_perm(hd, hd, 0x01000100u));
+    const hf2 z2 = as_h2(__builtin_amdgcn_perm(hd, hd, 0x03020302u));
+    c2 = -(z2 * s2);
+}
+__device__ inline h8 dequant8_pk(unsigned c, hf2 s2, hf2 c2, PkConst k) {
+    const hf2 m1024 = {static_cast<_Float16>(-1024.f), static_cast<_Float16>(-1024.f)};
+    const hf2 m64 = {static_cast<_Float16>(-64.f), static_cast<_Float16>(-64.f)};
+    const unsigned c8 = c >> 8;
+    const hf2 q0 = as_h2(and_or(c, 0x000F000Fu, k.k64)) + m1024;   // elements 0, 4
+    const hf2 q1 = as_h2(and_or(c, 0x00F000F0u, k.k54)) + m64;     // 1, 5
+    const hf2 q2 = as_h2(and_or(c8, 0x000F000Fu, k.k64)) + m1024;  // 2, 6
+    const hf2 q3 = as_h2(and_or(c8, 0x00F000F0u, k.k54)) + m64;    // 3, 7
+    u4v pk;
+    pk[0] = as_u(__builtin_elementwise_fma(q0, s2, c2));
+    pk[1] = as_u(__builtin_elementwise_fma(q1, s2, c2));
+    pk[2] = as_u(__builtin_elementwise_fma(q2, s2, c2));
+    pk[3] = as_u(__builtin_elementwise_fma(q3, s2, c2));
     return __builtin_bit_cast(h8, pk);
 }
 
@@ -536,12 +593,16 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma2(const uint8_t *__res
 //   The loop is unrolled by S so that every register slot index is a
 //   constant; steps past the last are loaded (never consumed) and not
 //   computed, which keeps every wait one constant s_waitcnt.
-//   Measured per wave on MI355X at 512 tokens (cycle counters around the loop
-//   phases): about a third of the time went to issuing a step's loads (the CU's
-//   memory pipeline takes some 64 bytes a clock, and a step of two workgroups
-//   per CU asks for ~40 KB), half to the dequantization and MFMAs, and the
-//   waits for data and the barrier took under a tenth. Hence 20 bytes of W per
-//   lane (not the whole 36-byte record) and the fp32 dequantization.
+//   The A operands are dequantized with packed fp16 arithmetic (dequant8_pk), which
+//   leaves a code dword's elements in k-slot order (0, 4, 1, 5, 2, 6, 3, 7); X comes
+//   from x_to_f16<true> in the same order, so both operands agree slot for slot.
+//   Y leaves in 16-byte stores (4 rows of a token) where M % 4 == 0 and y is 16-byte
+//   aligned: four times fewer store instructions than one float each, which took
+//   the 512-token call from 48 to 39 us on MI355X (the output is 20 MB there).
+//   Measured on MI355X at 512 tokens with copies of this kernel that skip parts of
+//   the work: without the MFMAs or without the dequantization the time hardly
+//   changes; without the loads of W and X it drops by three quarters. The loop is
+//   bound by the time each workgroup's loads take to arrive, not by arithmetic.
 __device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char *st, const int *xvo, int nx, int xso,
                                         int wave) {
 #pragma unroll
@@ -554,7 +615,7 @@ template <int WN, int S, int NWV>
 __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restrict__ w,
                                                           const _Float16 *__restrict__ xh,
                                                           const float *__restrict__ xinv, float *__restrict__ y, int M,
-                                                          int N, int K, int Kp, int row_bytes) {
+                                                          int N, int K, int Kp, int row_bytes, int vec_y) {
     constexpr int BN = 32 * WN;
     constexpr int BM = 32 * NWV;
     constexpr int XStage = BN * 128;
@@ -575,7 +636,7 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
                                                 static_cast<size_t>(N - n0) * Kp * 2);
     // Lane (row li, half h) takes elements 32 h .. 32 h + 31 of every step: the group header
     // and code bytes 16 h .. 16 h + 15; MFMA k-slot 8 h + p of k-block kk holds element
-    // 32 h + 8 kk + p on the A (W) and the B (X) side.
+    // 32 h + 8 kk + e, p = pk_slot(e), on the A (W) and the B (X) side.
     const int li = lane & 31, h = lane >> 5;
     const int wvo = (32 * wave + li) * row_bytes;
     int xvo[XD];
@@ -594,6 +655,7 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
             xro[kk][j] = 16 * (8 * r + ((4 * h + kk) ^ ((r >> 1) & 7)));
         }
 
+    const PkConst pkc = pk_const();
     unsigned hd[S];
     u4v cd[S];
     auto issue = [&](auto uc, int s) {  // step s into register slot and X stage u = s % S
@@ -610,15 +672,14 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
     auto compute = [&](auto uc, int k0, int k1) {
         constexpr int u = decltype(uc)::value;
         const unsigned char *st = smem + u * XStage;
-        float sc = half_bits_f(hd[u]);
-        float zs = -(half_bits_f(hd[u] >> 16) * sc);
-        opaque_f32(sc, zs);
+        hf2 s2, c2;
+        pk_header(hd[u], s2, c2);
 #pragma unroll
         for (int kk = k0; kk < k1; ++kk) {
             h8 b[WN];
 #pragma unroll
             for (int j = 0; j < WN; ++j) b[j] = *reinterpret_cast<const h8 *>(st + xro[kk][j]);
-            const h8 a = dequant8(cd[u][kk], sc, zs);
+            const h8 a = dequant8_pk(cd[u][kk], s2, c2, pkc);
 #pragma unroll
             for (int j = 0; j < WN; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[j], acc[j], 0, 0, 0);
         }
@@ -671,9 +732,14 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
             const int m = m0 + 32 * wave + 8 * r4 + 4 * h;
+            if (vec_y && m + 3 < M) {
+                *reinterpret_cast<float4 *>(yc + m) = make_float4(acc[j][4 * r4] * sc, acc[j][4 * r4 + 1] * sc,
+                                                                  acc[j][4 * r4 + 2] * sc, acc[j][4 * r4 + 3] * sc);
+            } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (m + q < M) yc[m + q] = acc[j][4 * r4 + q] * sc;
+                for (int q = 0; q < 4; ++q)
+                    if (m + q < M) yc[m + q] = acc[j][4 * r4 + q] * sc;
+            }
         }
     }
 }
@@ -692,7 +758,8 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
 //     [2^13, 2^14), and stored to LDS as fp16, [step][token][64 elements] with the
 //     16-byte chunks of token n at positions c ^ ((n >> 1) & 7): the 16 rows a
 //     ds_read_b128 pass serves cover one 256-byte bank sweep exactly (rows n and n + 8 on
-//     the same chunk, as c ^ (n & 7) had them, share banks).
+//     the same chunk, as c ^ (n & 7) had them, share banks). Within a chunk the 8 elements
+//     are in the k-slot order of the packed-fp16 dequantization (dequant8_pk).
 //   - W: each row's slice (9 dwords a step, contiguous) comes in with one DMA into LDS at
 //     an odd dword pitch. (A load per lane and row touches a cache line per lane; the
 //     DMA touches the 2-3 lines the slice spans.) Wave w then takes rows 32 w .. 32 w + 31:
@@ -786,18 +853,25 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
     if (m > 0.f && m <= 3.0e38f) e = min(14 - __builtin_amdgcn_frexp_expf(m), 126);
     const float sc = ldexpf(1.f, e);
     if (sub == 0) inv_s[n] = ldexpf(1.f, -e);
+    // Within each 8 elements the chunk holds them in the packed dequantization's k-slot order
+    // (0, 4, 1, 5, 2, 6, 3, 7): the even thread of a pair (elements 0..3 of the 8) takes 4, 5
+    // from the odd one and writes slots 0..3; the odd thread takes 2, 3 and writes slots 4..7.
+    const bool odd = sub & 1;
 #pragma unroll
     for (int q = 0; q < 2 * SMAX; ++q) {
         const int c = (sub >> 1) + 4 * (q & 1);  // 16-byte chunk of step q / 2
+        const float a0 = xv[q].x * sc, a1 = xv[q].y * sc, a2 = xv[q].z * sc, a3 = xv[q].w * sc;  // exact scaling
+        const float r0 = dpp_f<kDppXor1>(odd ? a0 : a2), r1 = dpp_f<kDppXor1>(odd ? a1 : a3);
         uint2 pk;
-        pk.x = pair_f16(xv[q].x * sc, xv[q].y * sc);  // exact scaling, one rounding
-        pk.y = pair_f16(xv[q].z * sc, xv[q].w * sc);
+        pk.x = odd ? pair_f16(r0, a2) : pair_f16(a0, r0);  // one rounding each
+        pk.y = odd ? pair_f16(r1, a3) : pair_f16(a1, r1);
         *reinterpret_cast<uint2 *>(xs + 4096 * (q >> 1) + 128 * n + 16 * (c ^ ((n >> 1) & 7)) + 8 * (sub & 1)) = pk;
     }
     lds_barrier();
 
     // 4. the slice's steps: lane (row 32 w + li, half h) takes the header and code dwords
     //    1 + 4 h .. 4 + 4 h of the step's group
+    const PkConst pkc = pk_const();
     f16x acc = {};
     const unsigned *wl = reinterpret_cast<const unsigned *>(ws_lds) + (32 * wave + li) * P;
 #pragma unroll
@@ -807,16 +881,15 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
             unsigned cd[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) cd[kk] = wl[9 * j + 1 + 4 * h + kk];
-            float s = half_bits_f(hd);
-            float zs = -(half_bits_f(hd >> 16) * s);
-            opaque_f32(s, zs);
+            hf2 s2, c2;
+            pk_header(hd, s2, c2);
             h8 b[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
                 b[kk] = *reinterpret_cast<const h8 *>(xs + 4096 * j + 128 * li + 16 * ((4 * h + kk) ^ ((li >> 1) & 7)));
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(dequant8(cd[kk], s, zs), b[kk], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(dequant8_pk(cd[kk], s2, c2, pkc), b[kk], acc, 0, 0, 0);
         }
     }
 
@@ -971,8 +1044,9 @@ int launch_g64(const uint8_t *w, const _Float16 *xh, const float *xinv, float *y
     if (lds > 64 * 1024 && lds > limit) return kTooLarge;
     if (static_cast<size_t>(BM) * rb + static_cast<size_t>(Kp) * 2 * BN >= (1ull << 31)) return kTooLarge;
     const dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
+    const int vec_y = M % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
     hipLaunchKernelGGL((i4_matmul_g64<WN, S, NWV>), grid, dim3(64 * NWV), lds, stream, w, xh, xinv, y, M, N, K, Kp,
-                       rb);
+                       rb, vec_y);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -1053,25 +1127,36 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
     const size_t xh_bytes = (Kp * 2 * N + 255) / 256 * 256;
     _Float16 *xh = reinterpret_cast<_Float16 *>(ws);
     float *xinv = reinterpret_cast<float *>(ws + xh_bytes);
-    if (Kp <= static_cast<size_t>(256 * kXRegs))
-        hipLaunchKernelGGL(x_to_f16, dim3(N), dim3(256), 0, stream, x, K, static_cast<int>(Kp), xh, xinv);
-    else
-        hipLaunchKernelGGL(x_to_f16_long, dim3(N), dim3(256), 0, stream, x, K, static_cast<int>(Kp), xh, xinv);
-    if (hipGetLastError() != hipSuccess) return kLaunchFailed;
     const int ikp = static_cast<int>(Kp), irb = static_cast<int>(rb);
     const int wn = pick_wn(N);
+    // The G = 64 kernel (packed-fp16 dequantization) takes X in its k-slot order; the other
+    // kernels in natural order. Its workgroups address 32 NWV rows and 32 WN token rows of X
+    // with 32-bit offsets.
+    const int g64_bm = wn == 1 ? 32 : 128;
+    const bool g64 = group_size == 64 && static_cast<size_t>(g64_bm) * rb + Kp * 2 * 32 * wn < (1ull << 31);
+    const bool lng = Kp > static_cast<size_t>(256 * kXRegs);
+    if (g64)
+        hipLaunchKernelGGL(lng ? x_to_f16_long<true> : x_to_f16<true>, dim3(N), dim3(256), 0, stream, x, K, ikp, xh,
+                           xinv);
+    else
+        hipLaunchKernelGGL(lng ? x_to_f16_long<false> : x_to_f16<false>, dim3(N), dim3(256), 0, stream, x, K, ikp, xh,
+                           xinv);
+    if (hipGetLastError() != hipSuccess) return kLaunchFailed;
     int st;
-    if (group_size == 64) {
+    if (g64) {
         // one-wave workgroups of 32 rows for a single token block: four times
         // the workgroups (304 at 9728 rows), each with a wave-private X ring
         // Tiles measured on MI355X at 9728x2560 (512 / 128 tokens): 128 x 96 52.9 / 33.0 us,
         // 128 x 64 57.9 / 27.7, 128 x 128 58.7 / 38.9; two or more row blocks per wave
         // (256 x 96, 256 x 64, 128 x 96 over 2 waves, ...) 66-82 / 40-72; and staging W
         // through LDS in 3-step chunks did not beat the loads straight into registers.
-        st = wn == 1   ? launch_g64<1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-             : wn == 2 ? launch_g64<2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-                       : launch_g64<3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
-        if (st != kTooLarge) return st;
+        // (At 512 tokens, 128 x 160 tiles with 1 wave per SIMD, 256 x 128 tiles of 8 waves and
+        // W staged through LDS in 4-step chunks by 16-byte DMAs were no faster either.)
+        return wn == 1   ? launch_g64<1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+               : wn == 2 ? launch_g64<2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
+                         : launch_g64<3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
+    }
+    if (group_size == 64) {
         st = wn == 1   ? launch_tiles2<1, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
              : wn == 2 ? launch_tiles2<2, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
                        : launch_tiles2<3, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream);
