@@ -47,6 +47,20 @@ def test_vq2_device_api_matches_oracle(gpu, orc, M, K):
     assert_close(dy.download(np.float32, M), want, 1e-5, f"vq2 {M}x{K}")
 
 
+@pytest.mark.parametrize("M,K", [(896, 896), (4864, 896), (16384, 2048)])
+def test_vq2_activations_at_any_float_offset(gpu, orc, M, K):
+    """x 4 bytes past a 16-byte boundary: the one-wave-per-row kernel (up to 4M lookups) then
+    loads the activations one float at a time; the replica kernel never needs the alignment."""
+    w = gpu.synth_vq2(M, K, seed=M + 3 * K)
+    x = gpu.synth_normal(K, seed=K + 1)
+    xb = np.zeros(K + 4, np.float32)
+    xb[1:K + 1] = x
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(xb), gpu.DeviceBuffer(4 * M)
+    assert gpu.lib().tqhip_matvec_vq2_dev(dw.ptr, dx.ptr + 4, dy.ptr, M, K, None) == 0
+    gpu.synchronize()
+    assert_close(dy.download(np.float32, M), orc.matvec_vq2(w, x, M, K, threads=8), 1e-5, f"vq2 {M}x{K} x+4")
+
+
 @pytest.mark.parametrize("name", golden_names("mm_i4_"))
 def test_matmul_i4_golden_through_registry(gpu, name):
     f = golden(name)

@@ -14,7 +14,11 @@
 //   byte load per index. A wave owns a tile of kRows rows and sweeps the row in
 //   steps of 64 lanes x 4 indices; each lane keeps the 16 activations of its 4
 //   indices in VGPRs and reuses them for all kRows rows.
-// Both accumulate in fp32.
+// - vq2_matvec_rows (index rows dword-aligned, at most kDirectLookups lookups): one wave per
+//   row and no LDS at all. A grid this small cannot amortise building a 64 KB codebook
+//   replica per workgroup, so every lookup is an 8-byte load of the fp16 entry from the
+//   2 KB codebook in global memory (it stays in each CU's L1 after the first touch).
+// All accumulate in fp32.
 
 #include "tq_common.h"
 
@@ -234,12 +238,61 @@ __global__ __launch_bounds__(64 * kVq2Waves) void vq2_matvec_copies(const uint8_
     }
 }
 
+// ---- One wave per row, codebook entries gathered from global memory (small launches).
+// Lane l takes index dwords l, l + 64, ... of the row (indices 4 b .. 4 b + 3) and their
+// activations; the 64 lane sums are added by a butterfly over the wave. Measured on MI355X
+// against vq2_matvec_copies: 896x896 2.5 vs 5.2 us, 3072x1024 3.3-3.6 vs 5.1-5.3 us (the
+// one-launch floor for its 0.8 MB is 3.3 us), 4864x896 4.1 vs 5.3, 2001x3056 4.7 vs 7.9; from
+// about 8M lookups (16384x2048, 32768x896) the replica kernel is faster.
+constexpr long long kDirectLookups = 4ll << 20;
+template <bool XALIGN>
+__global__ __launch_bounds__(256) void vq2_matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                                       float *__restrict__ y, int M, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int nb = K / kVq2Dim;  // index bytes per row (a multiple of 4)
+    const unsigned *qrow = reinterpret_cast<const unsigned *>(w + kVq2CodebookBytes + static_cast<size_t>(row) * nb);
+    const uint2 *cbg = reinterpret_cast<const uint2 *>(w);  // entry e: 4 fp16 in 8 bytes
+    float a = 0.f;
+    for (int d = lane; 4 * d < nb; d += 64) {
+        const unsigned q = qrow[d];
+        float4 xv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float *xp = x + 16 * d + 4 * j;
+            xv[j] = XALIGN ? *reinterpret_cast<const float4 *>(xp) : make_float4(xp[0], xp[1], xp[2], xp[3]);
+        }
+        uint2 c[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = cbg[(q >> (8 * j)) & 0xFFu];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a = fmaf(half_bits(c[j].x), xv[j].x, a);
+            a = fmaf(half_bits(c[j].x >> 16), xv[j].y, a);
+            a = fmaf(half_bits(c[j].y), xv[j].z, a);
+            a = fmaf(half_bits(c[j].y >> 16), xv[j].w, a);
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
+    if (lane == 0) y[row] = a;
+}
+
 }  // namespace
 
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream) {
     if (out_dim < 1 || in_dim < kVq2Dim || in_dim % kVq2Dim) return kBadShape;
     const int cus = device_cu_count();
-    if ((in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0) {
+    const bool aligned = (in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0;
+    if (aligned && static_cast<long long>(out_dim) * (in_dim / kVq2Dim) <= kDirectLookups) {
+        const dim3 grid((out_dim + 3) / 4);
+        if ((reinterpret_cast<uintptr_t>(x) & 15) == 0)
+            hipLaunchKernelGGL(vq2_matvec_rows<true>, grid, dim3(256), 0, stream, w, x, y, out_dim, in_dim);
+        else
+            hipLaunchKernelGGL(vq2_matvec_rows<false>, grid, dim3(256), 0, stream, w, x, y, out_dim, in_dim);
+        return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+    }
+    if (aligned) {
         // index rows dword-aligned: the conflict-free kernel (16 waves x 4-row
         // tiles measured fastest at 3072..16384 rows, within 4% of the best at
         // 151936 rows)
