@@ -218,6 +218,7 @@ __device__ __forceinline__ void wait_vm(int n) {
         TQ_VMWAIT(8) TQ_VMWAIT(9) TQ_VMWAIT(10) TQ_VMWAIT(11) TQ_VMWAIT(12) TQ_VMWAIT(13) TQ_VMWAIT(14)
         TQ_VMWAIT(15) TQ_VMWAIT(16) TQ_VMWAIT(17) TQ_VMWAIT(18) TQ_VMWAIT(19) TQ_VMWAIT(20) TQ_VMWAIT(21)
         TQ_VMWAIT(22) TQ_VMWAIT(23) TQ_VMWAIT(24) TQ_VMWAIT(25) TQ_VMWAIT(26) TQ_VMWAIT(27) TQ_VMWAIT(28)
+        TQ_VMWAIT(32)
 #undef TQ_VMWAIT
         default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break;
     }
@@ -786,7 +787,7 @@ template <int SMAX>
 __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                                         float *__restrict__ y, int M, int K, int N, int row_bytes,
                                                         int T, int KS, float *__restrict__ part,
-                                                        unsigned long long *__restrict__ arrivals) {
+                                                        unsigned long long *__restrict__ arrivals, int vec_y) {
     __shared__ __align__(16) unsigned char xs[SMAX * 4096];
     __shared__ __align__(16) unsigned char ws_lds[kSkRows * (9 * SMAX + 1) * 4];
     __shared__ float inv_s[32];
@@ -814,6 +815,9 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
         okm |= static_cast<unsigned>(ok) << q;
         xv[q] = xr[ok ? f : 0];
     }
+    // (the X loads stay ahead of the W DMAs in the instruction stream: step 3 counts on it)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
     // 2. W: the slice of each of the tile's 128 rows is 9 ns contiguous dwords; one DMA per row
     //    (wave w: rows 32 w .. 32 w + 31, lane i: dword i) lands it at LDS dword r * P, with
     //    the odd pitch P = 9 ns | 1, so the 32 rows a wave reads in step j (dword r P + 9 j + c)
@@ -823,7 +827,7 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
     if (lane < 9 * ns) {  // only the slice's lanes: a DMA lane writes LDS dword (base + lane), and
                           // lanes past 9 ns would land in the next row's dwords
         const __amdgpu_buffer_rsrc_t wr = rows_rsrc(w, M, row_bytes, m0);
-#pragma unroll 4
+#pragma unroll
         for (int i = 0; i < 32; ++i) {
             const int r = 32 * wave + i;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -832,8 +836,10 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
         }
     }
 
-    // 3. the slice's X to fp16 in LDS, scaled per token
-    wait_vm(0);
+    // 3. the slice's X to fp16 in LDS, scaled per token, while the W rows are in flight: the
+    //    wave's 32 row DMAs were issued after its X loads, so vmcnt(32) is the X loads alone
+    static_assert(kSkRows / 4 == 32, "32 row DMAs per wave");
+    wait_vm(32);
 #pragma unroll
     for (int q = 0; q < 2 * SMAX; ++q) {
         const bool ok = (okm >> q) & 1u;
@@ -867,6 +873,7 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
         pk.y = odd ? pair_f16(r1, a3) : pair_f16(a1, r1);
         *reinterpret_cast<uint2 *>(xs + 4096 * (q >> 1) + 128 * n + 16 * (c ^ ((n >> 1) & 7)) + 8 * (sub & 1)) = pk;
     }
+    wait_vm(0);  // this wave's W rows have landed in LDS
     lds_barrier();
 
     // 4. the slice's steps: lane (row 32 w + li, half h) takes the header and code dwords
@@ -972,12 +979,16 @@ __global__ __launch_bounds__(256) void i4_matmul_skinny(const uint8_t *__restric
     if (li >= N) return;
     float *yc = y + static_cast<size_t>(li) * M;
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4)
+    for (int r4 = 0; r4 < 4; ++r4) {
+        const int m = m0 + 32 * wave + 8 * r4 + 4 * h;
+        if (vec_y && m + 3 < M) {
+            *reinterpret_cast<float4 *>(yc + m) = make_float4(sum[r4][0], sum[r4][1], sum[r4][2], sum[r4][3]);
+        } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int m = m0 + 32 * wave + 8 * r4 + 4 * h + c;
-            if (m < M) yc[m] = sum[r4][c];
+            for (int c = 0; c < 4; ++c)
+                if (m + c < M) yc[m + c] = sum[r4][c];
         }
+    }
 }
 
 // Raises fn's dynamic-LDS limit to what the CU's 160 KB leaves beside its static LDS
@@ -1080,12 +1091,13 @@ SkinnyGeom skinny_geom(int M, int K) {
 int launch_skinny(const uint8_t *w, const float *x, float *y, int M, int K, int N, const SkinnyGeom &g, float *part,
                   unsigned long long *arrivals, hipStream_t stream) {
     const int rb = static_cast<int>(i4_row_bytes(K, 64));
+    const int vec_y = M % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;  // 16-byte Y stores
     const dim3 grid((g.tiles + 7) / 8 * 8 * g.KS), block(256);
     switch (g.smax) {
 #define TQ_SKINNY(S)                                                                                             \
     case S:                                                                                                      \
         hipLaunchKernelGGL(i4_matmul_skinny<S>, grid, block, 0, stream, w, x, y, M, K, N, rb, g.T, g.KS, part, \
-                           arrivals);                                                                            \
+                           arrivals, vec_y);                                                                     \
         break;
         TQ_SKINNY(1) TQ_SKINNY(2) TQ_SKINNY(3) TQ_SKINNY(4) TQ_SKINNY(5) TQ_SKINNY(6) TQ_SKINNY(7)
 #undef TQ_SKINNY
