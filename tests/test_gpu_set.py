@@ -81,12 +81,23 @@ def test_qwen25_layer_set(gpu, orc):
 
 
 def test_qwen35_4b_layer_shapes(gpu, orc):
+    """every long-row matrix has >= 2048 rows, so each wave takes two rows. With a
+    896x4864 matrix added, the set runs one long row per wave; the rows of a matrix get the same
+    bits either way, and the same bits as its single launch."""
     spec = [("qkv_in", 4096, 2560, "attn"), ("o", 2560, 4096, "o"), ("gate", 9728, 2560, "mlp"),
             ("up", 9728, 2560, "mlp"), ("down", 2560, 9728, "down")]
     mats = build(gpu, spec, 64, seed=60)
     got = run_set(gpu, mats, 64)
-    for (name, M, K, w, x, _, _), g in zip(mats, got):
+    alone = singles(gpu, mats, 64)
+    for (name, M, K, w, x, _, _), g, a in zip(mats, got, alone):
         assert_close(g, orc.matvec_i4(w, x[0], M, K, 64, threads=16), name)
+        assert np.array_equal(g, a), f"{name}: set output differs from the single launch"
+    small = build(gpu, [("small_down", 896, 4864, "s")], 64, seed=70)
+    mixed = run_set(gpu, mats + small, 64)
+    for (name, *_), g, m in zip(mats, got, mixed):
+        assert np.array_equal(g, m), f"{name}: two long rows per wave vs one differ"
+    _, M, K, w, x, _, _ = small[0]
+    assert_close(mixed[-1], orc.matvec_i4(w, x[0], M, K, 64, threads=16), "small_down")
 
 
 def test_golden_fixtures_in_one_set(gpu):

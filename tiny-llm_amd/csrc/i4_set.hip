@@ -15,7 +15,8 @@
 //     and one barrier later every wave reads its slices from LDS.
 //   * Rows of up to 32 half-groups (K <= 1024) take one half-wave each (two rows
 //     per half-wave on larger sets), longer rows (K <= 10240) one wave each over
-//     1..5 slots of 64 half-groups; lane u computes half-group u (32 weights: 16
+//     1..5 slots of 64 half-groups (two rows per wave when every long-row matrix
+//     of the launch has >= 2048 rows); lane u computes half-group u (32 weights: 16
 //     code bytes and the group header) with v_dot4 on the code nibbles and the
 //     activation digits, exact before a per-half-group fp32 epilogue.
 // The same kernel serves single-matrix and pair / qkv launches of decode size
@@ -130,12 +131,12 @@ __device__ __forceinline__ float half_group_int(const v4i &cd, unsigned hd, cons
 }
 
 // Rows of at most 32 half-groups (S = 0): R rows per half-wave, 2R per wave, 8R per
-// workgroup. Rows of more: one per wave over S slots, 4 per workgroup.
+// workgroup. Rows of more: R per wave over S slots, kSetWaves R per workgroup.
 template <int S, int R>
 __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char *lds) {
     // 16-byte activation loads per thread: the chunks of the widest row of this shape
     constexpr int NX = ((S == 0 ? 256 : 512 * S) + kSetThreads - 1) / kSetThreads;
-    constexpr int NR = S == 0 ? R : 1;      // rows per lane
+    constexpr int NR = R;                   // rows per lane
     constexpr int NS = S == 0 ? 1 : S;      // half-group slots per lane
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -158,7 +159,7 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
     const int half = S == 0 ? lane >> 5 : 0, u = S == 0 ? lane & 31 : lane;
     // the wave's first row (uniform, so the buffer resource stays in scalar registers); the
     // half-wave's row goes into the per-lane offset
-    const int base = S == 0 ? (blk * kSetWaves + wave) * 2 * R : blk * kSetWaves + wave;
+    const int base = S == 0 ? (blk * kSetWaves + wave) * 2 * R : (blk * kSetWaves + wave) * R;
     const __amdgpu_buffer_rsrc_t wr = rows_rsrc(m.w, m.M, rb, base);  // rows past the matrix read 0
     unsigned hd[NR * NS];
     v4i cd[NR * NS];
@@ -167,7 +168,7 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
 #pragma unroll
         for (int sl = 0; sl < NS; ++sl) {
             const int unit = u + 64 * sl;
-            const int off = (2 * r + half) * rb + (kI4Header + 32) * (unit >> 1);
+            const int off = (S == 0 ? 2 * r + half : r) * rb + (kI4Header + 32) * (unit >> 1);
             hd[r * NS + sl] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
             cd[r * NS + sl] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + kI4Header + 16 * (unit & 1), 0, 0);
         }
@@ -209,15 +210,16 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-        const int row = base + 2 * r + half;
+        const int row = base + (S == 0 ? 2 * r + half : r);
         const float sum = S == 0 ? sum_half_wave(p[r]) : sum_wave(p[r]);
         if (u == 0 && row < m.M) store_y(m.y + row, sum);
     }
 }
 
 // SMAX: the largest shape in the launch (the register budget follows it); R: rows per
-// half-wave for the short rows.
-template <int SMAX, int R>
+// half-wave for the short rows; RL: rows per wave for the long rows (two rows share the
+// activation operands each wave reads from LDS and halve the workgroups that convert x).
+template <int SMAX, int R, int RL>
 __global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int b = blockIdx.x;
@@ -232,15 +234,15 @@ __global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs a) {
     if (m.shape == 0) {
         set_rows<0, R>(m, blk, lds);
     } else if (SMAX <= 1 || m.shape == 1) {
-        set_rows<1, 1>(m, blk, lds);
+        set_rows<1, RL>(m, blk, lds);
     } else if (SMAX <= 2 || m.shape == 2) {
-        set_rows<2, 1>(m, blk, lds);
+        set_rows<2, RL>(m, blk, lds);
     } else if (SMAX <= 3 || m.shape == 3) {
-        set_rows<3, 1>(m, blk, lds);
+        set_rows<3, RL>(m, blk, lds);
     } else if (SMAX <= 4 || m.shape == 4) {
-        set_rows<4, 1>(m, blk, lds);
+        set_rows<4, RL>(m, blk, lds);
     } else {
-        set_rows<5, 1>(m, blk, lds);
+        set_rows<5, RL>(m, blk, lds);
     }
 }
 
@@ -253,16 +255,31 @@ int set_shape(const I4Mat &mt, int group_size) {
     return mt.K <= 1024 ? 0 : (mt.K + 64 * 32 - 1) / (64 * 32);
 }
 
-template <int R>
+template <int R, int RL>
 void launch_r(int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream, const SetArgs &a) {
     switch (smax) {
-        case 0: hipLaunchKernelGGL((i4_matvec_set<0, R>), grid, block, lds, stream, a); break;
-        case 1: hipLaunchKernelGGL((i4_matvec_set<1, R>), grid, block, lds, stream, a); break;
-        case 2: hipLaunchKernelGGL((i4_matvec_set<2, R>), grid, block, lds, stream, a); break;
-        case 3: hipLaunchKernelGGL((i4_matvec_set<3, R>), grid, block, lds, stream, a); break;
-        case 4: hipLaunchKernelGGL((i4_matvec_set<4, R>), grid, block, lds, stream, a); break;
-        default: hipLaunchKernelGGL((i4_matvec_set<5, R>), grid, block, lds, stream, a); break;
+        case 0: hipLaunchKernelGGL((i4_matvec_set<0, R, 1>), grid, block, lds, stream, a); break;
+        case 1: hipLaunchKernelGGL((i4_matvec_set<1, R, RL>), grid, block, lds, stream, a); break;
+        case 2: hipLaunchKernelGGL((i4_matvec_set<2, R, RL>), grid, block, lds, stream, a); break;
+        case 3: hipLaunchKernelGGL((i4_matvec_set<3, R, RL>), grid, block, lds, stream, a); break;
+        case 4: hipLaunchKernelGGL((i4_matvec_set<4, R, RL>), grid, block, lds, stream, a); break;
+        default: hipLaunchKernelGGL((i4_matvec_set<5, R, RL>), grid, block, lds, stream, a); break;
     }
+}
+
+// Two long rows per wave when every long-row matrix of the launch has at least this many rows.
+// Measured on MI355X (cold, one launch): 9728x2560 7.66 -> 7.38 us, 2560x9728 8.60 -> 7.82,
+// 4096x2560 4.72 -> 4.40, 2560x4096 4.81 -> 4.36; the decode layer set, whose only long-row
+// matrix (down, 896x4864) then has half the workgroups, 4.90 -> 5.83 (so it keeps one).
+constexpr int kLongRowPairMinRows = 2048;
+int long_rows_per_wave(const I4Mat *mats, const int *shape, int n) {
+    bool any = false;
+    for (int i = 0; i < n; ++i) {
+        if (shape[i] == 0) continue;
+        if (mats[i].M < kLongRowPairMinRows) return 1;
+        any = true;
+    }
+    return any ? 2 : 1;
 }
 
 int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream) {
@@ -277,12 +294,13 @@ int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream) {
     for (int k = 0; k < n; ++k)
         if (shape[k] == 0) short_rows += mats[k].M;
     const int R = short_rows > 16L * device_cu_count() ? 2 : 1;
+    const int RL = long_rows_per_wave(mats, shape, n);
     int blocks = 0, smax = 0, umax = 0;
     for (int k = 0; k < n; ++k) {
         const I4Mat &mt = mats[order[k]];
         const int s = shape[order[k]];
         a.m[k] = SetMat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, s};
-        const int per = s == 0 ? 2 * R * kSetWaves : kSetWaves;  // rows per workgroup
+        const int per = s == 0 ? 2 * R * kSetWaves : RL * kSetWaves;  // rows per workgroup
         blocks += (mt.M + per - 1) / per;
         smax = std::max(smax, s);
         umax = std::max(umax, 2 * ((mt.K + 63) / 64));
@@ -292,9 +310,9 @@ int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(umax) * (4 * kBlockBytes + 8);  // the widest row's operands
     const dim3 grid(blocks), block(kSetThreads);
     if (R == 2)
-        launch_r<2>(smax, grid, block, lds, stream, a);
+        RL == 2 ? launch_r<2, 2>(smax, grid, block, lds, stream, a) : launch_r<2, 1>(smax, grid, block, lds, stream, a);
     else
-        launch_r<1>(smax, grid, block, lds, stream, a);
+        RL == 2 ? launch_r<1, 2>(smax, grid, block, lds, stream, a) : launch_r<1, 1>(smax, grid, block, lds, stream, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -310,13 +328,15 @@ constexpr int kSetMaxBlocksPerCu = 8;
 int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream_t stream) {
     if (n < 1 || n > kSetMaxMats) return kNotFused;
     int shape[kSetMaxMats];
-    long blocks = 0;
     for (int i = 0; i < n; ++i) {
         shape[i] = set_shape(mats[i], group_size);
         if (shape[i] < 0 || mats[i].M < 1) return kNotFused;
-        blocks += shape[i] == 0 ? (mats[i].M + 4 * kSetWaves - 1) / (4 * kSetWaves)
-                                : (mats[i].M + kSetWaves - 1) / kSetWaves;
     }
+    const int RL = long_rows_per_wave(mats, shape, n);
+    long blocks = 0;
+    for (int i = 0; i < n; ++i)
+        blocks += shape[i] == 0 ? (mats[i].M + 4 * kSetWaves - 1) / (4 * kSetWaves)
+                                : (mats[i].M + RL * kSetWaves - 1) / (RL * kSetWaves);
     if (blocks > static_cast<long>(kSetMaxBlocksPerCu) * device_cu_count()) return kNotFused;
     return launch_set(mats, shape, n, stream);
 }
