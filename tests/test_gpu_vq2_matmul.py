@@ -33,9 +33,9 @@ def test_matmul_vq2_golden_decomposes(gpu):
     assert_close(gpu.matmul_vq2(f["w"], f["x"], M, K, N), f["y"], 1e-5, "matmul_vq2")
 
 
-# aligned index rows (in_dim % 16 == 0): conflict-free kernel with one chunk per
-# row, several, a partial last chunk and many tiles per wave; the rest: the
-# byte-load kernel
+# aligned index rows (in_dim % 16 == 0): one wave per row up to 4M lookups, then the
+# conflict-free replica kernel with one chunk per row, several, a partial last chunk and many
+# tiles per wave (151936x896: the table kernel); the rest: the byte-load kernel
 @pytest.mark.parametrize("M,K", [(3072, 1024), (1, 4), (513, 896), (4864, 896), (100, 52), (77, 1000), (16384, 2048),
                                  (2001, 3056), (151936, 896), (3, 16)])
 def test_vq2_device_api_matches_oracle(gpu, orc, M, K):
@@ -47,7 +47,43 @@ def test_vq2_device_api_matches_oracle(gpu, orc, M, K):
     assert_close(dy.download(np.float32, M), want, 1e-5, f"vq2 {M}x{K}")
 
 
-@pytest.mark.parametrize("M,K", [(896, 896), (4864, 896), (16384, 2048)])
+# at least 256 rows per CU, in_dim % 64 == 0 and <= 1024: the dot-product table kernel.
+# Rows per workgroup not a multiple of a wave's 16-row batch (65869 rows: 258 per workgroup,
+# two batches on some waves), four batches on some waves (200000 rows: 782 per workgroup),
+# more workgroups than CUs (300001 rows: 293 workgroups of up to 1024 rows), a full 64-dword
+# row (1024), rows of 40 dwords (640), 16 (256) and one dword (64).
+@pytest.mark.parametrize("M,K", [(65869, 896), (131072, 1024), (200000, 640), (70001, 64), (300001, 256)])
+def test_vq2_table_kernel_matches_oracle(gpu, orc, M, K):
+    w = gpu.synth_vq2(M, K, seed=M + 7 * K)
+    x = gpu.synth_normal(K, seed=K + 5)
+    want = orc.matvec_vq2(w, x, M, K, threads=8)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
+    gpu.lib().tqhip_memset(dy.ptr, 0xFF, 4 * M)  # every row must be written
+    gpu.matvec_vq2_dev(dw, dx, dy, M, K)
+    assert_close(dy.download(np.float32, M), want, 1e-5, f"vq2 {M}x{K}")
+
+
+@pytest.mark.parametrize("M,K", [(3072, 1024), (32768, 896), (151936, 896), (2001, 3052)])
+def test_vq2_non_finite_codebook_entry(gpu, orc, M, K):
+    """Codebook entry 0 set to +inf: a row is non-finite exactly where the oracle's is (the rows
+    that use entry 0), so positions past the row end (padding lanes, table columns) contribute
+    exactly 0 whatever the entries hold. One shape per kernel, each with a padded last chunk:
+    one wave per row, replica (224-byte rows), table, byte loads (in_dim % 16 != 0)."""
+    w = gpu.synth_vq2(M, K, seed=M + 11 * K)
+    w[0:8] = np.frombuffer(np.full(4, np.inf, np.float16).tobytes(), np.uint8)
+    x = gpu.synth_normal(K, seed=K + 9)
+    want = orc.matvec_vq2(w, x, M, K, threads=8)
+    dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M)
+    gpu.matvec_vq2_dev(dw, dx, dy, M, K)
+    got = dy.download(np.float32, M)
+    fin = np.isfinite(want)
+    assert 0 < np.count_nonzero(~fin) < M, "the case needs rows with and without entry 0"
+    assert np.array_equal(np.isfinite(got), fin), f"{np.count_nonzero(np.isfinite(got) != fin)} rows differ in finiteness"
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert_close(got[fin], want[fin], 1e-5, f"vq2 {M}x{K} finite rows")
+
+
+@pytest.mark.parametrize("M,K", [(896, 896), (4864, 896), (16384, 2048), (65869, 896)])
 def test_vq2_activations_at_any_float_offset(gpu, orc, M, K):
     """x 4 bytes past a 16-byte boundary: the one-wave-per-row kernel (up to 4M lookups) then
     loads the activations one float at a time; the replica kernel never needs the alignment."""

@@ -4,7 +4,11 @@
 // reference's matvec_vq2_ref (kernels/matvec/matvec_vq2_ref.cpp:52-81), on the
 // layout [codebook 256 x 4 fp16 = 2048 B][out_dim x in_dim/4 uint8 indices].
 //
-// Two kernels:
+// Four kernels:
+// - vq2_matvec_table (index rows 16-byte aligned, in_dim <= 1024, at least 256 rows per CU):
+//   per workgroup a table of every codebook entry's dot product with every 4-element block of
+//   x, built with fp32 MFMAs in LDS; a lookup is then one 4-byte LDS read and one add (see its
+//   comment).
 // - vq2_matvec_copies (index rows dword-aligned, in_dim % 16 == 0): 16 bank-
 //   interleaved fp32 copies of the codebook in LDS make every lookup
 //   conflict-free; tiles of 4 rows per wave, the next tile's index dwords in
@@ -79,11 +83,13 @@ __global__ __launch_bounds__(256) void vq2_matvec_kernel(const uint8_t *__restri
                 float a = acc[r];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float4 c = cb[(q >> (8 * j)) & 0xFFu];
-                    a = fmaf(c.x, xv[j].x, a);
-                    a = fmaf(c.y, xv[j].y, a);
-                    a = fmaf(c.z, xv[j].z, a);
-                    a = fmaf(c.w, xv[j].w, a);
+                    if (b + j < nb) {  // past the row end: nothing (entry 0 may be non-finite)
+                        const float4 c = cb[(q >> (8 * j)) & 0xFFu];
+                        a = fmaf(c.x, xv[j].x, a);
+                        a = fmaf(c.y, xv[j].y, a);
+                        a = fmaf(c.z, xv[j].z, a);
+                        a = fmaf(c.w, xv[j].w, a);
+                    }
                 }
                 acc[r] = a;
             }
@@ -180,18 +186,22 @@ __global__ __launch_bounds__(64 * kVq2Waves) void vq2_matvec_copies(const uint8_
     auto step = [&](int s, const unsigned (&q)[R]) {
         const int t = s / nchunk, ch = s - t * nchunk;
         if constexpr (!ONE_CHUNK) xvals(ch, xv);  // (with one chunk, loaded once before the loop)
+        // a lane past the row end adds nothing: its index 0 and zero activations would still
+        // give NaN for a non-finite entry 0, which the row never uses
+        if (256 * ch + 4 * lane < nb) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float a = acc[r];
+            for (int r = 0; r < R; ++r) {
+                float a = acc[r];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 c = cbl[kCopies * ((q[r] >> (8 * j)) & 0xFFu)];
-                a = fmaf(c.x, xv[j].x, a);
-                a = fmaf(c.y, xv[j].y, a);
-                a = fmaf(c.z, xv[j].z, a);
-                a = fmaf(c.w, xv[j].w, a);
+                for (int j = 0; j < 4; ++j) {
+                    const float4 c = cbl[kCopies * ((q[r] >> (8 * j)) & 0xFFu)];
+                    a = fmaf(c.x, xv[j].x, a);
+                    a = fmaf(c.y, xv[j].y, a);
+                    a = fmaf(c.z, xv[j].z, a);
+                    a = fmaf(c.w, xv[j].w, a);
+                }
+                acc[r] = a;
             }
-            acc[r] = a;
         }
         if (ch + 1 < nchunk) return;
         // halving exchanges: after the exchange over lane bit `bit`, half the
@@ -278,6 +288,196 @@ __global__ __launch_bounds__(256) void vq2_matvec_rows(const uint8_t *__restrict
     if (lane == 0) y[row] = a;
 }
 
+// ---- Dot-product table (large launches, index rows 16-byte aligned, in_dim <= 1024).
+// A lookup of the replica kernel costs four fp32 FMAs and a 16-byte LDS read per index, which
+// bounds it by VALU and LDS issue (151936x896: 16 us). Here the products are formed once per
+// workgroup: T[c][b] = codebook[c] . x[4 b .. 4 b + 3] for every entry c and index position b of
+// the row, and a lookup is one 4-byte LDS read and one add. The whole table (256 x in_dim / 4
+// fp32) does not fit in LDS at in_dim 896, so the row's index dwords d are taken in two passes,
+// d mod 4 in {0, 1}, then {2, 3}, each with a 128 KB table of two 64 KB sub-tables:
+//   pass p, sub-table s (d mod 4 = 2 p + s): entry (c, byte j, q = d / 4) at byte
+//   s * 65536 + 256 c + 64 j + 4 q holds T[c][4 d + j], and 0 past the row end.
+// Lane (rho = lane / 16, q = lane % 16) loads 16 bytes, dwords 4 q .. 4 q + 3, of rows
+// 16 (wave + 16 i) + 4 r + rho (r = 0..3): a load instruction moves 4 x 256 contiguous bytes.
+// In pass p the lane looks up bytes of dwords 4 q + 2 p and 4 q + 2 p + 1; at step k it takes
+// byte jl = (k + rho) & 3, so the 32 lanes of an LDS pass read banks (16 jl + q) mod 32, all
+// different. One v_perm forms the address from the index byte, the lane's 64 jl + 4 q and
+// the sub-table number.
+// The table is built with v_mfma_f32_32x32x2_f32 (codebook entries x positions, the four
+// components as two k-steps); a 32-position tile is two bytes j x 16 q, so its LDS stores
+// are conflict-free as well. Every index load of the workgroup is issued up front, after the
+// codebook and x loads and before anything waits for them (a conversion there would make the
+// index stream wait for a round trip), so the first table is built while the indices stream
+// in. Measured on MI355X (cold weights, 256 workgroups): 151936x896 12.3-12.5 us (replica
+// kernel 16.1), 131072x1024 12.1 (14.6), 65536x896 8.4 (8.8). Per workgroup (timestamps): the
+// first table waits ~4 us for the cold 2 KB codebook, each lookup pass takes ~1.3 us (LDS
+// issue), the second table ~0.9 us.
+constexpr int kTabWaves = 16;           // waves per workgroup
+constexpr int kTabBatchRows = 16;       // rows of a wave's batch (4 per load instruction x 4)
+constexpr int kTabMaxBatches = 4;       // batches per wave held in VGPRs: <= 1024 rows per workgroup
+constexpr int kTabMinRowsPerCu = 256;   // fewer rows: the replica kernel (65536 rows at 256 CUs)
+constexpr int kTabMaxDim = 1024;        // 64 index dwords per row: 16 lanes x 16 bytes
+
+template <int CTRL>
+__device__ inline float tab_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int BMAX>
+__global__ __launch_bounds__(64 * kTabWaves) void vq2_matvec_table(const uint8_t *__restrict__ w,
+                                                                   const float *__restrict__ x,
+                                                                   float *__restrict__ y, int M, int K,
+                                                                   int rows_per_wg) {
+    __shared__ __align__(16) unsigned char tab[2 * 65536];
+    typedef float f16v __attribute__((ext_vector_type(16)));
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nb = K / kVq2Dim, nd = nb / 4;  // index bytes and dwords per row
+    const int r0 = blockIdx.x * rows_per_wg;
+    const int nrows = min(rows_per_wg, M - r0);
+    if (nrows <= 0) return;
+    const uint16_t *cbh = reinterpret_cast<const uint16_t *>(w);
+    const int rho = lane >> 4, q = lane & 15;
+    const int nbatch = (nrows + kTabBatchRows - 1) / kTabBatchRows;
+    const int mynb = wave < nbatch ? (nbatch - 1 - wave) / kTabWaves + 1 : 0;  // this wave's batches (<= BMAX)
+
+    // 1. table operands, raw: tile t = 2 wave + tt covers entries 32 (t & 7) + 0..31 and
+    //    positions of sub-table (t >> 4), bytes 2 ((t >> 3) & 1) + 0..1; MFMA column n = lane % 32
+    //    is byte 2 ((t >> 3) & 1) + n / 16 of dword 4 (n % 16) + 2 p + sub-table
+    uint16_t cbr[2][2];
+    float xr[2][2][2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int t = 2 * wave + tt, c0 = 32 * (t & 7), ts = t >> 3;
+        const int j = 2 * (ts & 1) + ((lane >> 4) & 1), qn = lane & 15;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+            const int e = 2 * k2 + (lane >> 5);
+            cbr[tt][k2] = cbh[kVq2Dim * (c0 + (lane & 31)) + e];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int b = 4 * (4 * qn + 2 * p + (ts >> 1)) + j;
+                xr[p][tt][k2] = x[b < nb ? kVq2Dim * b + e : 0];
+            }
+        }
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. every index load of this wave's rows (out-of-range offsets read 0 and fetch nothing)
+    const uint8_t *idx = w + kVq2CodebookBytes + static_cast<size_t>(r0) * nb;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(idx), static_cast<short>(0),
+                                                                        nrows * nb, kBufferFlags);
+    uint4 q4[BMAX][4];
+    {
+        const bool qok = 4 * q < nd;
+#pragma unroll
+        for (int i = 0; i < BMAX; ++i) {
+            const int row0 = kTabBatchRows * (wave + kTabWaves * i) + rho;
+            const bool ok = i < mynb && qok;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                q4[i][r] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? (row0 + 4 * r) * nb + 16 * q : 0xFFFFFFF0u, 0, 0));
+        }
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+
+    float av[2][2], bv[2][2][2];
+    bool pad[2][2];  // the tile column lies past the row end: its entries are stored as 0
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int ts = (2 * wave + tt) >> 3;
+        const int j = 2 * (ts & 1) + ((lane >> 4) & 1), qn = lane & 15;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) pad[p][tt] = 4 * (4 * qn + 2 * p + (ts >> 1)) + j >= nb;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+            av[tt][k2] = half_bits(cbr[tt][k2]);
+#pragma unroll
+            for (int p = 0; p < 2; ++p) bv[p][tt][k2] = pad[p][tt] ? 0.f : xr[p][tt][k2];
+        }
+    }
+    unsigned loff[2][4], sel[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const unsigned jl = (k + rho) & 3;
+        loff[0][k] = 64u * jl + 4u * q;
+        loff[1][k] = loff[0][k] | 0x10000u;
+        sel[k] = 0x0C020000u | ((4u + jl) << 8);  // bytes: loff.0, index byte jl, loff.2, zero
+    }
+    auto build = [&](int p) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = 2 * wave + tt, c0 = 32 * (t & 7), ts = t >> 3;
+            f16v d = {};
+            d = __builtin_amdgcn_mfma_f32_32x32x2f32(av[tt][0], bv[p][tt][0], d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_32x32x2f32(av[tt][1], bv[p][tt][1], d, 0, 0, 0);
+            const unsigned base = ((ts >> 1) << 16) + 64 * (2 * (ts & 1) + ((lane >> 4) & 1)) + 4 * (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {  // D row 8 (r / 4) + 4 (lane / 32) + r % 4 = entry offset
+                const int c = c0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                *reinterpret_cast<float *>(tab + base + 256 * c) = pad[p][tt] ? 0.f : d[r];
+            }
+        }
+    };
+
+    float acc[BMAX][4];
+#pragma unroll
+    for (int i = 0; i < BMAX; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][r] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        if (p) __syncthreads();  // every lookup of the first pass is done
+        build(p);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < BMAX; ++i) {
+            if (i < mynb) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float s = acc[i][r];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const unsigned dw = p == 0 ? (h ? q4[i][r].y : q4[i][r].x) : (h ? q4[i][r].w : q4[i][r].z);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            s += *reinterpret_cast<const float *>(tab + __builtin_amdgcn_perm(dw, loff[h][k], sel[k]));
+                    }
+                    acc[i][r] = s;
+                }
+            }
+        }
+    }
+
+    // 3. per batch: the 4 row sums of each lane added over its 16 lanes by halving exchanges
+    //    (row_mirror, row_half_mirror, then quad swaps); lanes 4 m + 0 of each 16 keep row
+    //    4 m + rho's total
+#pragma unroll
+    for (int i = 0; i < BMAX; ++i) {
+        if (i < mynb) {
+            float v0 = acc[i][0], v1 = acc[i][1], v2 = acc[i][2], v3 = acc[i][3];
+            const bool u8 = lane & 8, u4 = lane & 4;
+            {
+                const float lo0 = v0 + tab_dpp<0x140>(v0), hi0 = v2 + tab_dpp<0x140>(v2);
+                const float lo1 = v1 + tab_dpp<0x140>(v1), hi1 = v3 + tab_dpp<0x140>(v3);
+                v0 = u8 ? hi0 : lo0;
+                v1 = u8 ? hi1 : lo1;
+            }
+            {
+                const float lo = v0 + tab_dpp<0x141>(v0), hi = v1 + tab_dpp<0x141>(v1);
+                v0 = u4 ? hi : lo;
+            }
+            v0 += tab_dpp<0x4E>(v0);
+            v0 += tab_dpp<0xB1>(v0);
+            const int row = kTabBatchRows * (wave + kTabWaves * i) + 4 * ((lane >> 2) & 3) + rho;
+            if ((lane & 3) == 0 && row < nrows) y[r0 + row] = v0;
+        }
+    }
+}
+
 }  // namespace
 
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream) {
@@ -290,6 +490,23 @@ int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, i
             hipLaunchKernelGGL(vq2_matvec_rows<true>, grid, dim3(256), 0, stream, w, x, y, out_dim, in_dim);
         else
             hipLaunchKernelGGL(vq2_matvec_rows<false>, grid, dim3(256), 0, stream, w, x, y, out_dim, in_dim);
+        return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+    }
+    if (in_dim % 64 == 0 && in_dim <= kTabMaxDim && (reinterpret_cast<uintptr_t>(w) % 16) == 0 &&
+        static_cast<long long>(out_dim) >= static_cast<long long>(kTabMinRowsPerCu) * cus) {
+        // index rows 16-byte aligned and large: the dot-product table, one workgroup per CU (at
+        // most 1024 rows each, more workgroups beyond 1024 rows per CU)
+        constexpr int kMaxRows = kTabWaves * kTabBatchRows * kTabMaxBatches;
+        const int grid = std::max(cus, (out_dim + kMaxRows - 1) / kMaxRows);
+        const int rpw = (out_dim + grid - 1) / grid;
+        const int batches = ((rpw + kTabBatchRows - 1) / kTabBatchRows + kTabWaves - 1) / kTabWaves;
+        switch (batches) {
+            case 1: hipLaunchKernelGGL(vq2_matvec_table<1>, dim3(grid), dim3(64 * kTabWaves), 0, stream, w, x, y, out_dim, in_dim, rpw); break;
+            case 2: hipLaunchKernelGGL(vq2_matvec_table<2>, dim3(grid), dim3(64 * kTabWaves), 0, stream, w, x, y, out_dim, in_dim, rpw); break;
+            case 3: hipLaunchKernelGGL(vq2_matvec_table<3>, dim3(grid), dim3(64 * kTabWaves), 0, stream, w, x, y, out_dim, in_dim, rpw); break;
+            case 4: hipLaunchKernelGGL(vq2_matvec_table<4>, dim3(grid), dim3(64 * kTabWaves), 0, stream, w, x, y, out_dim, in_dim, rpw); break;
+            default: return kBadShape;  // unreachable: rpw <= kMaxRows
+        }
         return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
     }
     if (aligned) {
