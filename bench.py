@@ -278,11 +278,12 @@ def ceilings(tq, stream):
         for blocks in (2048, 4096, 8192):
             ms = timed(lambda: lib.tqceil_stream_read(buf.ptr, nb, out.ptr, blocks, variant, sp))
             read[f"{names[variant]}, {blocks} wg"] = nb / (ms * 1e-3) / 1e9
-    # cold reads of one matrix's size (the configs[2] and VQ2 shapes), one launch each at offsets
-    # rotating through the 1 GiB buffer, back to back: the floor a single matvec launch of that
-    # many bytes can reach here (launch cost and the ramp to full bandwidth included)
+    # cold reads of one matrix's size (configs[0], the layer set, the configs[2] and VQ2 shapes, the
+    # i4 lm_head 151936x896), one launch each at offsets rotating through the 1 GiB buffer, back to
+    # back: the floor a single matvec launch of that many bytes can reach here (launch cost and the
+    # ramp to full bandwidth included)
     sized = {}
-    for size in (804864, 5924864, 14057472, 34647040):
+    for size in (804864, 2474496, 5924864, 8478208, 14057472, 34647040, 77187072):
         step = (size + 4095) // 4096 * 4096
         offs = [(i * step) % (nb - step) for i in range(60)]
         best_s = None
@@ -383,6 +384,31 @@ def prefill(tq, stream, reps=30):
 CONFIGS2 = ((9728, 2560, "gate/up"), (2560, 9728, "down"), (4096, 2560, "attn in"), (2560, 4096, "attn out"))
 
 
+def cold_matvec(tq, stream, M, K, tag):
+    """One i4 matvec M x K G64 per launch, device-resident, rotated over enough weight copies to
+    exceed 2x the 256 MB MALL (cold reads); median of 7 batches of at least 60 launches."""
+    w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -4, f"{tag}_{M}x{K}"))
+    x = tq.synth_normal(K, seed=tq.synth_seed(0, -4, f"{tag}x_{K}"))
+    b = algo_bytes(M, K)
+    ncopy = (512 << 20) // (M * ((K + G - 1) // G) * (4 + G // 2)) + 1
+    copies = [tq.DeviceBuffer.from_array(w) for _ in range(ncopy)]
+    dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
+    ops = [tq.Op(tq.OP_I4_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, G) for c in copies]
+    ms = time_ops(tq, ops, max(1, 60 // ncopy), 1, stream, batches=7) / len(ops)
+    for c in copies:
+        c.free()
+    dx.free()
+    dy.free()
+    return {"shape": f"{M}x{K}", "us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+            "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b, "copies": ncopy}
+
+
+def configs0(tq, stream):
+    """the single i4 matvec 4864x896 (the reference's CPU-runnable case) on
+    the GPU, one launch, cold. Launch-bound: compare with the one-launch floor for its bytes."""
+    return cold_matvec(tq, stream, 4864, HIDDEN, "c0")
+
+
 def configs2(tq, stream):
     """BASELINE configs[2] (Qwen3.5-4B scale) matvecs other than the lm_head:
     gate/up 9728x2560, down 2560x9728, attention 4096x2560 and 2560x4096, each
@@ -390,21 +416,8 @@ def configs2(tq, stream):
     median of 7 batches of at least 60 launches."""
     rows = []
     for M, K, role in CONFIGS2:
-        w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -4, f"c2_{M}x{K}"))
-        x = tq.synth_normal(K, seed=tq.synth_seed(0, -4, f"c2x_{K}"))
-        b = algo_bytes(M, K)
-        ncopy = (512 << 20) // (M * ((K + G - 1) // G) * (4 + G // 2)) + 1
-        copies = [tq.DeviceBuffer.from_array(w) for _ in range(ncopy)]
-        dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
-        ops = [tq.Op(tq.OP_I4_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, G) for c in copies]
-        ms = time_ops(tq, ops, max(1, 60 // ncopy), 1, stream, batches=7) / len(ops)
-        rows.append({"shape": f"{M}x{K}", "role": role, "us": round(ms * 1e3, 2),
-                     "gbs": round(b / (ms * 1e-3) / 1e9, 1), "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
-                     "bytes": b, "copies": ncopy})
-        for c in copies:
-            c.free()
-        dx.free()
-        dy.free()
+        r = cold_matvec(tq, stream, M, K, "c2")
+        rows.append({"shape": r["shape"], "role": role, **{k: v for k, v in r.items() if k != "shape"}})
     return rows
 
 
@@ -586,9 +599,10 @@ def main():
     ap.add_argument("--no-vq2", action="store_true", help="skip the VQ2 matvec timings")
     ap.add_argument("--no-engine", action="store_true", help="skip the device-resident decode engine timing")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of the step")
-    ap.add_argument("--no-configs2", action="store_true", help="skip the configs[2] gate/up, down and attention matvecs")
+    ap.add_argument("--no-configs2", action="store_true",
+                    help="skip the configs[0] matvec and the configs[2] gate/up, down and attention matvecs")
     ap.add_argument("--no-ceilings", action="store_true", help="skip the stream-read / launch / MFMA ceilings")
-    ap.add_argument("--only", choices=("prefill", "vq2", "headline", "configs2", "ceilings", "engine"),
+    ap.add_argument("--only", choices=("prefill", "vq2", "headline", "configs0", "configs2", "ceilings", "engine"),
                     help="run just this section and print its JSON (for profiler runs; not the contract line)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="first run one device-to-device copy of MB MiB (a known-size kernel for counter runs)")
@@ -618,7 +632,8 @@ def main():
         if args.only == "engine":
             print(json.dumps({"engine": engine(tq, args.steps, args.warmup)}), flush=True)
             return
-        fn = {"prefill": prefill, "vq2": vq2, "headline": headline, "configs2": configs2, "ceilings": ceilings}[args.only]
+        fn = {"prefill": prefill, "vq2": vq2, "headline": headline, "configs2": configs2, "ceilings": ceilings,
+              "configs0": configs0}[args.only]
         print(json.dumps({args.only: fn(tq, stream)}), flush=True)
         return
     work = Workload(tq)
@@ -653,6 +668,9 @@ def main():
     head = None if args.no_headline else headline(tq, stream)
     if head:
         log(f"[bench] headline 151936x2560: {head['us']} us, {head['gbs']} GB/s ({100 * head['frac']:.1f}% of 8 TB/s)")
+    c0 = None if args.no_configs2 else configs0(tq, stream)
+    if c0:
+        log(f"[bench] configs[0] matvec {c0['shape']}: {c0['us']} us, {c0['gbs']} GB/s (one cold launch)")
     c2 = None if args.no_configs2 else configs2(tq, stream)
     if c2:
         log("[bench] configs[2] matvecs: " + ", ".join(f"{r['shape']} {r['us']} us {r['gbs']} GB/s" for r in c2))
@@ -700,6 +718,7 @@ def main():
         "roofline": roof,
         "ceilings": ceil,
         "headline": head,
+        "configs0": c0,
         "configs2": c2,
         "prefill": pre,
         "vq2": v,
