@@ -123,6 +123,29 @@ def test_matmul_i4_device_api_matches_oracle(gpu, orc, M, K, N, G):
         assert_close(got, want, 2e-3, f"matmul {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("M,K,N", [(512, 2560, 64), (300, 1000, 40)])
+def test_matmul_i4_x_conversion_paths_same_bits(gpu, orc, M, K, N):
+    """X 16-byte aligned (16-byte loads and stores in the fp16 conversion) and X 4 bytes past an
+    alignment (one float per load): the same fp16 X, so the same output bits (above 32 tokens
+    both go through the MFMA GEMM)."""
+    w = gpu.synth_i4(M, K, 64, seed=M + K + N)
+    x = gpu.synth_normal(K * N, seed=N + 3)
+    x[5 * K:6 * K] *= 1e-20  # a token far below the others: its own exponent
+    dw, dy_a, dy_u = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer(4 * M * N), gpu.DeviceBuffer(4 * M * N)
+    xb = np.zeros(K * N + 8, np.float32)
+    xb[4:4 + K * N] = x  # 16-byte aligned copy at float 4
+    xb_u = np.zeros(K * N + 8, np.float32)
+    xb_u[1:1 + K * N] = x  # misaligned copy at float 1
+    da, du = gpu.DeviceBuffer.from_array(xb), gpu.DeviceBuffer.from_array(xb_u)
+    lib = gpu.lib()
+    assert lib.tqhip_matmul_i4_dev(dw.ptr, da.ptr + 16, dy_a.ptr, M, K, N, 64, None) == 0
+    assert lib.tqhip_matmul_i4_dev(dw.ptr, du.ptr + 4, dy_u.ptr, M, K, N, 64, None) == 0
+    gpu.synchronize()
+    ya, yu = dy_a.download(np.float32, M * N), dy_u.download(np.float32, M * N)
+    assert np.array_equal(ya.view(np.uint32), yu.view(np.uint32))
+    assert_close(ya, orc.matmul_i4(w, x, M, K, N, 64, threads=16), 2e-3, f"matmul {M}x{K}x{N}")
+
+
 def test_matmul_i4_per_token_scale_extremes(gpu, orc):
     """Token columns of very different magnitude (1e30, 1e-30, 0, N(0,1)) each
     keep the bar on their own: the fp16 staging scales every column by its own

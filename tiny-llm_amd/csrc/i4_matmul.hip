@@ -98,6 +98,58 @@ __global__ __launch_bounds__(256) void x_to_f16(const float *__restrict__ x, int
     if (threadIdx.x == 0) xinv[n] = ldexpf(1.f, -e);
 }
 
+// x_to_f16 for K % 4 == 0 and x 16-byte aligned: thread t takes 8-element chunks t and t + 256
+// (two 16-byte loads each) and stores each chunk's 8 fp16 values, in the chunk's slot order,
+// with one 16-byte store. The same exponent and the same per-element rounding as x_to_f16.
+template <bool PERM>
+__global__ __launch_bounds__(256) void x_to_f16_vec(const float *__restrict__ x, int K, int Kp,
+                                                      _Float16 *__restrict__ xh, float *__restrict__ xinv) {
+    constexpr int kChunks = kXRegs / 8;  // 8-element chunks per thread (Kp <= 256 * kXRegs)
+    const int n = blockIdx.x;
+    const float4 *xc = reinterpret_cast<const float4 *>(x + static_cast<size_t>(n) * K);
+    float v[kChunks][8];
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        const int c = threadIdx.x + 256 * i;  // elements 8c .. 8c + 7
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool ok = 8 * c + 4 * h < K;  // K % 4 == 0: a float4 is all in or all out
+            const float4 q = ok ? xc[2 * c + h] : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[i][4 * h] = q.x;
+            v[i][4 * h + 1] = q.y;
+            v[i][4 * h + 2] = q.z;
+            v[i][4 * h + 3] = q.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[i][e]));
+    }
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __shared__ float wm[4];
+    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+    int e = 0;
+    if (m > 0.f && m <= 3.0e38f) {  // finite, nonzero: max * 2^e in [2^14, 2^15)
+        int E;
+        frexpf(m, &E);
+        e = min(max(15 - E, -120), 120);
+    }
+    uint4 *hc = reinterpret_cast<uint4 *>(xh + static_cast<size_t>(n) * Kp);
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        if (8 * c >= Kp) continue;
+        unsigned short o[8];
+#pragma unroll
+        for (int el = 0; el < 8; ++el)
+            o[x_pos(el, PERM)] = __builtin_bit_cast(unsigned short, static_cast<_Float16>(ldexpf(v[i][el], e)));
+        hc[c] = make_uint4(o[0] | (static_cast<unsigned>(o[1]) << 16), o[2] | (static_cast<unsigned>(o[3]) << 16),
+                           o[4] | (static_cast<unsigned>(o[5]) << 16), o[6] | (static_cast<unsigned>(o[7]) << 16));
+    }
+    if (threadIdx.x == 0) xinv[n] = ldexpf(1.f, -e);
+}
+
 template <bool PERM>
 __global__ __launch_bounds__(256) void x_to_f16_long(const float *__restrict__ x, int K, int Kp,
                                                        _Float16 *__restrict__ xh, float *__restrict__ xinv) {
@@ -1147,12 +1199,13 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
     const int g64_bm = wn == 1 ? 32 : 128;
     const bool g64 = group_size == 64 && static_cast<size_t>(g64_bm) * rb + Kp * 2 * 32 * wn < (1ull << 31);
     const bool lng = Kp > static_cast<size_t>(256 * kXRegs);
+    const bool vec = !lng && K % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;  // 16-byte loads
     if (g64)
-        hipLaunchKernelGGL(lng ? x_to_f16_long<true> : x_to_f16<true>, dim3(N), dim3(256), 0, stream, x, K, ikp, xh,
-                           xinv);
+        hipLaunchKernelGGL(lng ? x_to_f16_long<true> : vec ? x_to_f16_vec<true> : x_to_f16<true>, dim3(N), dim3(256), 0,
+                           stream, x, K, ikp, xh, xinv);
     else
-        hipLaunchKernelGGL(lng ? x_to_f16_long<false> : x_to_f16<false>, dim3(N), dim3(256), 0, stream, x, K, ikp, xh,
-                           xinv);
+        hipLaunchKernelGGL(lng ? x_to_f16_long<false> : vec ? x_to_f16_vec<false> : x_to_f16<false>, dim3(N), dim3(256),
+                           0, stream, x, K, ikp, xh, xinv);
     if (hipGetLastError() != hipSuccess) return kLaunchFailed;
     int st;
     if (g64) {
