@@ -305,13 +305,12 @@ __global__ __launch_bounds__(256) void vq2_matvec_rows(const uint8_t *__restrict
 // the sub-table number.
 // The table is built with v_mfma_f32_32x32x2_f32 (codebook entries x positions, the four
 // components as two k-steps); a 32-position tile is two bytes j x 16 q, so its LDS stores
-// are conflict-free as well. Every index load of the workgroup is issued up front, after the
-// codebook and x loads and before anything waits for them (a conversion there would make the
-// index stream wait for a round trip), so the first table is built while the indices stream
-// in. Measured on MI355X (cold weights, 256 workgroups): 151936x896 12.3-12.5 us (replica
-// kernel 16.1), 131072x1024 12.1 (14.6), 65536x896 8.4 (8.8). Per workgroup (timestamps): the
-// first table waits ~4 us for the cold 2 KB codebook, each lookup pass takes ~1.3 us (LDS
-// issue), the second table ~0.9 us.
+// are conflict-free as well. The first batch's index loads go out right after the codebook and
+// x loads and before anything waits for them (a conversion there would make the index stream
+// wait for a round trip); the other batches follow once the first table is built (see step 3
+// in the kernel). Measured on MI355X (cold weights, 256 workgroups): 151936x896 11.6-11.8 us
+// (replica kernel 15.6), 131072x1024 11.3 (13.5), 65536x896 8.5 (8.8). Per workgroup, each
+// lookup pass takes ~1.3 us (LDS issue) and the second table ~0.9 us.
 constexpr int kTabWaves = 16;           // waves per workgroup
 constexpr int kTabBatchRows = 16;       // rows of a wave's batch (4 per load instruction x 4)
 constexpr int kTabMaxBatches = 4;       // batches per wave held in VGPRs: <= 1024 rows per workgroup
@@ -364,23 +363,22 @@ __global__ __launch_bounds__(64 * kTabWaves) void vq2_matvec_table(const uint8_t
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. every index load of this wave's rows (out-of-range offsets read 0 and fetch nothing)
+    // 2. the index loads of this wave's first batch (out-of-range offsets read 0 and fetch
+    //    nothing); the other batches follow once the first table is built (step 3)
     const uint8_t *idx = w + kVq2CodebookBytes + static_cast<size_t>(r0) * nb;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(idx), static_cast<short>(0),
                                                                         nrows * nb, kBufferFlags);
     uint4 q4[BMAX][4];
-    {
-        const bool qok = 4 * q < nd;
+    const bool qok = 4 * q < nd;
+    auto issue = [&](int i) {
+        const int row0 = kTabBatchRows * (wave + kTabWaves * i) + rho;
+        const bool ok = i < mynb && qok;
 #pragma unroll
-        for (int i = 0; i < BMAX; ++i) {
-            const int row0 = kTabBatchRows * (wave + kTabWaves * i) + rho;
-            const bool ok = i < mynb && qok;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                q4[i][r] = __builtin_bit_cast(
-                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? (row0 + 4 * r) * nb + 16 * q : 0xFFFFFFF0u, 0, 0));
-        }
-    }
+        for (int r = 0; r < 4; ++r)
+            q4[i][r] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, ok ? (row0 + 4 * r) * nb + 16 * q : 0xFFFFFFF0u, 0, 0));
+    };
+    issue(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
@@ -428,10 +426,24 @@ __global__ __launch_bounds__(64 * kTabWaves) void vq2_matvec_table(const uint8_t
     for (int i = 0; i < BMAX; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[i][r] = 0.f;
+    // 3. the first table, then the rest of the index stream. Issued whole before the first table,
+    //    the stream queued the cold codebook's read behind all 34 MB of index reads (the table
+    //    was ready ~4 us after the start at 151936x896); with the first batch alone in flight
+    //    the codebook arrives early and the first pass's lookups overlap the stream (12.5 ->
+    //    11.7 us, 131072x1024 12.4 -> 11.3). The first batch keeps HBM busy meanwhile.
+    build(0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 1; i < BMAX; ++i) issue(i);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-        if (p) __syncthreads();  // every lookup of the first pass is done
-        build(p);
+        if (p) {
+            __syncthreads();  // every lookup of the first pass is done
+            build(1);
+        }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < BMAX; ++i) {
@@ -452,7 +464,7 @@ __global__ __launch_bounds__(64 * kTabWaves) void vq2_matvec_table(const uint8_t
         }
     }
 
-    // 3. per batch: the 4 row sums of each lane added over its 16 lanes by halving exchanges
+    // 4. per batch: the 4 row sums of each lane added over its 16 lanes by halving exchanges
     //    (row_mirror, row_half_mirror, then quad swaps); lanes 4 m + 0 of each 16 keep row
     //    4 m + rho's total
 #pragma unroll
