@@ -609,7 +609,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the matvec would shard by "
-              "output rows with one all-gather of y; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "output rows, each GPU holding whole 16-row tiles and the full x, with one all-gather of y). "
+              "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     tq = load_pkg()

@@ -1,8 +1,8 @@
-"""The reference-side binding of INTEGRATION.md, compiled and linked for real (CPU only).
+"""The reference-side binding, compiled and linked for real (CPU only).
 
-INTEGRATION.md shows the translation unit a tiny-llm maintainer adds (kernels/matvec/
-hip_variants.cpp: the six TINYQWEN_*_VARIANT registrations and the gpu_decode engine
-adapter). This test extracts those C++ blocks from the document, compiles them with g++
+The repository's integration guide carries the translation unit a tiny-llm maintainer adds
+(kernels/matvec/hip_variants.cpp: the six TINYQWEN_*_VARIANT registrations and the gpu_decode
+engine adapter). This test extracts those C++ blocks from that file, compiles them with g++
 against the reference's own headers (kernels/dispatch.h, runtime/model_loader.h), links
 them with the reference's registry (kernels/dispatch.cpp and the rest of the reference,
 compiled unmodified into oracle/_ref/libtqref.so) and with libtqhip.so, and runs a driver
@@ -30,7 +30,7 @@ pytestmark = pytest.mark.skipif(
 
 
 def binding_source():
-    """The C++ blocks of INTEGRATION.md that make up hip_variants.cpp (sections 1 and 4)."""
+    """The C++ blocks of the integration guide that make up hip_variants.cpp (its sections 1 and 4)."""
     text = open(os.path.join(REPO, "INTEGRATION.md")).read()
     blocks = [re.sub(r"^  ", "", b, flags=re.M) for b in re.findall(r"```cpp\n(.*?)```", text, flags=re.S)]
     parts = [b for b in blocks if "TINYQWEN_" in b and "VARIANT" in b]
