@@ -6,7 +6,8 @@ the replays and new activations written before each one: the replay reads the
 buffers at replay time, and the split-K tile counters come back to zero after
 every replay. The list covers every kernel family the step uses: the
 register-path matvec (single, qkv, pair), split-K, the wave-private DMA ring,
-VQ2 and the prefill GEMM. The eager result is also checked against the oracle.
+VQ2 (one wave per row, and the dot-product table kernel with its 128 KB of static LDS) and
+the prefill GEMM. The eager result is also checked against the oracle.
 """
 import numpy as np
 import pytest
@@ -24,13 +25,15 @@ def test_graph_replays_match_eager_runs(gpu, orc):
             "down": (896, 4864), "ring": (40000, 2560), "mm": (300, K)}
     ws = {n: gpu.synth_i4(m, k, G, seed=300 + i) for i, (n, (m, k)) in enumerate(mats.items())}
     wv = gpu.synth_vq2(3072, 1024, seed=400)
+    MT = 151936  # VQ2 lm_head rows: the table kernel
+    wvt = gpu.synth_vq2(MT, K, seed=401)
     dw = {n: gpu.DeviceBuffer.from_array(w) for n, w in ws.items()}
-    dwv = gpu.DeviceBuffer.from_array(wv)
+    dwv, dwvt = gpu.DeviceBuffer.from_array(wv), gpu.DeviceBuffer.from_array(wvt)
     NT = 7  # prefill tokens
     xk = {K: gpu.DeviceBuffer(4 * K), 4864: gpu.DeviceBuffer(4 * 4864), 2560: gpu.DeviceBuffer(4 * 2560),
           1024: gpu.DeviceBuffer(4 * 1024), "mm": gpu.DeviceBuffer(4 * K * NT)}
     dy = {n: gpu.DeviceBuffer(4 * m * (NT if n == "mm" else 1)) for n, (m, _) in mats.items()}
-    dyv = gpu.DeviceBuffer(4 * 3072)
+    dyv, dyvt = gpu.DeviceBuffer(4 * 3072), gpu.DeviceBuffer(4 * MT)
     Op = gpu.Op
     ops = [
         Op(gpu.OP_I4_MATVEC, dw["single"].ptr, xk[K].ptr, dy["single"].ptr, 4864, K, 1, G, None, None, None, None, 0),
@@ -42,11 +45,13 @@ def test_graph_replays_match_eager_runs(gpu, orc):
         Op(gpu.OP_I4_MATVEC, dw["ring"].ptr, xk[2560].ptr, dy["ring"].ptr, 40000, 2560, 1, G, None, None, None, None,
            0),
         Op(gpu.OP_VQ2_MATVEC, dwv.ptr, xk[1024].ptr, dyv.ptr, 3072, 1024, 1, 0, None, None, None, None, 0),
+        Op(gpu.OP_VQ2_MATVEC, dwvt.ptr, xk[K].ptr, dyvt.ptr, MT, K, 1, 0, None, None, None, None, 0),
         Op(gpu.OP_I4_MATMUL, dw["mm"].ptr, xk["mm"].ptr, dy["mm"].ptr, 300, K, NT, G, None, None, None, None, 0),
     ]
-    outs = list(dy.items()) + [("vq2", dyv)]
+    outs = list(dy.items()) + [("vq2", dyv), ("vq2_table", dyvt)]
     sizes = {n: m * (NT if n == "mm" else 1) for n, (m, _) in mats.items()}
     sizes["vq2"] = 3072
+    sizes["vq2_table"] = MT
 
     def set_inputs(seed):
         xs = {}
@@ -83,6 +88,8 @@ def test_graph_replays_match_eager_runs(gpu, orc):
             assert rel_l2(want[n], ref) <= 1e-5 and max_abs_rel(want[n], ref) <= 1e-3, n
         ref = orc.matvec_vq2(wv, xs[1024], 3072, 1024)
         assert rel_l2(want["vq2"], ref) <= 1e-5, "vq2"
+        ref = orc.matvec_vq2(wvt, xs[K], MT, K, threads=8)
+        assert rel_l2(want["vq2_table"], ref) <= 1e-5 and max_abs_rel(want["vq2_table"], ref) <= 1e-3, "vq2_table"
     finally:
         graph.close()
 
