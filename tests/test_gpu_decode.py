@@ -67,6 +67,31 @@ def test_prompt_logits_match_oracle(gpu, tmp_path, case):
     eng.close()
 
 
+@pytest.mark.parametrize("case", ["qwen25_0p5b_2layers", "qwen3_qknorm_hd128", "head_dim256"])
+def test_fused_layers_match_unfused(gpu, tmp_path, monkeypatch, case):
+    """i4 files at G 64 without rotations run fused layers: the residual adds, the RMSNorms and
+    SwiGLU inside the next projection's set launch (its activation prologue). The same steps
+    with TQHIP_DECODE_UNFUSED set (separate add_rmsnorm and swiglu launches) give the same tokens
+    and logits within 1e-6: the operations are the same, only the double sum of squares of each
+    RMSNorm is added in another order."""
+    m, cfg, _ = open_model(gpu, tmp_path, case)
+    fused = gpu.DecodeEngine(m, 32)
+    monkeypatch.setenv("TQHIP_DECODE_UNFUSED", "1")
+    plain = gpu.DecodeEngine(m, 32)
+    monkeypatch.delenv("TQHIP_DECODE_UNFUSED")
+    same = 0
+    for t in PROMPT:
+        t %= cfg["vocab_size"]
+        a, b = fused.step(t), plain.step(t)
+        la, lb = fused.logits(), plain.logits()
+        assert a == b, (case, t)
+        assert rel_l2(la, lb) <= 1e-6, (case, t, rel_l2(la, lb))
+        same += np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    print(f"{case}: {same} of {len(PROMPT)} steps bit-identical")
+    fused.close()
+    plain.close()
+
+
 def test_greedy_generation_and_reset_replay(gpu, tmp_path):
     from oracle.decode import DenseDecoder
     m, cfg, tensors = open_model(gpu, tmp_path, "qwen25_0p5b_2layers", seed=7)

@@ -70,31 +70,33 @@ __device__ float block_max(float v, float *red) {
     return t;
 }
 
-// hidden += delta (when given); out = rmsnorm(hidden) * w. rmsnorm_ref
+// hidden += delta, then += delta2 (each when given); out = rmsnorm(hidden) * w. rmsnorm_ref
 // (kernels/rmsnorm/rmsnorm_ref.cpp): double sum of squares, float mean,
 // 1 / sqrt(mean + eps), then (x * scale) * w. NT threads hold PER values each.
 // The launch is latency-bound: many waves issuing one load each finish sooner
 // than one wave issuing many (6.5 vs 3.4 us at hidden 896).
 template <int NT, int PER>
 __global__ __launch_bounds__(NT) void add_rmsnorm(float *__restrict__ hidden, const float *__restrict__ delta,
-                                                  const float *__restrict__ w, float *__restrict__ out, int n,
-                                                  float eps) {
+                                                  const float *__restrict__ delta2, const float *__restrict__ w,
+                                                  float *__restrict__ out, int n, float eps) {
     __shared__ double red[NT / 64];
-    float h[PER], dl[PER], wv[PER];
+    float h[PER], dl[PER], dl2[PER], wv[PER];
     // Every load is issued before the first store, so they share one round trip.
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int i = threadIdx.x + j * NT;
         h[j] = i < n ? hidden[i] : 0.0f;
         dl[j] = delta && i < n ? delta[i] : 0.0f;
+        dl2[j] = delta2 && i < n ? delta2[i] : 0.0f;
         wv[j] = i < n ? w[i] : 0.0f;
     }
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int i = threadIdx.x + j * NT;
-        if (delta) {
-            h[j] = h[j] + dl[j];
+        if (delta) h[j] = h[j] + dl[j];
+        if (delta2) h[j] = h[j] + dl2[j];
+        if (delta || delta2) {
             if (i < n) hidden[i] = h[j];
         }
         ss += static_cast<double>(h[j]) * static_cast<double>(h[j]);
@@ -109,14 +111,15 @@ __global__ __launch_bounds__(NT) void add_rmsnorm(float *__restrict__ hidden, co
     }
 }
 
-void launch_add_rmsnorm(float *hidden, const float *delta, const float *w, float *out, int n, float eps,
-                        hipStream_t s) {
+void launch_add_rmsnorm(float *hidden, const float *delta, const float *delta2, const float *w, float *out, int n,
+                        float eps, hipStream_t s) {
     if (n <= kNormThreads)
-        add_rmsnorm<kNormThreads, 1><<<1, kNormThreads, 0, s>>>(hidden, delta, w, out, n, eps);
+        add_rmsnorm<kNormThreads, 1><<<1, kNormThreads, 0, s>>>(hidden, delta, delta2, w, out, n, eps);
     else if (n <= 4 * kNormThreads)
-        add_rmsnorm<kNormThreads, 4><<<1, kNormThreads, 0, s>>>(hidden, delta, w, out, n, eps);
+        add_rmsnorm<kNormThreads, 4><<<1, kNormThreads, 0, s>>>(hidden, delta, delta2, w, out, n, eps);
     else
-        add_rmsnorm<kNormThreads, kMaxHidden / kNormThreads><<<1, kNormThreads, 0, s>>>(hidden, delta, w, out, n, eps);
+        add_rmsnorm<kNormThreads, kMaxHidden / kNormThreads><<<1, kNormThreads, 0, s>>>(hidden, delta, delta2, w, out, n,
+                                                                                          eps);
 }
 
 // Row `*token` of an fp32 embedding table.
@@ -412,6 +415,11 @@ struct Engine {
     float *hidden = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr,
           *o = nullptr, *gate = nullptr, *up = nullptr, *ffn = nullptr, *logits = nullptr, *kv = nullptr,
           *amax_v = nullptr, *rotbuf = nullptr;
+    // Fused layers (i4 files without rotations whose projections the set kernel takes): the
+    // residual adds, the RMSNorms and SwiGLU run inside the next projection's launch (its
+    // activation prologue), and the layers' hidden states alternate between hidden and hidden2.
+    bool fused = false;
+    float *hidden2 = nullptr;
     size_t rotbuf_floats = 0;
     int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next
     int *host_io = nullptr;                     // pinned mirror of dev_io
@@ -465,6 +473,7 @@ int mv_rotated_set(const Engine &e, int n, const uint8_t *const *w, float *const
 int forward(Engine &e) {
     hipStream_t s = e.stream;
     const int H = e.c.hidden_size, I = e.c.intermediate_size;
+    const float eps = e.c.rms_norm_eps;
     int st = kOk;
     if (e.embed_i4) {
         st = launch_i4_embed_rows(static_cast<const uint8_t *>(e.embed), e.dev_io + 1, 1, H, e.gs, e.hidden, s);
@@ -472,15 +481,30 @@ int forward(Engine &e) {
     } else {
         embed_f32_row<<<(H + 255) / 256, 256, 0, s>>>(static_cast<const float *>(e.embed), e.dev_io + 1, e.hidden, H);
     }
-    launch_add_rmsnorm(e.hidden, nullptr, e.layers[0].in_ln, e.normed, H, e.c.rms_norm_eps, s);
+    if (!e.fused) launch_add_rmsnorm(e.hidden, nullptr, nullptr, e.layers[0].in_ln, e.normed, H, eps, s);
+    // A fused launch that does not apply returns kNotFused; the engine chose fused layers
+    // only where every one applies, so that is a launch failure here.
+    auto fused_set = [&](int n, const I4Mat *m, const SetPrologue &p) {
+        const int r = launch_i4_matvec_set_pro(n, m, e.gs, p, s);
+        return r == kNotFused ? static_cast<int>(kLaunchFailed) : r;
+    };
     for (size_t li = 0; li < e.layers.size(); ++li) {
         const Layer &L = e.layers[li];
         float *kc = e.kv + (2 * li) * e.layer_stride, *vc = e.kv + (2 * li + 1) * e.layer_stride;
+        // fused: this layer's hidden state, cur = (prev + o) + ffn of the layer before, stored by
+        // the q/k/v launch (layer 0: the embedding, in hidden)
+        float *cur = (li & 1) ? e.hidden2 : e.hidden, *prev = (li & 1) ? e.hidden : e.hidden2;
         const uint8_t *w3[3] = {L.q, L.k, L.v};
         float *y3[3] = {e.q, e.k, e.v};
         const int d3[3] = {e.q_dim, e.kv_dim, e.kv_dim};
         const Rot *r3[3] = {&L.rq, &L.rk, &L.rv};
-        if (e.pd == 3 && !L.rotated) {
+        if (e.fused) {
+            const float *xb = li == 0 ? e.hidden : prev;
+            const I4Mat m3[3] = {{L.q, xb, e.q, e.q_dim, H}, {L.k, xb, e.k, e.kv_dim, H}, {L.v, xb, e.v, e.kv_dim, H}};
+            const SetPrologue p{2, nullptr, li == 0 ? nullptr : e.o, li == 0 ? nullptr : e.ffn, L.in_ln,
+                                li == 0 ? nullptr : cur, eps};
+            if ((st = fused_set(3, m3, p)) != kOk) return st;
+        } else if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
         } else if ((st = mv_rotated_set(e, 3, w3, y3, d3, H, r3, s)) != kNotFused) {
             if (st != kOk) return st;
@@ -494,7 +518,17 @@ int forward(Engine &e) {
                                                   e.dev_io, e.c.n_heads / e.c.n_kv_heads, e.max_seq, e.c.rope_theta,
                                                   e.c.rms_norm_eps, e.attn_scale);
         if ((st = mvr(e, L.o, e.pd, e.attn, e.o, H, e.q_dim, L.ro, s)) != kOk) return st;
-        launch_add_rmsnorm(e.hidden, e.o, L.post_ln, e.normed, H, e.c.rms_norm_eps, s);
+        if (e.fused) {
+            // gate/up read rmsnorm(cur + o) * post_ln; down reads silu(gate) * up
+            const I4Mat m2[2] = {{L.gate, cur, e.gate, I, H}, {L.up, cur, e.up, I, H}};
+            if ((st = fused_set(2, m2, SetPrologue{2, nullptr, e.o, nullptr, L.post_ln, nullptr, eps})) != kOk)
+                return st;
+            const I4Mat m1[1] = {{L.down, e.gate, e.ffn, H, I}};
+            if ((st = fused_set(1, m1, SetPrologue{1, e.up, nullptr, nullptr, nullptr, nullptr, eps})) != kOk)
+                return st;
+            continue;
+        }
+        launch_add_rmsnorm(e.hidden, e.o, nullptr, L.post_ln, e.normed, H, eps, s);
         const uint8_t *w2[2] = {L.gate, L.up};
         float *y2[2] = {e.gate, e.up};
         const int d2[2] = {I, I};
@@ -510,7 +544,11 @@ int forward(Engine &e) {
         swiglu<<<(I + 255) / 256, 256, 0, s>>>(e.gate, e.up, I);
         if ((st = mvr(e, L.down, e.pd, e.gate, e.ffn, H, I, L.rd, s)) != kOk) return st;
         const float *next_ln = li + 1 < e.layers.size() ? e.layers[li + 1].in_ln : e.final_norm;
-        launch_add_rmsnorm(e.hidden, e.ffn, next_ln, e.normed, H, e.c.rms_norm_eps, s);
+        launch_add_rmsnorm(e.hidden, e.ffn, nullptr, next_ln, e.normed, H, eps, s);
+    }
+    if (e.fused) {  // the last layer's (cur + o) + ffn, normed with the final norm
+        float *last = ((e.layers.size() - 1) & 1) ? e.hidden2 : e.hidden;
+        launch_add_rmsnorm(last, e.o, e.ffn, e.final_norm, e.normed, H, eps, s);
     }
     if ((st = mv(e, e.lm_head, e.lm_dtype, e.normed, e.logits, e.c.vocab_size, H, s)) != kOk) return st;
     argmax_partial<<<e.amax_blocks, kArgmaxThreads, 0, s>>>(e.logits, e.c.vocab_size, e.amax_v, e.amax_i);
@@ -709,11 +747,11 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
                              static_cast<size_t>(e->kv_dim), static_cast<size_t>(e->q_dim), H, I, I, H, V,
                              2 * static_cast<size_t>(c.n_layers) * e->layer_stride,
                              static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 4,
-                             f16_floats, std::max<size_t>(std::max<size_t>(3 * H, I), e->q_dim)};
+                             f16_floats, std::max<size_t>(std::max<size_t>(3 * H, I), e->q_dim), H};
     float **slots[] = {&e->hidden, &e->normed, &e->q, &e->k, &e->v, &e->attn, &e->o, &e->gate, &e->up, &e->ffn,
                        &e->logits, &e->kv, &e->amax_v};
-    size_t offs[17], total = 0;
-    for (int i = 0; i < 17; ++i) {
+    size_t offs[18], total = 0;
+    for (int i = 0; i < 18; ++i) {
         offs[i] = total;
         total += (counts[i] * 4 + 255) / 256 * 256;
     }
@@ -734,6 +772,17 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     }
     e->rotbuf = reinterpret_cast<float *>(base + offs[16]);
     e->rotbuf_floats = counts[16];
+    e->hidden2 = reinterpret_cast<float *>(base + offs[17]);
+    // fused layers where the set kernel takes every projection around a residual add, an
+    // RMSNorm or SwiGLU: q/k/v and gate/up (rows of hidden_size) and down (intermediate_size)
+    bool any_rot = false, aligned = true;
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    for (const Layer &L : e->layers) {
+        any_rot = any_rot || L.rotated;
+        aligned = aligned && al16(L.in_ln) && al16(L.post_ln);
+    }
+    e->fused = e->pd == 3 && !any_rot && aligned && set_kernel_takes(c.hidden_size, e->gs) &&
+               set_kernel_takes(c.intermediate_size, e->gs) && std::getenv("TQHIP_DECODE_UNFUSED") == nullptr;
     float *conv = reinterpret_cast<float *>(base + offs[15]);
     for (const F16Vec &f : f16s) {
         f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);

@@ -50,6 +50,7 @@ struct SetMat {
 struct SetArgs {
     SetMat m[kSetMaxMats];
     int n;
+    SetPrologue pro;  // XM != 0 instances only
 };
 
 // ---- activations as exact integers -------------------------------------------------------
@@ -133,8 +134,27 @@ __device__ __forceinline__ float half_group_int(const v4i &cd, unsigned hd, cons
 
 // Rows of at most 32 half-groups (S = 0): R rows per half-wave, 2R per wave, 8R per
 // workgroup. Rows of more: R per wave over S slots, kSetWaves R per workgroup.
-template <int S, int R>
-__device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char *lds) {
+// Sum of v over the workgroup, in double, in a fixed order (each wave by shuffles, then the
+// kSetWaves wave sums in wave order).
+__device__ inline double set_block_sum(double v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __shared__ double red[kSetWaves];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = red[0];
+#pragma unroll
+    for (int w = 1; w < kSetWaves; ++w) t += red[w];
+    return t;
+}
+
+__device__ inline float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// XM: the activation prologue (0 none; 1 x = silu(x) * x2; 2 x = rmsnorm((x + d1) + d2) * nw,
+// workgroup 0 storing the sum to hout), with its operands in pro.
+template <int S, int R, int XM>
+__device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char *lds, const SetPrologue &pro) {
     // 16-byte activation loads per thread: the chunks of the widest row of this shape
     constexpr int NX = ((S == 0 ? 256 : 512 * S) + kSetThreads - 1) / kSetThreads;
     constexpr int NR = R;                   // rows per lane
@@ -155,6 +175,25 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
     float4 xq[NX];
 #pragma unroll
     for (int i = 0; i < NX; ++i) xq[i] = x4[min(t + kSetThreads * i, Kc - 1)];
+    // the prologue's operands, loaded with x: up (XM 1); the deltas and the norm weight (XM 2)
+    constexpr int NP = XM ? NX : 1, NQ = XM == 2 ? NX : 1;
+    float4 pa[NP], pb[NQ], pw[NQ];
+    if constexpr (XM == 1) {
+        const float4 *u4 = reinterpret_cast<const float4 *>(pro.x2);
+#pragma unroll
+        for (int i = 0; i < NX; ++i) pa[i] = u4[min(t + kSetThreads * i, Kc - 1)];
+    } else if constexpr (XM == 2) {
+        const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 *d1 = reinterpret_cast<const float4 *>(pro.d1), *d2 = reinterpret_cast<const float4 *>(pro.d2);
+        const float4 *w4 = reinterpret_cast<const float4 *>(pro.nw);
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            const int c = min(t + kSetThreads * i, Kc - 1);
+            pa[i] = d1 ? d1[c] : zero;
+            pb[i] = d2 ? d2[c] : zero;
+            pw[i] = w4[c];
+        }
+    }
 
     // 2. the weights: lane u of a row takes half-group u (+ 64 per slot)
     const int half = S == 0 ? lane >> 5 : 0, u = S == 0 ? lane & 31 : lane;
@@ -187,6 +226,43 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
     // 3. activations to integer operands in LDS, while the weights arrive. Every iteration
     // runs (stage_x writes only chunks below C): a loop that stopped early would let the
     // compiler sink the later activation loads behind the weight loads.
+    if constexpr (XM == 1) {  // swiglu_ref (kernels/silu/swiglu_ref.cpp): silu(g) * u
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            float e[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w};
+            const float u[4] = {pa[i].x, pa[i].y, pa[i].z, pa[i].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) e[c] = (e[c] / (1.0f + expf(-e[c]))) * u[c];
+            xq[i] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+    } else if constexpr (XM == 2) {
+        // hidden + delta(s) in the runtime's order, then rmsnorm_ref (kernels/rmsnorm/rmsnorm_ref.cpp):
+        // a double sum of squares, a float mean, 1 / sqrt(mean + eps), (h * scale) * w
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            if (pro.d1) xq[i] = add4(xq[i], pa[i]);
+            if (pro.d2) xq[i] = add4(xq[i], pb[i]);
+            if (t + kSetThreads * i < Kc) {
+                const float4 h = xq[i];
+                ss += static_cast<double>(h.x) * h.x + static_cast<double>(h.y) * h.y +
+                      static_cast<double>(h.z) * h.z + static_cast<double>(h.w) * h.w;
+            }
+        }
+        if (pro.hout && blockIdx.x == 0) {
+            float4 *h4 = reinterpret_cast<float4 *>(pro.hout);
+#pragma unroll
+            for (int i = 0; i < NX; ++i)
+                if (t + kSetThreads * i < Kc) h4[t + kSetThreads * i] = xq[i];
+        }
+        ss = set_block_sum(ss);
+        const float mean_sq = static_cast<float>(ss / m.K);
+        const float scale = 1.0f / sqrtf(mean_sq + pro.eps);
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            xq[i] = make_float4((xq[i].x * scale) * pw[i].x, (xq[i].y * scale) * pw[i].y, (xq[i].z * scale) * pw[i].z,
+                                (xq[i].w * scale) * pw[i].w);
+    }
 #pragma unroll
     for (int i = 0; i < NX; ++i) stage_x(xq[i], t + kSetThreads * i, Kc, C, xp, hs);
     __builtin_amdgcn_sched_barrier(0);
@@ -231,7 +307,7 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
 // SMAX: the largest shape in the launch (the register budget follows it); R: rows per
 // half-wave for the short rows; RL: rows per wave for the long rows (two rows share the
 // activation operands each wave reads from LDS and halve the workgroups that convert x).
-template <int SMAX, int R, int RL>
+template <int SMAX, int R, int RL, int XM = 0>
 __global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs a) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int b = blockIdx.x;
@@ -244,17 +320,17 @@ __global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs a) {
         if (i == j) m = a.m[i];
     const int blk = b - m.blk0;
     if (m.shape == 0) {
-        set_rows<0, R>(m, blk, lds);
+        set_rows<0, R, XM>(m, blk, lds, a.pro);
     } else if (SMAX <= 1 || m.shape == 1) {
-        set_rows<1, RL>(m, blk, lds);
+        set_rows<1, RL, XM>(m, blk, lds, a.pro);
     } else if (SMAX <= 2 || m.shape == 2) {
-        set_rows<2, RL>(m, blk, lds);
+        set_rows<2, RL, XM>(m, blk, lds, a.pro);
     } else if (SMAX <= 3 || m.shape == 3) {
-        set_rows<3, RL>(m, blk, lds);
+        set_rows<3, RL, XM>(m, blk, lds, a.pro);
     } else if (SMAX <= 4 || m.shape == 4) {
-        set_rows<4, RL>(m, blk, lds);
+        set_rows<4, RL, XM>(m, blk, lds, a.pro);
     } else {
-        set_rows<5, RL>(m, blk, lds);
+        set_rows<5, RL, XM>(m, blk, lds, a.pro);
     }
 }
 
@@ -267,16 +343,27 @@ int set_shape(const I4Mat &mt, int group_size) {
     return mt.K <= 1024 ? 0 : (mt.K + 64 * 32 - 1) / (64 * 32);
 }
 
-template <int R, int RL>
+template <int R, int RL, int XM>
 void launch_r(int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream, const SetArgs &a) {
     switch (smax) {
-        case 0: hipLaunchKernelGGL((i4_matvec_set<0, R, 1>), grid, block, lds, stream, a); break;
-        case 1: hipLaunchKernelGGL((i4_matvec_set<1, R, RL>), grid, block, lds, stream, a); break;
-        case 2: hipLaunchKernelGGL((i4_matvec_set<2, R, RL>), grid, block, lds, stream, a); break;
-        case 3: hipLaunchKernelGGL((i4_matvec_set<3, R, RL>), grid, block, lds, stream, a); break;
-        case 4: hipLaunchKernelGGL((i4_matvec_set<4, R, RL>), grid, block, lds, stream, a); break;
-        default: hipLaunchKernelGGL((i4_matvec_set<5, R, RL>), grid, block, lds, stream, a); break;
+        case 0: hipLaunchKernelGGL((i4_matvec_set<0, R, 1, XM>), grid, block, lds, stream, a); break;
+        case 1: hipLaunchKernelGGL((i4_matvec_set<1, R, RL, XM>), grid, block, lds, stream, a); break;
+        case 2: hipLaunchKernelGGL((i4_matvec_set<2, R, RL, XM>), grid, block, lds, stream, a); break;
+        case 3: hipLaunchKernelGGL((i4_matvec_set<3, R, RL, XM>), grid, block, lds, stream, a); break;
+        case 4: hipLaunchKernelGGL((i4_matvec_set<4, R, RL, XM>), grid, block, lds, stream, a); break;
+        default: hipLaunchKernelGGL((i4_matvec_set<5, R, RL, XM>), grid, block, lds, stream, a); break;
     }
+}
+
+template <int XM>
+void launch_rr(int R, int RL, int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream,
+               const SetArgs &a) {
+    if (R == 2)
+        RL == 2 ? launch_r<2, 2, XM>(smax, grid, block, lds, stream, a)
+                : launch_r<2, 1, XM>(smax, grid, block, lds, stream, a);
+    else
+        RL == 2 ? launch_r<1, 2, XM>(smax, grid, block, lds, stream, a)
+                : launch_r<1, 1, XM>(smax, grid, block, lds, stream, a);
 }
 
 // Two long rows per wave when every long-row matrix of the launch has at least this many rows.
@@ -294,8 +381,9 @@ int long_rows_per_wave(const I4Mat *mats, const int *shape, int n) {
     return any ? 2 : 1;
 }
 
-int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream) {
+int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream, const SetPrologue *pro = nullptr) {
     SetArgs a{};
+    if (pro) a.pro = *pro;
     int order[kSetMaxMats];
     for (int i = 0; i < n; ++i) order[i] = i;
     // longest rows first: their workgroups are dispatched first
@@ -321,10 +409,13 @@ int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream) {
     a.n = n;
     const size_t lds = static_cast<size_t>(umax) * (4 * kBlockBytes + 8);  // the widest row's operands
     const dim3 grid(blocks), block(kSetThreads);
-    if (R == 2)
-        RL == 2 ? launch_r<2, 2>(smax, grid, block, lds, stream, a) : launch_r<2, 1>(smax, grid, block, lds, stream, a);
+    const int xm = pro ? pro->kind : 0;
+    if (xm == 1)
+        launch_rr<1>(R, RL, smax, grid, block, lds, stream, a);
+    else if (xm == 2)
+        launch_rr<2>(R, RL, smax, grid, block, lds, stream, a);
     else
-        RL == 2 ? launch_r<1, 2>(smax, grid, block, lds, stream, a) : launch_r<1, 1>(smax, grid, block, lds, stream, a);
+        launch_rr<0>(R, RL, smax, grid, block, lds, stream, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -351,6 +442,25 @@ int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream
                                 : (mats[i].M + RL * kSetWaves - 1) / (RL * kSetWaves);
     if (blocks > static_cast<long>(kSetMaxBlocksPerCu) * device_cu_count()) return kNotFused;
     return launch_set(mats, shape, n, stream);
+}
+
+bool set_kernel_takes(int K, int group_size) {
+    const I4Mat probe{nullptr, nullptr, nullptr, 1, K};  // (a null x is 16-byte aligned)
+    return K >= 1 && set_shape(probe, group_size) >= 0;
+}
+
+int launch_i4_matvec_set_pro(int n, const I4Mat *mats, int group_size, const SetPrologue &pro, hipStream_t stream) {
+    if (n < 1 || n > kSetMaxMats || pro.kind < 1 || pro.kind > 2) return kNotFused;
+    const auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (!al(pro.x2) || !al(pro.d1) || !al(pro.d2) || !al(pro.nw) || !al(pro.hout) ||
+        (pro.kind == 1 && !pro.x2) || (pro.kind == 2 && !pro.nw))
+        return kNotFused;
+    int shape[kSetMaxMats];
+    for (int i = 0; i < n; ++i) {
+        shape[i] = set_shape(mats[i], group_size);
+        if (shape[i] < 0 || mats[i].M < 1 || mats[i].x != mats[0].x || mats[i].K != mats[0].K) return kNotFused;
+    }
+    return launch_set(mats, shape, n, stream, &pro);
 }
 
 int launch_i4_matvec_set(int n, const I4Mat *mats, int group_size, hipStream_t stream) {

@@ -77,6 +77,22 @@ int launch_i4_matvec_set(int n, const I4Mat *mats, int group_size, hipStream_t s
 // The set kernel for a single or fused launch when every matrix takes it and its grid is small
 // enough to beat the MFMA kernels; kNotFused (nothing launched) otherwise.
 int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream_t stream);
+// Activation prologue of a set launch whose matrices all read the same x (the decode engine's
+// fused launches), applied as the activations are loaded:
+//   kind 1: x = silu(x) * x2 (swiglu_ref);
+//   kind 2: h = (x + d1) + d2 (d1, d2 optional), x = rmsnorm(h) * nw (rmsnorm_ref, eps), and
+//           workgroup 0 also stores h to hout when hout is given.
+struct SetPrologue {
+    int kind;
+    const float *x2, *d1, *d2, *nw;
+    float *hout;
+    float eps;
+};
+// The set kernel with a prologue for n matrices sharing x (mats[i].x equal, 16-byte aligned like
+// x2, d1, d2, nw and hout); kNotFused (nothing launched) when the set kernel does not take them.
+int launch_i4_matvec_set_pro(int n, const I4Mat *mats, int group_size, const SetPrologue &pro, hipStream_t stream);
+// Whether the set kernel takes rows of K elements at this group size (with x 16-byte aligned).
+bool set_kernel_takes(int K, int group_size);
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
 int launch_i4_embed_rows(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
                          hipStream_t stream);
