@@ -114,6 +114,16 @@ typedef struct tqhip_i4_mat {
  * it where those run (rows up to 1024 wide on small grids, up to 6144 wide on very small
  * ones). mats is read during the call. */
 int tqhip_matvec_i4_set_dev(const tqhip_i4_mat *mats, int n, int group_size, void *stream);
+/* n independent VQ2 matvecs y_i = W_i x_i, each with its own activation vector and shape
+ * (tqhip_i4_mat's fields: the weights are a VQ2 tensor, codebook then indices). No
+ * counterpart in the reference, whose runtime issues a VQ2 layer as single matvec_vq2 calls
+ * (its pair and qkv forms are decompositions, kernels/dispatch.cpp:511-532): this is the
+ * "matvec set" for VQ2 as one launch. Every matrix with in_dim % 16 == 0, 4-byte aligned
+ * weights and at most 4M lookups (out_dim * in_dim / 4) goes into one launch per 8 such
+ * matrices, while a launch holds at most 8M lookups; any other runs alone through
+ * tqhip_matvec_vq2_dev's kernels. Each output has the same bits tqhip_matvec_vq2_dev gives
+ * it. mats is read during the call. */
+int tqhip_matvec_vq2_set_dev(const tqhip_i4_mat *mats, int n, void *stream);
 /* tqhip_matmul_i4_dev without any allocation. No counterpart in the reference: this is
  * for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc). Same kernels and results as

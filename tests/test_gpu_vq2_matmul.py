@@ -193,3 +193,59 @@ def test_matmul_i4_prefill_rows_full_shape_128_tokens(gpu, orc):
     gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G)
     want = orc.matmul_i4(w, x, M, K, N, G, threads=16)
     assert_close(dy.download(np.float32, M * N), want, 2e-3, "9728x2560x128")
+
+
+# tqhip_matvec_vq2_set_dev: a VQ2 layer's projections with their own activations in one launch of
+# the one-wave-per-row kernel. Every output within the matvec bar of the oracle and bit-identical
+# to tqhip_matvec_vq2_dev on the same matrix. Cases: the Qwen2.5-0.5B layer (q/k/v sharing x,
+# gate/up sharing x, o and down with their own), more than eight matrices (two launches), a launch
+# closed at 8M lookups, matrices that run alone (in_dim % 16 != 0, above 4M lookups), x at a
+# 4-byte offset (the scalar activation loads for the whole launch), and the error codes.
+def _vq2_set_case(gpu, orc, spec, seed, x_offset=0):
+    xs, mats = {}, []
+    for i, (M, K, key) in enumerate(spec):
+        if key not in xs:
+            x = gpu.synth_normal(K, seed=seed + 100 + len(xs))
+            xb = np.zeros(K + 4, np.float32)
+            xb[x_offset // 4:x_offset // 4 + K] = x
+            xs[key] = (x, gpu.DeviceBuffer.from_array(xb))
+        w = gpu.synth_vq2(M, K, seed=seed + i)
+        mats.append((M, K, w, xs[key], gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer(4 * M)))
+    arr = gpu.i4_set([(dw, x[1].ptr + x_offset, dy, M, K) for M, K, _, x, dw, dy in mats])
+    for M, _, _, _, _, dy in mats:
+        gpu.lib().tqhip_memset(dy.ptr, 0xFF, 4 * M)  # every output must be written by the set
+    gpu.matvec_vq2_set_dev(arr)
+    gpu.synchronize()
+    for i, (M, K, w, x, dw, dy) in enumerate(mats):
+        got = dy.download(np.float32, M)
+        assert_close(got, orc.matvec_vq2(w, x[0], M, K, threads=8), 1e-5, f"set matrix {i} {M}x{K}")
+        alone = gpu.DeviceBuffer(4 * M)
+        assert gpu.lib().tqhip_matvec_vq2_dev(dw.ptr, x[1].ptr + x_offset, alone.ptr, M, K, None) == 0
+        gpu.synchronize()
+        assert np.array_equal(got.view(np.uint32), alone.download(np.float32, M).view(np.uint32)), \
+            f"set matrix {i} {M}x{K}: differs from the single launch"
+
+
+def test_vq2_set_qwen25_layer(gpu, orc):
+    _vq2_set_case(gpu, orc, [(896, 896, "a"), (128, 896, "a"), (128, 896, "a"), (896, 896, "o"),
+                             (4864, 896, "m"), (4864, 896, "m"), (896, 4864, "d")], seed=3)
+
+
+def test_vq2_set_many_mixed_and_offset(gpu, orc):
+    spec = [(300 + 37 * i, 64 * (1 + i % 5), "k%d" % (i % 5)) for i in range(10)]  # ten: two launches
+    spec += [(2001, 3052, "odd"),        # in_dim % 16 != 0: alone (byte kernel)
+             (20000, 1024, "big"),       # 5.1M lookups: alone (replica kernel)
+             (16384, 1024, "c1"), (16384, 1024, "c1")]  # 4M lookups each: the second opens a new launch
+    _vq2_set_case(gpu, orc, spec, seed=11)
+    _vq2_set_case(gpu, orc, [(896, 896, "a"), (128, 896, "a"), (4864, 896, "m")], seed=5, x_offset=4)
+
+
+def test_vq2_set_errors(gpu):
+    lib = gpu.lib()
+    w, x, y = gpu.DeviceBuffer(4096), gpu.DeviceBuffer(4096), gpu.DeviceBuffer(4096)
+    assert lib.tqhip_matvec_vq2_set_dev(None, 1, None) == gpu.EBADSHAPE
+    assert lib.tqhip_matvec_vq2_set_dev(None, 0, None) == gpu.OK  # an empty set launches nothing
+    arr = gpu.i4_set([(w, x, y, 4, 6)])  # in_dim not a multiple of 4
+    assert lib.tqhip_matvec_vq2_set_dev(gpu.ctypes.addressof(arr), 1, None) == gpu.EBADSHAPE
+    arr = gpu.i4_set([(w, x, y, 0, 64)])
+    assert lib.tqhip_matvec_vq2_set_dev(gpu.ctypes.addressof(arr), 1, None) == gpu.EBADSHAPE

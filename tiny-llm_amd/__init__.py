@@ -87,6 +87,7 @@ _SIGS = {
     "tqhip_matmul_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matmul_i4_noalloc_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tqhip_matvec_i4_set_dev": (_i, [_vp, _i, _i, _vp]),
+    "tqhip_matvec_vq2_set_dev": (_i, [_vp, _i, _vp]),
     "tqhip_biip_rotate_dev": (_i, [_vp, _vp, _i, _vp, _vp, _i, _vp]),
     "tqhip_dequant_i4_rows_dev": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp]),
     # registry
@@ -427,6 +428,12 @@ def matvec_i4_set_dev(mats, group_size: int, stream=None) -> None:
     arr = mats if isinstance(mats, ctypes.Array) else i4_set(mats)
     _check(lib().tqhip_matvec_i4_set_dev(ctypes.addressof(arr), len(arr), group_size, _stream(stream)),
            "tqhip_matvec_i4_set_dev")
+
+
+def matvec_vq2_set_dev(mats, stream=None) -> None:
+    """tqhip_matvec_vq2_set_dev over a tqhip_i4_mat array (see i4_set) or a list of tuples."""
+    arr = mats if isinstance(mats, ctypes.Array) else i4_set(mats)
+    _check(lib().tqhip_matvec_vq2_set_dev(ctypes.addressof(arr), len(arr), _stream(stream)), "tqhip_matvec_vq2_set_dev")
 
 
 def matmul_i4_noalloc_dev(w, x, y, M: int, K: int, N: int, group_size: int, stream=None) -> int:

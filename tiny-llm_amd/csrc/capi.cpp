@@ -269,6 +269,9 @@ int tqhip_matmul_i4_dev(const uint8_t *w, const float *x, float *y, int M, int K
 int tqhip_matvec_i4_set_dev(const tqhip_i4_mat *mats, int n, int group_size, void *stream) {
     return launch_i4_matvec_set(n, reinterpret_cast<const I4Mat *>(mats), group_size, static_cast<hipStream_t>(stream));
 }
+int tqhip_matvec_vq2_set_dev(const tqhip_i4_mat *mats, int n, void *stream) {
+    return launch_vq2_matvec_set(n, reinterpret_cast<const I4Mat *>(mats), static_cast<hipStream_t>(stream));
+}
 int tqhip_matmul_i4_noalloc_dev(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                                 void *stream) {
     static_assert(TQHIP_NOALLOC_SCRATCH_BYTES == kNoAllocScratchBytes, "header and library agree on the size");

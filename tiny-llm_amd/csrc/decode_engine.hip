@@ -450,9 +450,9 @@ int mvr(const Engine &e, const uint8_t *w, int dtype, const float *x, float *y, 
 }
 
 // Projections of one x that all carry a rotation with the same block: the n
-// rotations in one launch (into rotbuf, rotset_stride apart), then the n matvecs
-// (one group launch for i4). kNotFused when the rotations differ in presence
-// or block, or rotbuf cannot hold n copies.
+// rotations in one launch (into rotbuf, K floats apart), then the n matvecs, each
+// on its own rotated copy, as one set launch. kNotFused when the rotations differ
+// in presence or block, or rotbuf cannot hold n copies.
 int mv_rotated_set(const Engine &e, int n, const uint8_t *const *w, float *const *y, const int *m, int K,
                    const Rot *const *r, hipStream_t s) {
     if (static_cast<size_t>(n) * K > e.rotbuf_floats) return kNotFused;
@@ -466,8 +466,10 @@ int mv_rotated_set(const Engine &e, int n, const uint8_t *const *w, float *const
         sg[j] = r[j]->sign;
     }
     int st = launch_biip_rotate_n(n, e.normed, xr, K, sc, sg, r[0]->bs, s);
-    for (int j = 0; j < n && st == kOk; ++j) st = mv(e, w[j], e.pd, xr[j], y[j], m[j], K, s);
-    return st;
+    if (st != kOk) return st;
+    I4Mat mats[3];
+    for (int j = 0; j < n; ++j) mats[j] = I4Mat{w[j], xr[j], y[j], m[j], K};
+    return e.pd == 4 ? launch_vq2_matvec_set(n, mats, s) : launch_i4_matvec_set(n, mats, e.gs, s);
 }
 
 int forward(Engine &e) {
@@ -506,6 +508,10 @@ int forward(Engine &e) {
             if ((st = fused_set(3, m3, p)) != kOk) return st;
         } else if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
+        } else if (e.pd == 4 && !L.rotated) {
+            const I4Mat m3[3] = {{L.q, e.normed, e.q, e.q_dim, H}, {L.k, e.normed, e.k, e.kv_dim, H},
+                                 {L.v, e.normed, e.v, e.kv_dim, H}};
+            if ((st = launch_vq2_matvec_set(3, m3, s)) != kOk) return st;
         } else if ((st = mv_rotated_set(e, 3, w3, y3, d3, H, r3, s)) != kNotFused) {
             if (st != kOk) return st;
         } else {
@@ -535,6 +541,9 @@ int forward(Engine &e) {
         const Rot *r2[2] = {&L.rg, &L.ru};
         if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(2, w2, y2, d2, e.normed, H, e.gs, s)) != kOk) return st;
+        } else if (e.pd == 4 && !L.rotated) {
+            const I4Mat m2[2] = {{L.gate, e.normed, e.gate, I, H}, {L.up, e.normed, e.up, I, H}};
+            if ((st = launch_vq2_matvec_set(2, m2, s)) != kOk) return st;
         } else if ((st = mv_rotated_set(e, 2, w2, y2, d2, H, r2, s)) != kNotFused) {
             if (st != kOk) return st;
         } else {

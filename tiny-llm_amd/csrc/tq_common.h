@@ -94,6 +94,9 @@ int launch_i4_matvec_set_pro(int n, const I4Mat *mats, int group_size, const Set
 // Whether the set kernel takes rows of K elements at this group size (with x 16-byte aligned).
 bool set_kernel_takes(int K, int group_size);
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
+// n independent VQ2 matvecs (I4Mat: weights, activations, output, shape) in as few launches as
+// the one-wave-per-row kernel allows; each output has the bits launch_vq2_matvec gives it.
+int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream);
 int launch_i4_embed_rows(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
                          hipStream_t stream);
 int launch_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,

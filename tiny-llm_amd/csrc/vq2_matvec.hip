@@ -21,7 +21,9 @@
 // - vq2_matvec_rows (index rows dword-aligned, at most kDirectLookups lookups): one wave per
 //   row and no LDS at all. A grid this small cannot amortise building a 64 KB codebook
 //   replica per workgroup, so every lookup is an 8-byte load of the fp16 entry from the
-//   2 KB codebook in global memory (it stays in each CU's L1 after the first touch).
+//   2 KB codebook in global memory (it stays in each CU's L1 after the first touch). One
+//   launch serves up to kSetMaxMats matrices with their own activations
+//   (launch_vq2_matvec_set: a decoder layer's q/k/v or gate/up).
 // All accumulate in fp32.
 
 #include "tq_common.h"
@@ -255,37 +257,76 @@ __global__ __launch_bounds__(64 * kVq2Waves) void vq2_matvec_copies(const uint8_
 // one-launch floor for its 0.8 MB is 3.3 us), 4864x896 4.1 vs 5.3, 2001x3056 4.7 vs 7.9; from
 // about 8M lookups (16384x2048, 32768x896) the replica kernel is faster.
 constexpr long long kDirectLookups = 4ll << 20;
+// A launch of this kernel serves up to kSetMaxMats matrices, each with its own activations
+// (a layer's q/k/v, gate/up, or rotated copies of x): workgroups are numbered matrix after
+// matrix and a workgroup finds its matrix with scalar compares against the kernel argument.
+// A row's bits do not depend on the other matrices of the launch.
+struct Vq2Mat {
+    const uint8_t *w;
+    const float *x;
+    float *y;
+    int M, K;
+    int blk0;  // first workgroup of this matrix
+};
+struct Vq2SetArgs {
+    Vq2Mat m[kSetMaxMats];
+    int n;
+};
 template <bool XALIGN>
-__global__ __launch_bounds__(256) void vq2_matvec_rows(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                                                       float *__restrict__ y, int M, int K) {
+__global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
+    const int b = blockIdx.x;
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < kSetMaxMats; ++i) j = (i < a.n && b >= a.m[i].blk0) ? i : j;
+    Vq2Mat m = a.m[0];
+#pragma unroll
+    for (int i = 1; i < kSetMaxMats; ++i)
+        if (i == j) m = a.m[i];
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const int nb = K / kVq2Dim;  // index bytes per row (a multiple of 4)
-    const unsigned *qrow = reinterpret_cast<const unsigned *>(w + kVq2CodebookBytes + static_cast<size_t>(row) * nb);
-    const uint2 *cbg = reinterpret_cast<const uint2 *>(w);  // entry e: 4 fp16 in 8 bytes
-    float a = 0.f;
+    const int row = (b - m.blk0) * 4 + (threadIdx.x >> 6);
+    if (row >= m.M) return;
+    const int nb = m.K / kVq2Dim;  // index bytes per row (a multiple of 4)
+    const unsigned *qrow = reinterpret_cast<const unsigned *>(m.w + kVq2CodebookBytes + static_cast<size_t>(row) * nb);
+    const uint2 *cbg = reinterpret_cast<const uint2 *>(m.w);  // entry e: 4 fp16 in 8 bytes
+    float acc = 0.f;
     for (int d = lane; 4 * d < nb; d += 64) {
         const unsigned q = qrow[d];
         float4 xv[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float *xp = x + 16 * d + 4 * j;
-            xv[j] = XALIGN ? *reinterpret_cast<const float4 *>(xp) : make_float4(xp[0], xp[1], xp[2], xp[3]);
+        for (int jj = 0; jj < 4; ++jj) {
+            const float *xp = m.x + 16 * d + 4 * jj;
+            xv[jj] = XALIGN ? *reinterpret_cast<const float4 *>(xp) : make_float4(xp[0], xp[1], xp[2], xp[3]);
         }
         uint2 c[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) c[j] = cbg[(q >> (8 * j)) & 0xFFu];
+        for (int jj = 0; jj < 4; ++jj) c[jj] = cbg[(q >> (8 * jj)) & 0xFFu];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            a = fmaf(half_bits(c[j].x), xv[j].x, a);
-            a = fmaf(half_bits(c[j].x >> 16), xv[j].y, a);
-            a = fmaf(half_bits(c[j].y), xv[j].z, a);
-            a = fmaf(half_bits(c[j].y >> 16), xv[j].w, a);
+        for (int jj = 0; jj < 4; ++jj) {
+            acc = fmaf(half_bits(c[jj].x), xv[jj].x, acc);
+            acc = fmaf(half_bits(c[jj].x >> 16), xv[jj].y, acc);
+            acc = fmaf(half_bits(c[jj].y), xv[jj].z, acc);
+            acc = fmaf(half_bits(c[jj].y >> 16), xv[jj].w, acc);
         }
     }
-    for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off);
-    if (lane == 0) y[row] = a;
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) m.y[row] = acc;
+}
+
+// The matrix the one-wave-per-row kernel takes: index rows dword-aligned, at most
+// kDirectLookups lookups.
+bool rows_kernel_takes(const uint8_t *w, int out_dim, int in_dim) {
+    return (in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0 &&
+           static_cast<long long>(out_dim) * (in_dim / kVq2Dim) <= kDirectLookups;
+}
+
+int launch_rows(Vq2SetArgs &a, int n, int blocks, bool xalign, hipStream_t stream) {
+    for (int k = n; k < kSetMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
+    a.n = n;
+    if (xalign)
+        hipLaunchKernelGGL(vq2_matvec_rows<true>, dim3(blocks), dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(vq2_matvec_rows<false>, dim3(blocks), dim3(256), 0, stream, a);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
 // ---- Dot-product table (large launches, index rows 16-byte aligned, in_dim <= 1024).
@@ -496,13 +537,10 @@ int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, i
     if (out_dim < 1 || in_dim < kVq2Dim || in_dim % kVq2Dim) return kBadShape;
     const int cus = device_cu_count();
     const bool aligned = (in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0;
-    if (aligned && static_cast<long long>(out_dim) * (in_dim / kVq2Dim) <= kDirectLookups) {
-        const dim3 grid((out_dim + 3) / 4);
-        if ((reinterpret_cast<uintptr_t>(x) & 15) == 0)
-            hipLaunchKernelGGL(vq2_matvec_rows<true>, grid, dim3(256), 0, stream, w, x, y, out_dim, in_dim);
-        else
-            hipLaunchKernelGGL(vq2_matvec_rows<false>, grid, dim3(256), 0, stream, w, x, y, out_dim, in_dim);
-        return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+    if (rows_kernel_takes(w, out_dim, in_dim)) {
+        Vq2SetArgs a{};
+        a.m[0] = Vq2Mat{w, x, y, out_dim, in_dim, 0};
+        return launch_rows(a, 1, (out_dim + 3) / 4, (reinterpret_cast<uintptr_t>(x) & 15) == 0, stream);
     }
     if (in_dim % 64 == 0 && in_dim <= kTabMaxDim && (reinterpret_cast<uintptr_t>(w) % 16) == 0 &&
         static_cast<long long>(out_dim) >= static_cast<long long>(kTabMinRowsPerCu) * cus) {
@@ -537,6 +575,41 @@ int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, i
     hipLaunchKernelGGL(vq2_matvec_kernel, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream, w, x, y, out_dim,
                        in_dim);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+// The matrices the one-wave-per-row kernel takes go into one launch per kSetMaxMats of them
+// (a launch is closed early once it holds more than 2 kDirectLookups lookups, where the replica
+// kernel would be faster); any other matrix is launched alone by launch_vq2_matvec. Every row
+// gets the same bits as from launch_vq2_matvec.
+int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream) {
+    if (n < 0 || (n > 0 && !mats)) return kBadShape;
+    for (int i = 0; i < n; ++i)
+        if (mats[i].M < 1 || mats[i].K < kVq2Dim || mats[i].K % kVq2Dim) return kBadShape;
+    Vq2SetArgs a{};
+    int nb = 0, blocks = 0;
+    long long lookups = 0;
+    bool xalign = true;
+    for (int i = 0; i < n; ++i) {
+        const I4Mat &mt = mats[i];
+        if (!rows_kernel_takes(mt.w, mt.M, mt.K)) {
+            const int st = launch_vq2_matvec(mt.w, mt.x, mt.y, mt.M, mt.K, stream);
+            if (st != kOk) return st;
+            continue;
+        }
+        const long long lk = static_cast<long long>(mt.M) * (mt.K / kVq2Dim);
+        if (nb == kSetMaxMats || (nb > 0 && lookups + lk > 2 * kDirectLookups)) {
+            const int st = launch_rows(a, nb, blocks, xalign, stream);
+            if (st != kOk) return st;
+            nb = blocks = 0;
+            lookups = 0;
+            xalign = true;
+        }
+        a.m[nb++] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks};
+        blocks += (mt.M + 3) / 4;
+        lookups += lk;
+        xalign = xalign && (reinterpret_cast<uintptr_t>(mt.x) & 15) == 0;
+    }
+    return nb > 0 ? launch_rows(a, nb, blocks, xalign, stream) : kOk;
 }
 
 }  // namespace tqhip
