@@ -419,6 +419,7 @@ struct Engine {
     // residual adds, the RMSNorms and SwiGLU run inside the next projection's launch (its
     // activation prologue), and the layers' hidden states alternate between hidden and hidden2.
     bool fused = false;
+    bool fused_rot = false;  // VQ2 rotations inside the matvec launches (unless TQHIP_DECODE_UNFUSED)
     float *hidden2 = nullptr;
     size_t rotbuf_floats = 0;
     int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next
@@ -438,9 +439,15 @@ int mv(const Engine &e, const uint8_t *w, int dtype, const float *x, float *y, i
 }
 
 // mv_rot (runtime/qwen_model.cpp:229-238): the activation rotated into rotbuf
-// first when the projection carries a rotation.
+// first when the projection carries a rotation (for VQ2, inside the matvec launch where
+// that takes it: the same bits, one launch fewer).
 int mvr(const Engine &e, const uint8_t *w, int dtype, const float *x, float *y, int M, int K, const Rot &r,
         hipStream_t s) {
+    if (r.sign && dtype == 4 && e.fused_rot) {
+        const I4Mat m1{w, x, y, M, K};
+        const int st = launch_vq2_matvec_set_rot(1, &m1, &r.scale, &r.sign, r.bs, s);
+        if (st != kNotFused) return st;
+    }
     if (r.sign) {
         const int st = launch_biip_rotate(x, e.rotbuf, K, r.scale, r.sign, r.bs, s);
         if (st != kOk) return st;
@@ -458,6 +465,17 @@ int mv_rotated_set(const Engine &e, int n, const uint8_t *const *w, float *const
     if (static_cast<size_t>(n) * K > e.rotbuf_floats) return kNotFused;
     for (int j = 0; j < n; ++j)
         if (!r[j]->sign || r[j]->bs != r[0]->bs) return kNotFused;
+    if (e.pd == 4 && e.fused_rot) {  // VQ2: the rotations inside the set launch where it takes them
+        I4Mat mats[3];
+        const float *sc[3], *sg[3];
+        for (int j = 0; j < n; ++j) {
+            mats[j] = I4Mat{w[j], e.normed, y[j], m[j], K};
+            sc[j] = r[j]->scale;
+            sg[j] = r[j]->sign;
+        }
+        const int st = launch_vq2_matvec_set_rot(n, mats, sc, sg, r[0]->bs, s);
+        if (st != kNotFused) return st;
+    }
     float *xr[3];
     const float *sc[3], *sg[3];
     for (int j = 0; j < n; ++j) {
@@ -792,6 +810,7 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     }
     e->fused = e->pd == 3 && !any_rot && aligned && set_kernel_takes(c.hidden_size, e->gs) &&
                set_kernel_takes(c.intermediate_size, e->gs) && std::getenv("TQHIP_DECODE_UNFUSED") == nullptr;
+    e->fused_rot = e->pd == 4 && std::getenv("TQHIP_DECODE_UNFUSED") == nullptr;
     float *conv = reinterpret_cast<float *>(base + offs[15]);
     for (const F16Vec &f : f16s) {
         f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);

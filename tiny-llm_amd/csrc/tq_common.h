@@ -97,6 +97,10 @@ int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, i
 // n independent VQ2 matvecs (I4Mat: weights, activations, output, shape) in as few launches as
 // the one-wave-per-row kernel allows; each output has the bits launch_vq2_matvec gives it.
 int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream);
+// The same with each matrix's activations BiIP-rotated first (scale may be null, sign not), in
+// one launch; kNotFused when that launch does not take the set.
+int launch_vq2_matvec_set_rot(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
+                              int block_size, hipStream_t stream);
 int launch_i4_embed_rows(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
                          hipStream_t stream);
 int launch_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size,

@@ -29,6 +29,7 @@
 #include "tq_common.h"
 
 #include <algorithm>
+#include <cmath>
 
 namespace tqhip {
 namespace {
@@ -261,19 +262,27 @@ constexpr long long kDirectLookups = 4ll << 20;
 // (a layer's q/k/v, gate/up, or rotated copies of x): workgroups are numbered matrix after
 // matrix and a workgroup finds its matrix with scalar compares against the kernel argument.
 // A row's bits do not depend on the other matrices of the launch.
+// ROT: each matrix's activations are first BiIP-rotated into LDS by every workgroup, with the
+// operations of biip_rotate_kernel in the same order (division by the scale, the sign
+// product, the butterfly stages, the final 1 / sqrt(block) product), so the rows see exactly
+// the values a biip_rotate launch would have written, without that launch.
 struct Vq2Mat {
     const uint8_t *w;
     const float *x;
     float *y;
     int M, K;
-    int blk0;  // first workgroup of this matrix
+    int blk0;                  // first workgroup of this matrix
+    const float *scale, *sign;  // ROT: the matrix's rotation (scale may be null)
 };
 struct Vq2SetArgs {
     Vq2Mat m[kSetMaxMats];
     int n;
+    int lg_bs;       // ROT: log2 of the rotation block
+    float inv_sqrt;  // ROT: 1 / sqrt(block), as the host computes it for biip_rotate
 };
-template <bool XALIGN>
-__global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
+template <bool XALIGN, int WAVES, bool ROT>
+__global__ __launch_bounds__(64 * WAVES) void vq2_matvec_rows(Vq2SetArgs a) {
+    extern __shared__ __align__(16) float xs[];  // ROT: the matrix's rotated activations
     const int b = blockIdx.x;
     int j = 0;
 #pragma unroll
@@ -283,7 +292,25 @@ __global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
     for (int i = 1; i < kSetMaxMats; ++i)
         if (i == j) m = a.m[i];
     const int lane = threadIdx.x & 63;
-    const int row = (b - m.blk0) * 4 + (threadIdx.x >> 6);
+    if constexpr (ROT) {
+        constexpr int T = 64 * WAVES;
+        for (int i = threadIdx.x; i < m.K; i += T)
+            xs[i] = m.scale ? (m.x[i] / m.scale[i]) * m.sign[i] : m.x[i] * m.sign[i];
+        for (int lg = 0; lg < a.lg_bs; ++lg) {  // stage h = 2^lg: (u, c) at (jj, jj + h) -> (u + c, u - c)
+            __syncthreads();
+            const int h = 1 << lg;
+            for (int p = threadIdx.x; p < m.K / 2; p += T) {
+                const int jj = ((p >> lg) << (lg + 1)) + (p & (h - 1));
+                const float u = xs[jj], c = xs[jj + h];
+                xs[jj] = u + c;
+                xs[jj + h] = u - c;
+            }
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < m.K; i += T) xs[i] = xs[i] * a.inv_sqrt;
+        __syncthreads();
+    }
+    const int row = (b - m.blk0) * WAVES + (threadIdx.x >> 6);
     if (row >= m.M) return;
     const int nb = m.K / kVq2Dim;  // index bytes per row (a multiple of 4)
     const unsigned *qrow = reinterpret_cast<const unsigned *>(m.w + kVq2CodebookBytes + static_cast<size_t>(row) * nb);
@@ -294,8 +321,12 @@ __global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
         float4 xv[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-            const float *xp = m.x + 16 * d + 4 * jj;
-            xv[jj] = XALIGN ? *reinterpret_cast<const float4 *>(xp) : make_float4(xp[0], xp[1], xp[2], xp[3]);
+            if constexpr (ROT) {
+                xv[jj] = *reinterpret_cast<const float4 *>(xs + 16 * d + 4 * jj);
+            } else {
+                const float *xp = m.x + 16 * d + 4 * jj;
+                xv[jj] = XALIGN ? *reinterpret_cast<const float4 *>(xp) : make_float4(xp[0], xp[1], xp[2], xp[3]);
+            }
         }
         uint2 c[4];
 #pragma unroll
@@ -323,11 +354,15 @@ int launch_rows(Vq2SetArgs &a, int n, int blocks, bool xalign, hipStream_t strea
     for (int k = n; k < kSetMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
     a.n = n;
     if (xalign)
-        hipLaunchKernelGGL(vq2_matvec_rows<true>, dim3(blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((vq2_matvec_rows<true, 4, false>), dim3(blocks), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL(vq2_matvec_rows<false>, dim3(blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((vq2_matvec_rows<false, 4, false>), dim3(blocks), dim3(256), 0, stream, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
+
+// The rotating form: 8 rows per workgroup, so that each workgroup's rotation of x serves twice
+// the rows.
+constexpr int kRotWaves = 8;
 
 // ---- Dot-product table (large launches, index rows 16-byte aligned, in_dim <= 1024).
 // A lookup of the replica kernel costs four fp32 FMAs and a 16-byte LDS read per index, which
@@ -539,7 +574,7 @@ int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, i
     const bool aligned = (in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0;
     if (rows_kernel_takes(w, out_dim, in_dim)) {
         Vq2SetArgs a{};
-        a.m[0] = Vq2Mat{w, x, y, out_dim, in_dim, 0};
+        a.m[0] = Vq2Mat{w, x, y, out_dim, in_dim, 0, nullptr, nullptr};
         return launch_rows(a, 1, (out_dim + 3) / 4, (reinterpret_cast<uintptr_t>(x) & 15) == 0, stream);
     }
     if (in_dim % 64 == 0 && in_dim <= kTabMaxDim && (reinterpret_cast<uintptr_t>(w) % 16) == 0 &&
@@ -604,12 +639,46 @@ int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream) {
             lookups = 0;
             xalign = true;
         }
-        a.m[nb++] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks};
+        a.m[nb++] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, nullptr, nullptr};
         blocks += (mt.M + 3) / 4;
         lookups += lk;
         xalign = xalign && (reinterpret_cast<uintptr_t>(mt.x) & 15) == 0;
     }
     return nb > 0 ? launch_rows(a, nb, blocks, xalign, stream) : kOk;
+}
+
+// n VQ2 matvecs whose activations each go through their own BiIP rotation first (y_i = W_i
+// rotate_i(x_i), rotate as launch_biip_rotate with the block size shared by the launch), in ONE
+// launch of the one-wave-per-row kernel: each workgroup rotates its matrix's activations into
+// LDS. Each output has the bits of launch_biip_rotate followed by launch_vq2_matvec.
+// kNotFused (nothing launched) when a matrix is not one the kernel takes, the set needs more
+// than one launch, or the block does not divide a row length.
+int launch_vq2_matvec_set_rot(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
+                              int block_size, hipStream_t stream) {
+    if (n < 1 || n > kSetMaxMats || block_size < 1 || (block_size & (block_size - 1))) return kNotFused;
+    Vq2SetArgs a{};
+    int blocks = 0, kmax = 0;
+    long long lookups = 0;
+    for (int i = 0; i < n; ++i) {
+        const I4Mat &mt = mats[i];
+        if (mt.M < 1 || mt.K < kVq2Dim || mt.K % kVq2Dim || mt.K % block_size || !sign[i] ||
+            !rows_kernel_takes(mt.w, mt.M, mt.K))
+            return kNotFused;
+        a.m[i] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, scale[i], sign[i]};
+        blocks += (mt.M + kRotWaves - 1) / kRotWaves;
+        lookups += static_cast<long long>(mt.M) * (mt.K / kVq2Dim);
+        kmax = std::max(kmax, mt.K);
+    }
+    if (lookups > 2 * kDirectLookups || static_cast<size_t>(kmax) * 4 > 64 * 1024) return kNotFused;
+    for (int k = n; k < kSetMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
+    a.n = n;
+    int lg = 0;
+    while ((1 << lg) < block_size) ++lg;
+    a.lg_bs = lg;
+    a.inv_sqrt = 1.0f / std::sqrt(static_cast<float>(block_size));  // as launch_biip_rotate computes it
+    hipLaunchKernelGGL((vq2_matvec_rows<true, kRotWaves, true>), dim3(blocks), dim3(64 * kRotWaves),
+                       static_cast<size_t>(kmax) * 4, stream, a);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
 }  // namespace tqhip
