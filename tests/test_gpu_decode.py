@@ -68,15 +68,16 @@ def test_prompt_logits_match_oracle(gpu, tmp_path, case):
 
 
 @pytest.mark.parametrize("case", ["qwen25_0p5b_2layers", "qwen3_qknorm_hd128", "head_dim256",
-                                  "vq2_rotated_qwen25_shape"])
+                                  "vq2_qwen25_shape", "vq2_untied_gqa4", "vq2_rotated_qwen25_shape"])
 def test_fused_layers_match_unfused(gpu, tmp_path, monkeypatch, case):
     """i4 files at G 64 without rotations run fused layers: the residual adds, the RMSNorms and
     SwiGLU inside the next projection's set launch (its activation prologue). The same steps
     with TQHIP_DECODE_UNFUSED set (separate add_rmsnorm and swiglu launches) give the same tokens
     and logits within 1e-6: the operations are the same, only the double sum of squares of each
-    RMSNorm is added in another order. BiIP-rotated VQ2 files rotate the activations inside the
-    VQ2 matvec launches (each workgroup into LDS, the rotation kernel's operations in its order):
-    every step bit-identical to the separate rotation launches."""
+    RMSNorm is added in another order. VQ2 files run the same fused layers through the VQ2
+    kernel's staged activations (each workgroup builds them in LDS with the separate kernels'
+    operations in their order), which also apply the BiIP rotations of rotated files: every step
+    bit-identical to the separate add_rmsnorm, swiglu and rotation launches."""
     m, cfg, _ = open_model(gpu, tmp_path, case)
     fused = gpu.DecodeEngine(m, 32)
     monkeypatch.setenv("TQHIP_DECODE_UNFUSED", "1")

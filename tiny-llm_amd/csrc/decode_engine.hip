@@ -503,9 +503,20 @@ int forward(Engine &e) {
     }
     if (!e.fused) launch_add_rmsnorm(e.hidden, nullptr, nullptr, e.layers[0].in_ln, e.normed, H, eps, s);
     // A fused launch that does not apply returns kNotFused; the engine chose fused layers
-    // only where every one applies, so that is a launch failure here.
-    auto fused_set = [&](int n, const I4Mat *m, const SetPrologue &p) {
-        const int r = launch_i4_matvec_set_pro(n, m, e.gs, p, s);
+    // only where every one applies, so that is a launch failure here. i4: the set kernel's
+    // prologue; VQ2: the staged launch, which also applies the projections' rotations.
+    auto fused_set = [&](int n, const I4Mat *m, const Rot *const *rot, const SetPrologue &p) {
+        int r;
+        if (e.pd == 3) {
+            r = launch_i4_matvec_set_pro(n, m, e.gs, p, s);
+        } else {
+            const float *sc[3], *sg[3];
+            for (int j = 0; j < n; ++j) {
+                sc[j] = rot[j]->scale;
+                sg[j] = rot[j]->sign;
+            }
+            r = launch_vq2_matvec_set_pro(n, m, sc, rot[0]->sign ? sg : nullptr, rot[0]->bs, &p, s);
+        }
         return r == kNotFused ? static_cast<int>(kLaunchFailed) : r;
     };
     for (size_t li = 0; li < e.layers.size(); ++li) {
@@ -523,7 +534,7 @@ int forward(Engine &e) {
             const I4Mat m3[3] = {{L.q, xb, e.q, e.q_dim, H}, {L.k, xb, e.k, e.kv_dim, H}, {L.v, xb, e.v, e.kv_dim, H}};
             const SetPrologue p{2, nullptr, li == 0 ? nullptr : e.o, li == 0 ? nullptr : e.ffn, L.in_ln,
                                 li == 0 ? nullptr : cur, eps};
-            if ((st = fused_set(3, m3, p)) != kOk) return st;
+            if ((st = fused_set(3, m3, r3, p)) != kOk) return st;
         } else if (e.pd == 3 && !L.rotated) {
             if ((st = launch_i4_matvec_group(3, w3, y3, d3, e.normed, H, e.gs, s)) != kOk) return st;
         } else if (e.pd == 4 && !L.rotated) {
@@ -545,10 +556,11 @@ int forward(Engine &e) {
         if (e.fused) {
             // gate/up read rmsnorm(cur + o) * post_ln; down reads silu(gate) * up
             const I4Mat m2[2] = {{L.gate, cur, e.gate, I, H}, {L.up, cur, e.up, I, H}};
-            if ((st = fused_set(2, m2, SetPrologue{2, nullptr, e.o, nullptr, L.post_ln, nullptr, eps})) != kOk)
+            const Rot *r2[2] = {&L.rg, &L.ru}, *r1[1] = {&L.rd};
+            if ((st = fused_set(2, m2, r2, SetPrologue{2, nullptr, e.o, nullptr, L.post_ln, nullptr, eps})) != kOk)
                 return st;
             const I4Mat m1[1] = {{L.down, e.gate, e.ffn, H, I}};
-            if ((st = fused_set(1, m1, SetPrologue{1, e.up, nullptr, nullptr, nullptr, nullptr, eps})) != kOk)
+            if ((st = fused_set(1, m1, r1, SetPrologue{1, e.up, nullptr, nullptr, nullptr, nullptr, eps})) != kOk)
                 return st;
             continue;
         }
@@ -802,15 +814,23 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     e->hidden2 = reinterpret_cast<float *>(base + offs[17]);
     // fused layers where the set kernel takes every projection around a residual add, an
     // RMSNorm or SwiGLU: q/k/v and gate/up (rows of hidden_size) and down (intermediate_size)
-    bool any_rot = false, aligned = true;
+    bool any_rot = false, aligned = true, rot_sets = true;
     const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    // a fused VQ2 launch rotates all of its matrices or none, with one block size
+    const auto same = [](const Rot &a, const Rot &b) { return !a.sign == !b.sign && (!a.sign || a.bs == b.bs); };
     for (const Layer &L : e->layers) {
         any_rot = any_rot || L.rotated;
         aligned = aligned && al16(L.in_ln) && al16(L.post_ln);
+        rot_sets = rot_sets && same(L.rq, L.rk) && same(L.rq, L.rv) && same(L.rg, L.ru);
     }
-    e->fused = e->pd == 3 && !any_rot && aligned && set_kernel_takes(c.hidden_size, e->gs) &&
-               set_kernel_takes(c.intermediate_size, e->gs) && std::getenv("TQHIP_DECODE_UNFUSED") == nullptr;
-    e->fused_rot = e->pd == 4 && std::getenv("TQHIP_DECODE_UNFUSED") == nullptr;
+    const bool unfused = std::getenv("TQHIP_DECODE_UNFUSED") != nullptr;
+    const int hs = static_cast<int>(c.hidden_size), is = static_cast<int>(c.intermediate_size);
+    const int m3[3] = {e->q_dim, e->kv_dim, e->kv_dim}, m2[2] = {is, is}, m1[1] = {hs};
+    const bool vq2_sets = vq2_set_takes(3, m3, hs, 2) && vq2_set_takes(2, m2, hs, 2) && vq2_set_takes(1, m1, is, 1);
+    e->fused = !unfused && ((e->pd == 3 && !any_rot && aligned && set_kernel_takes(hs, e->gs) &&
+                             set_kernel_takes(is, e->gs)) ||
+                            (e->pd == 4 && rot_sets && vq2_sets));
+    e->fused_rot = e->pd == 4 && !unfused;
     float *conv = reinterpret_cast<float *>(base + offs[15]);
     for (const F16Vec &f : f16s) {
         f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);

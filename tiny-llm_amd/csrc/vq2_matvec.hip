@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace tqhip {
 namespace {
@@ -262,10 +263,15 @@ constexpr long long kDirectLookups = 4ll << 20;
 // (a layer's q/k/v, gate/up, or rotated copies of x): workgroups are numbered matrix after
 // matrix and a workgroup finds its matrix with scalar compares against the kernel argument.
 // A row's bits do not depend on the other matrices of the launch.
-// ROT: each matrix's activations are first BiIP-rotated into LDS by every workgroup, with the
-// operations of biip_rotate_kernel in the same order (division by the scale, the sign
-// product, the butterfly stages, the final 1 / sqrt(block) product), so the rows see exactly
-// the values a biip_rotate launch would have written, without that launch.
+// Staged activations (XM != 0 or ROT; 8-wave workgroups): every workgroup first builds its
+// matrix's activations in LDS, and the rows read them from there.
+// - XM, the prologue shared by the launch's matrices (one x): 1 x = silu(x) * x2 (swiglu's
+//   operations); 2 x = rmsnorm((x + d1) + d2) * nw (add_rmsnorm's: a double sum of squares,
+//   a float mean, 1 / sqrt(mean + eps), (h * scale) * w), workgroup 0 storing the sum to hout.
+// - ROT: then each matrix's own BiIP rotation, with biip_rotate_kernel's operations in its
+//   order (division by the scale, sign product, butterfly stages, the 1 / sqrt(block)
+//   product).
+// The rows see exactly the values the separate launches would have written.
 struct Vq2Mat {
     const uint8_t *w;
     const float *x;
@@ -277,40 +283,50 @@ struct Vq2Mat {
 struct Vq2SetArgs {
     Vq2Mat m[kSetMaxMats];
     int n;
-    int lg_bs;       // ROT: log2 of the rotation block
-    float inv_sqrt;  // ROT: 1 / sqrt(block), as the host computes it for biip_rotate
+    int lg_bs;        // ROT: log2 of the rotation block
+    float inv_sqrt;   // ROT: 1 / sqrt(block), as the host computes it for biip_rotate
+    SetPrologue pro;  // XM != 0
 };
-template <bool XALIGN, int WAVES, bool ROT>
-__global__ __launch_bounds__(64 * WAVES) void vq2_matvec_rows(Vq2SetArgs a) {
-    extern __shared__ __align__(16) float xs[];  // ROT: the matrix's rotated activations
-    const int b = blockIdx.x;
-    int j = 0;
+template <int WAVES>
+__device__ inline double vq2_block_sum(double v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __shared__ double red[WAVES];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double t = red[0];
 #pragma unroll
-    for (int i = 1; i < kSetMaxMats; ++i) j = (i < a.n && b >= a.m[i].blk0) ? i : j;
-    Vq2Mat m = a.m[0];
+    for (int w = 1; w < WAVES; ++w) t += red[w];
+    return t;
+}
+// One step of a row's dot product: the four entries of index dword q against 16 activations.
+__device__ inline float vq2_accum(float acc, const uint2 *c, const float4 *xv) {
 #pragma unroll
-    for (int i = 1; i < kSetMaxMats; ++i)
-        if (i == j) m = a.m[i];
-    const int lane = threadIdx.x & 63;
-    if constexpr (ROT) {
-        constexpr int T = 64 * WAVES;
-        for (int i = threadIdx.x; i < m.K; i += T)
-            xs[i] = m.scale ? (m.x[i] / m.scale[i]) * m.sign[i] : m.x[i] * m.sign[i];
-        for (int lg = 0; lg < a.lg_bs; ++lg) {  // stage h = 2^lg: (u, c) at (jj, jj + h) -> (u + c, u - c)
-            __syncthreads();
-            const int h = 1 << lg;
-            for (int p = threadIdx.x; p < m.K / 2; p += T) {
-                const int jj = ((p >> lg) << (lg + 1)) + (p & (h - 1));
-                const float u = xs[jj], c = xs[jj + h];
-                xs[jj] = u + c;
-                xs[jj + h] = u - c;
-            }
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < m.K; i += T) xs[i] = xs[i] * a.inv_sqrt;
-        __syncthreads();
+    for (int jj = 0; jj < 4; ++jj) {
+        acc = fmaf(half_bits(c[jj].x), xv[jj].x, acc);
+        acc = fmaf(half_bits(c[jj].x >> 16), xv[jj].y, acc);
+        acc = fmaf(half_bits(c[jj].y), xv[jj].z, acc);
+        acc = fmaf(half_bits(c[jj].y >> 16), xv[jj].w, acc);
     }
-    const int row = (b - m.blk0) * WAVES + (threadIdx.x >> 6);
+    return acc;
+}
+
+// The workgroup's matrix: scalar compares against the kernel argument, every field selected
+// in registers. (A helper that returned the record, or a reference into the argument, made the
+// compiler copy the argument to scratch memory.)
+#define TQ_VQ2_SELECT(a, m)                                                               \
+    Vq2Mat m = (a).m[0];                                                                  \
+    {                                                                                     \
+        int j_ = 0;                                                                       \
+        _Pragma("unroll") for (int i_ = 1; i_ < kSetMaxMats; ++i_) j_ =                   \
+            (i_ < (a).n && static_cast<int>(blockIdx.x) >= (a).m[i_].blk0) ? i_ : j_;      \
+        _Pragma("unroll") for (int i_ = 1; i_ < kSetMaxMats; ++i_) if (i_ == j_) m = (a).m[i_]; \
+    }
+
+template <bool XALIGN>
+__global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
+    TQ_VQ2_SELECT(a, m);
+    const int lane = threadIdx.x & 63;
+    const int row = (static_cast<int>(blockIdx.x) - m.blk0) * 4 + (threadIdx.x >> 6);
     if (row >= m.M) return;
     const int nb = m.K / kVq2Dim;  // index bytes per row (a multiple of 4)
     const unsigned *qrow = reinterpret_cast<const unsigned *>(m.w + kVq2CodebookBytes + static_cast<size_t>(row) * nb);
@@ -321,23 +337,119 @@ __global__ __launch_bounds__(64 * WAVES) void vq2_matvec_rows(Vq2SetArgs a) {
         float4 xv[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-            if constexpr (ROT) {
-                xv[jj] = *reinterpret_cast<const float4 *>(xs + 16 * d + 4 * jj);
-            } else {
-                const float *xp = m.x + 16 * d + 4 * jj;
-                xv[jj] = XALIGN ? *reinterpret_cast<const float4 *>(xp) : make_float4(xp[0], xp[1], xp[2], xp[3]);
-            }
+            const float *xp = m.x + 16 * d + 4 * jj;
+            xv[jj] = XALIGN ? *reinterpret_cast<const float4 *>(xp) : make_float4(xp[0], xp[1], xp[2], xp[3]);
         }
         uint2 c[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) c[jj] = cbg[(q >> (8 * jj)) & 0xFFu];
+        acc = vq2_accum(acc, c, xv);
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) m.y[row] = acc;
+}
+
+// The staged form: 8 rows per workgroup, so that each workgroup's prologue and rotation serve
+// twice the rows. PER: activations per thread (K <= 512 PER). Every load that does not wait for
+// the prologue goes out first: the prologue operands and rotation vectors of the thread's
+// activations, the row's first index dword and then its four codebook entries; the prologue
+// then runs in registers (one barrier for the RMSNorm's sum, one per butterfly stage).
+constexpr int kRotWaves = 8;
+template <int PER, int XM, bool ROT>
+__global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2SetArgs a) {
+    extern __shared__ __align__(16) float xs[];  // the matrix's activations
+    constexpr int T = 64 * kRotWaves;
+    TQ_VQ2_SELECT(a, m);
+    const float *const d1 = a.pro.d1, *const d2 = a.pro.d2, *const nw = a.pro.nw, *const x2 = a.pro.x2;
+    float *const hout = a.pro.hout;
+    const float eps = a.pro.eps;
+    const int t = threadIdx.x, lane = t & 63;
+    const int row = (static_cast<int>(blockIdx.x) - m.blk0) * kRotWaves + (t >> 6);
+    const bool live = row < m.M;  // no early return: every thread takes part in the barriers
+    const int nb = m.K / kVq2Dim;
+    const unsigned *qrow =
+        reinterpret_cast<const unsigned *>(m.w + kVq2CodebookBytes + static_cast<size_t>(live ? row : 0) * nb);
+    const uint2 *cbg = reinterpret_cast<const uint2 *>(m.w);
+    const bool first = live && 4 * lane < nb;
+    const unsigned q0 = first ? qrow[lane] : 0u;
+    float v[PER], p1[PER], p2[PER], p3[PER], sc[PER], sg[PER];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            acc = fmaf(half_bits(c[jj].x), xv[jj].x, acc);
-            acc = fmaf(half_bits(c[jj].x >> 16), xv[jj].y, acc);
-            acc = fmaf(half_bits(c[jj].y), xv[jj].z, acc);
-            acc = fmaf(half_bits(c[jj].y >> 16), xv[jj].w, acc);
+    for (int j = 0; j < PER; ++j) {
+        const int i = t + T * j;
+        const bool ok = i < m.K;
+        v[j] = ok ? m.x[i] : 0.f;
+        if constexpr (XM == 2) {
+            p1[j] = ok && d1 ? d1[i] : 0.f;
+            p2[j] = ok && d2 ? d2[i] : 0.f;
+            p3[j] = ok ? nw[i] : 0.f;
+        } else if constexpr (XM == 1) {
+            p1[j] = ok ? x2[i] : 0.f;
         }
+        if constexpr (ROT) {
+            sc[j] = ok && m.scale ? m.scale[i] : 1.f;
+            sg[j] = ok ? m.sign[i] : 0.f;
+        }
+    }
+    uint2 c0[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) c0[jj] = cbg[(q0 >> (8 * jj)) & 0xFFu];
+    if constexpr (XM == 2) {  // add_rmsnorm's operations
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            if (d1) v[j] = v[j] + p1[j];
+            if (d2) v[j] = v[j] + p2[j];
+            const int i = t + T * j;
+            if (hout && blockIdx.x == 0 && i < m.K) hout[i] = v[j];
+            ss += static_cast<double>(v[j]) * static_cast<double>(v[j]);
+        }
+        ss = vq2_block_sum<kRotWaves>(ss);
+        const float mean_sq = static_cast<float>(ss / m.K);
+        const float scale = 1.0f / sqrtf(mean_sq + eps);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) v[j] = (v[j] * scale) * p3[j];
+    } else if constexpr (XM == 1) {  // swiglu's operations
+#pragma unroll
+        for (int j = 0; j < PER; ++j) v[j] = (v[j] / (1.0f + expf(-v[j]))) * p1[j];
+    }
+    if constexpr (ROT) {  // biip_rotate_kernel's operations
+#pragma unroll
+        for (int j = 0; j < PER; ++j) v[j] = m.scale ? (v[j] / sc[j]) * sg[j] : v[j] * sg[j];
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+        if (t + T * j < m.K) xs[t + T * j] = v[j];
+    if constexpr (ROT) {
+        for (int lg = 0; lg < a.lg_bs; ++lg) {  // stage h = 2^lg: (u, c) at (jj, jj + h) -> (u + c, u - c)
+            __syncthreads();
+            const int h = 1 << lg;
+            for (int p = t; p < m.K / 2; p += T) {
+                const int jj = ((p >> lg) << (lg + 1)) + (p & (h - 1));
+                const float u = xs[jj], c = xs[jj + h];
+                xs[jj] = u + c;
+                xs[jj + h] = u - c;
+            }
+        }
+        __syncthreads();
+        for (int i = t; i < m.K; i += T) xs[i] = xs[i] * a.inv_sqrt;
+    }
+    __syncthreads();
+    if (!live) return;
+    float acc = 0.f;
+    for (int d = lane; 4 * d < nb; d += 64) {
+        uint2 c[4];
+        if (d == lane) {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) c[jj] = c0[jj];
+        } else {
+            const unsigned q = qrow[d];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) c[jj] = cbg[(q >> (8 * jj)) & 0xFFu];
+        }
+        float4 xv[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) xv[jj] = *reinterpret_cast<const float4 *>(xs + 16 * d + 4 * jj);
+        acc = vq2_accum(acc, c, xv);
     }
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
     if (lane == 0) m.y[row] = acc;
@@ -354,15 +466,12 @@ int launch_rows(Vq2SetArgs &a, int n, int blocks, bool xalign, hipStream_t strea
     for (int k = n; k < kSetMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
     a.n = n;
     if (xalign)
-        hipLaunchKernelGGL((vq2_matvec_rows<true, 4, false>), dim3(blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(vq2_matvec_rows<true>, dim3(blocks), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL((vq2_matvec_rows<false, 4, false>), dim3(blocks), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(vq2_matvec_rows<false>, dim3(blocks), dim3(256), 0, stream, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
-// The rotating form: 8 rows per workgroup, so that each workgroup's rotation of x serves twice
-// the rows.
-constexpr int kRotWaves = 8;
 
 // ---- Dot-product table (large launches, index rows 16-byte aligned, in_dim <= 1024).
 // A lookup of the replica kernel costs four fp32 FMAs and a 16-byte LDS read per index, which
@@ -647,38 +756,86 @@ int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream) {
     return nb > 0 ? launch_rows(a, nb, blocks, xalign, stream) : kOk;
 }
 
-// n VQ2 matvecs whose activations each go through their own BiIP rotation first (y_i = W_i
-// rotate_i(x_i), rotate as launch_biip_rotate with the block size shared by the launch), in ONE
-// launch of the one-wave-per-row kernel: each workgroup rotates its matrix's activations into
-// LDS. Each output has the bits of launch_biip_rotate followed by launch_vq2_matvec.
-// kNotFused (nothing launched) when a matrix is not one the kernel takes, the set needs more
-// than one launch, or the block does not divide a row length.
-int launch_vq2_matvec_set_rot(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
-                              int block_size, hipStream_t stream) {
-    if (n < 1 || n > kSetMaxMats || block_size < 1 || (block_size & (block_size - 1))) return kNotFused;
+// n VQ2 matvecs in ONE launch of the one-wave-per-row kernel with staged activations: the
+// prologue pro (kind 1 or 2, shared by the matrices, which then share x and K; null for none),
+// then, where sign is given, each matrix's own BiIP rotation (rotate as launch_biip_rotate, the
+// block size shared by the launch). Each output has the bits of the separate swiglu /
+// add_rmsnorm, biip_rotate and launch_vq2_matvec launches. kNotFused (nothing launched) when a
+// matrix is not one the kernel takes, the set needs more than one launch, the block does not
+// divide a row length, or there is nothing to stage.
+int launch_vq2_matvec_set_pro(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
+                              int block_size, const SetPrologue *pro, hipStream_t stream) {
+    const int xm = pro ? pro->kind : 0;
+    if (n < 1 || n > kSetMaxMats || xm < 0 || xm > 2 || (!sign && !xm)) return kNotFused;
+    if (xm == 1 && !pro->x2) return kNotFused;
+    if (xm == 2 && !pro->nw) return kNotFused;
+    if (sign && (block_size < 1 || (block_size & (block_size - 1)))) return kNotFused;
     Vq2SetArgs a{};
     int blocks = 0, kmax = 0;
     long long lookups = 0;
     for (int i = 0; i < n; ++i) {
         const I4Mat &mt = mats[i];
-        if (mt.M < 1 || mt.K < kVq2Dim || mt.K % kVq2Dim || mt.K % block_size || !sign[i] ||
-            !rows_kernel_takes(mt.w, mt.M, mt.K))
-            return kNotFused;
-        a.m[i] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, scale[i], sign[i]};
+        if (mt.M < 1 || mt.K < kVq2Dim || mt.K % kVq2Dim || !rows_kernel_takes(mt.w, mt.M, mt.K)) return kNotFused;
+        if (sign && (!sign[i] || mt.K % block_size)) return kNotFused;
+        if (xm && (mt.x != mats[0].x || mt.K != mats[0].K)) return kNotFused;
+        a.m[i] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, sign ? scale[i] : nullptr, sign ? sign[i] : nullptr};
         blocks += (mt.M + kRotWaves - 1) / kRotWaves;
         lookups += static_cast<long long>(mt.M) * (mt.K / kVq2Dim);
         kmax = std::max(kmax, mt.K);
     }
-    if (lookups > 2 * kDirectLookups || static_cast<size_t>(kmax) * 4 > 64 * 1024) return kNotFused;
+    // the staged kernel holds up to 20 activations per thread (10 with the RMSNorm's operands)
+    if (lookups > 2 * kDirectLookups || kmax > (xm == 2 ? 5120 : 10240)) return kNotFused;
     for (int k = n; k < kSetMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
     a.n = n;
-    int lg = 0;
-    while ((1 << lg) < block_size) ++lg;
-    a.lg_bs = lg;
-    a.inv_sqrt = 1.0f / std::sqrt(static_cast<float>(block_size));  // as launch_biip_rotate computes it
-    hipLaunchKernelGGL((vq2_matvec_rows<true, kRotWaves, true>), dim3(blocks), dim3(64 * kRotWaves),
-                       static_cast<size_t>(kmax) * 4, stream, a);
+    if (pro) a.pro = *pro;
+    if (sign) {
+        int lg = 0;
+        while ((1 << lg) < block_size) ++lg;
+        a.lg_bs = lg;
+        a.inv_sqrt = 1.0f / std::sqrt(static_cast<float>(block_size));  // as launch_biip_rotate computes it
+    }
+    const dim3 grid(blocks), block(64 * kRotWaves);
+    const size_t lds = static_cast<size_t>(kmax) * 4;
+    const int per = kmax <= 1024 ? 2 : kmax <= 2048 ? 4 : kmax <= 5120 ? 10 : 20;
+    auto go = [&](auto perc) {  // the instance of (xm, rotation); xm was checked above
+        constexpr int P = decltype(perc)::value;
+        if (xm == 0)
+            hipLaunchKernelGGL((vq2_matvec_staged<P, 0, true>), grid, block, lds, stream, a);
+        else if (xm == 1 && sign)
+            hipLaunchKernelGGL((vq2_matvec_staged<P, 1, true>), grid, block, lds, stream, a);
+        else if (xm == 1)
+            hipLaunchKernelGGL((vq2_matvec_staged<P, 1, false>), grid, block, lds, stream, a);
+        else if (sign)
+            hipLaunchKernelGGL((vq2_matvec_staged<P, 2, true>), grid, block, lds, stream, a);
+        else
+            hipLaunchKernelGGL((vq2_matvec_staged<P, 2, false>), grid, block, lds, stream, a);
+    };
+    if (per == 2)
+        go(std::integral_constant<int, 2>{});
+    else if (per == 4)
+        go(std::integral_constant<int, 4>{});
+    else if (per == 10)
+        go(std::integral_constant<int, 10>{});
+    else
+        go(std::integral_constant<int, 20>{});
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+int launch_vq2_matvec_set_rot(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
+                              int block_size, hipStream_t stream) {
+    if (!sign) return kNotFused;
+    return launch_vq2_matvec_set_pro(n, mats, scale, sign, block_size, nullptr, stream);
+}
+
+// The staged launch would take these shapes: a set of matrices of row length K with the given
+// rows, with prologue kind xm (the engine decides its fused layers with it).
+bool vq2_set_takes(int n, const int *M, int K, int xm) {
+    long long lookups = 0;
+    for (int i = 0; i < n; ++i) {
+        if (M[i] < 1 || K % 16 || static_cast<long long>(M[i]) * (K / kVq2Dim) > kDirectLookups) return false;
+        lookups += static_cast<long long>(M[i]) * (K / kVq2Dim);
+    }
+    return n >= 1 && n <= kSetMaxMats && lookups <= 2 * kDirectLookups && K <= (xm == 2 ? 5120 : 10240);
 }
 
 }  // namespace tqhip
