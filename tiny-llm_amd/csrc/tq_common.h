@@ -101,9 +101,9 @@ int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream);
 // one launch; kNotFused when that launch does not take the set.
 int launch_vq2_matvec_set_rot(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
                               int block_size, hipStream_t stream);
-// One launch with the activations staged per workgroup: the prologue pro (SetPrologue kind 1 or
-// 2, the matrices sharing x; null for none), then, with sign given, each matrix's BiIP rotation;
-// kNotFused when that launch does not take the set. vq2_set_takes: whether it would take n
+// One launch with the activations staged per workgroup, for up to 3 matrices: the prologue pro
+// (SetPrologue kind 1 or 2, the matrices sharing x; null for none), then, with sign given, each
+// matrix's BiIP rotation; kNotFused when that launch does not take the set. vq2_set_takes: whether it would take n
 // matrices of these rows and row length K (4-byte aligned weights).
 int launch_vq2_matvec_set_pro(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
                               int block_size, const SetPrologue *pro, hipStream_t stream);

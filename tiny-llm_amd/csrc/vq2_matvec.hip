@@ -283,6 +283,13 @@ struct Vq2Mat {
 struct Vq2SetArgs {
     Vq2Mat m[kSetMaxMats];
     int n;
+};
+// The staged launches carry at most three records (a layer's q/k/v at most): five fewer
+// records in the kernel argument measured 0.17 us less per launch in the decode engine.
+constexpr int kStagedMaxMats = 3;
+struct Vq2StagedArgs {
+    Vq2Mat m[kStagedMaxMats];
+    int n;
     int lg_bs;        // ROT: log2 of the rotation block
     float inv_sqrt;   // ROT: 1 / sqrt(block), as the host computes it for biip_rotate
     SetPrologue pro;  // XM != 0
@@ -313,13 +320,13 @@ __device__ inline float vq2_accum(float acc, const uint2 *c, const float4 *xv) {
 // The workgroup's matrix: scalar compares against the kernel argument, every field selected
 // in registers. (A helper that returned the record, or a reference into the argument, made the
 // compiler copy the argument to scratch memory.)
-#define TQ_VQ2_SELECT(a, m)                                                               \
+#define TQ_VQ2_SELECT(a, m, cap)                                                          \
     Vq2Mat m = (a).m[0];                                                                  \
     {                                                                                     \
         int j_ = 0;                                                                       \
-        _Pragma("unroll") for (int i_ = 1; i_ < kSetMaxMats; ++i_) j_ =                   \
+        _Pragma("unroll") for (int i_ = 1; i_ < (cap); ++i_) j_ =                         \
             (i_ < (a).n && static_cast<int>(blockIdx.x) >= (a).m[i_].blk0) ? i_ : j_;      \
-        _Pragma("unroll") for (int i_ = 1; i_ < kSetMaxMats; ++i_) if (i_ == j_) m = (a).m[i_]; \
+        _Pragma("unroll") for (int i_ = 1; i_ < (cap); ++i_) if (i_ == j_) m = (a).m[i_]; \
     }
 
 // Row `row` of one matrix, x from global memory, its 64 lane sums added over the wave.
@@ -359,7 +366,7 @@ __global__ __launch_bounds__(256) void vq2_matvec_row1(const uint8_t *__restrict
 
 template <bool XALIGN>
 __global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
-    TQ_VQ2_SELECT(a, m);
+    TQ_VQ2_SELECT(a, m, kSetMaxMats);
     const int row = (static_cast<int>(blockIdx.x) - m.blk0) * 4 + (threadIdx.x >> 6);
     if (row >= m.M) return;
     const float acc = vq2_row<XALIGN>(m.w, m.x, m.K, row, threadIdx.x & 63);
@@ -373,10 +380,10 @@ __global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
 // then runs in registers (one barrier for the RMSNorm's sum, one per butterfly stage).
 constexpr int kRotWaves = 8;
 template <int PER, int XM, bool ROT>
-__global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2SetArgs a) {
+__global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2StagedArgs a) {
     extern __shared__ __align__(16) float xs[];  // the matrix's activations
     constexpr int T = 64 * kRotWaves;
-    TQ_VQ2_SELECT(a, m);
+    TQ_VQ2_SELECT(a, m, kStagedMaxMats);
     const float *const d1 = a.pro.d1, *const d2 = a.pro.d2, *const nw = a.pro.nw, *const x2 = a.pro.x2;
     float *const hout = a.pro.hout;
     const float eps = a.pro.eps;
@@ -791,11 +798,11 @@ int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream) {
 int launch_vq2_matvec_set_pro(int n, const I4Mat *mats, const float *const *scale, const float *const *sign,
                               int block_size, const SetPrologue *pro, hipStream_t stream) {
     const int xm = pro ? pro->kind : 0;
-    if (n < 1 || n > kSetMaxMats || xm < 0 || xm > 2 || (!sign && !xm)) return kNotFused;
+    if (n < 1 || n > kStagedMaxMats || xm < 0 || xm > 2 || (!sign && !xm)) return kNotFused;
     if (xm == 1 && !pro->x2) return kNotFused;
     if (xm == 2 && !pro->nw) return kNotFused;
     if (sign && (block_size < 1 || (block_size & (block_size - 1)))) return kNotFused;
-    Vq2SetArgs a{};
+    Vq2StagedArgs a{};
     int blocks = 0, kmax = 0;
     long long lookups = 0;
     for (int i = 0; i < n; ++i) {
@@ -810,7 +817,7 @@ int launch_vq2_matvec_set_pro(int n, const I4Mat *mats, const float *const *scal
     }
     // the staged kernel holds up to 20 activations per thread (10 with the RMSNorm's operands)
     if (lookups > 2 * kDirectLookups || kmax > (xm == 2 ? 5120 : 10240)) return kNotFused;
-    for (int k = n; k < kSetMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
+    for (int k = n; k < kStagedMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
     a.n = n;
     if (pro) a.pro = *pro;
     if (sign) {
@@ -860,7 +867,7 @@ bool vq2_set_takes(int n, const int *M, int K, int xm) {
         if (M[i] < 1 || K % 16 || static_cast<long long>(M[i]) * (K / kVq2Dim) > kDirectLookups) return false;
         lookups += static_cast<long long>(M[i]) * (K / kVq2Dim);
     }
-    return n >= 1 && n <= kSetMaxMats && lookups <= 2 * kDirectLookups && K <= (xm == 2 ? 5120 : 10240);
+    return n >= 1 && n <= kStagedMaxMats && lookups <= 2 * kDirectLookups && K <= (xm == 2 ? 5120 : 10240);
 }
 
 }  // namespace tqhip
