@@ -47,8 +47,13 @@ struct SetMat {
     int blk0;   // first workgroup of this matrix
     int shape;  // 0: one row per half-wave (K <= 1024); s = 1..5: one row per wave over s slots
 };
+// C: the records the kernel argument holds. Launches of up to kSetSmallMats matrices (a decode
+// engine's launches, single and fused matvecs) carry that many; five fewer records in the
+// argument measured 0.17 us less per launch (VQ2 staged launches, decode engine).
+constexpr int kSetSmallMats = 3;
+template <int C>
 struct SetArgs {
-    SetMat m[kSetMaxMats];
+    SetMat m[C];
     int n;
     SetPrologue pro;  // XM != 0 instances only
 };
@@ -307,16 +312,16 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
 // SMAX: the largest shape in the launch (the register budget follows it); R: rows per
 // half-wave for the short rows; RL: rows per wave for the long rows (two rows share the
 // activation operands each wave reads from LDS and halve the workgroups that convert x).
-template <int SMAX, int R, int RL, int XM = 0>
-__global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs a) {
+template <int SMAX, int R, int RL, int XM, int C>
+__global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs<C> a) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int b = blockIdx.x;
     int j = 0;
 #pragma unroll
-    for (int i = 1; i < kSetMaxMats; ++i) j = (i < a.n && b >= a.m[i].blk0) ? i : j;
+    for (int i = 1; i < C; ++i) j = (i < a.n && b >= a.m[i].blk0) ? i : j;
     SetMat m = a.m[0];
 #pragma unroll
-    for (int i = 1; i < kSetMaxMats; ++i)
+    for (int i = 1; i < C; ++i)
         if (i == j) m = a.m[i];
     const int blk = b - m.blk0;
     if (m.shape == 0) {
@@ -343,27 +348,27 @@ int set_shape(const I4Mat &mt, int group_size) {
     return mt.K <= 1024 ? 0 : (mt.K + 64 * 32 - 1) / (64 * 32);
 }
 
-template <int R, int RL, int XM>
-void launch_r(int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream, const SetArgs &a) {
+template <int R, int RL, int XM, int C>
+void launch_r(int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream, const SetArgs<C> &a) {
     switch (smax) {
-        case 0: hipLaunchKernelGGL((i4_matvec_set<0, R, 1, XM>), grid, block, lds, stream, a); break;
-        case 1: hipLaunchKernelGGL((i4_matvec_set<1, R, RL, XM>), grid, block, lds, stream, a); break;
-        case 2: hipLaunchKernelGGL((i4_matvec_set<2, R, RL, XM>), grid, block, lds, stream, a); break;
-        case 3: hipLaunchKernelGGL((i4_matvec_set<3, R, RL, XM>), grid, block, lds, stream, a); break;
-        case 4: hipLaunchKernelGGL((i4_matvec_set<4, R, RL, XM>), grid, block, lds, stream, a); break;
-        default: hipLaunchKernelGGL((i4_matvec_set<5, R, RL, XM>), grid, block, lds, stream, a); break;
+        case 0: hipLaunchKernelGGL((i4_matvec_set<0, R, 1, XM, C>), grid, block, lds, stream, a); break;
+        case 1: hipLaunchKernelGGL((i4_matvec_set<1, R, RL, XM, C>), grid, block, lds, stream, a); break;
+        case 2: hipLaunchKernelGGL((i4_matvec_set<2, R, RL, XM, C>), grid, block, lds, stream, a); break;
+        case 3: hipLaunchKernelGGL((i4_matvec_set<3, R, RL, XM, C>), grid, block, lds, stream, a); break;
+        case 4: hipLaunchKernelGGL((i4_matvec_set<4, R, RL, XM, C>), grid, block, lds, stream, a); break;
+        default: hipLaunchKernelGGL((i4_matvec_set<5, R, RL, XM, C>), grid, block, lds, stream, a); break;
     }
 }
 
-template <int XM>
+template <int XM, int C>
 void launch_rr(int R, int RL, int smax, const dim3 &grid, const dim3 &block, size_t lds, hipStream_t stream,
-               const SetArgs &a) {
+               const SetArgs<C> &a) {
     if (R == 2)
-        RL == 2 ? launch_r<2, 2, XM>(smax, grid, block, lds, stream, a)
-                : launch_r<2, 1, XM>(smax, grid, block, lds, stream, a);
+        RL == 2 ? launch_r<2, 2, XM, C>(smax, grid, block, lds, stream, a)
+                : launch_r<2, 1, XM, C>(smax, grid, block, lds, stream, a);
     else
-        RL == 2 ? launch_r<1, 2, XM>(smax, grid, block, lds, stream, a)
-                : launch_r<1, 1, XM>(smax, grid, block, lds, stream, a);
+        RL == 2 ? launch_r<1, 2, XM, C>(smax, grid, block, lds, stream, a)
+                : launch_r<1, 1, XM, C>(smax, grid, block, lds, stream, a);
 }
 
 // Two long rows per wave when every long-row matrix of the launch has at least this many rows.
@@ -382,7 +387,7 @@ int long_rows_per_wave(const I4Mat *mats, const int *shape, int n) {
 }
 
 int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream, const SetPrologue *pro = nullptr) {
-    SetArgs a{};
+    SetArgs<kSetMaxMats> a{};
     if (pro) a.pro = *pro;
     int order[kSetMaxMats];
     for (int i = 0; i < n; ++i) order[i] = i;
@@ -410,12 +415,21 @@ int launch_set(const I4Mat *mats, const int *shape, int n, hipStream_t stream, c
     const size_t lds = static_cast<size_t>(umax) * (4 * kBlockBytes + 8);  // the widest row's operands
     const dim3 grid(blocks), block(kSetThreads);
     const int xm = pro ? pro->kind : 0;
-    if (xm == 1)
-        launch_rr<1>(R, RL, smax, grid, block, lds, stream, a);
-    else if (xm == 2)
-        launch_rr<2>(R, RL, smax, grid, block, lds, stream, a);
-    else
-        launch_rr<0>(R, RL, smax, grid, block, lds, stream, a);
+    if (n <= kSetSmallMats) {  // the prologue launches always (launch_i4_matvec_set_pro)
+        SetArgs<kSetSmallMats> s3{};
+        for (int k = 0; k < kSetSmallMats; ++k) s3.m[k] = a.m[k];
+        s3.n = a.n;
+        s3.pro = a.pro;
+        if (xm == 1)
+            launch_rr<1, kSetSmallMats>(R, RL, smax, grid, block, lds, stream, s3);
+        else if (xm == 2)
+            launch_rr<2, kSetSmallMats>(R, RL, smax, grid, block, lds, stream, s3);
+        else
+            launch_rr<0, kSetSmallMats>(R, RL, smax, grid, block, lds, stream, s3);
+    } else {
+        if (xm) return kNotFused;  // prologue launches hold at most kSetSmallMats matrices
+        launch_rr<0, kSetMaxMats>(R, RL, smax, grid, block, lds, stream, a);
+    }
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -450,7 +464,7 @@ bool set_kernel_takes(int K, int group_size) {
 }
 
 int launch_i4_matvec_set_pro(int n, const I4Mat *mats, int group_size, const SetPrologue &pro, hipStream_t stream) {
-    if (n < 1 || n > kSetMaxMats || pro.kind < 1 || pro.kind > 2) return kNotFused;
+    if (n < 1 || n > kSetSmallMats || pro.kind < 1 || pro.kind > 2) return kNotFused;
     const auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (!al(pro.x2) || !al(pro.d1) || !al(pro.d2) || !al(pro.nw) || !al(pro.hout) ||
         (pro.kind == 1 && !pro.x2) || (pro.kind == 2 && !pro.nw))

@@ -88,8 +88,8 @@ struct SetPrologue {
     float *hout;
     float eps;
 };
-// The set kernel with a prologue for n matrices sharing x (mats[i].x equal, 16-byte aligned like
-// x2, d1, d2, nw and hout); kNotFused (nothing launched) when the set kernel does not take them.
+// The set kernel with a prologue for up to 3 matrices sharing x (mats[i].x equal, 16-byte aligned
+// like x2, d1, d2, nw and hout); kNotFused (nothing launched) when the set kernel does not take them.
 int launch_i4_matvec_set_pro(int n, const I4Mat *mats, int group_size, const SetPrologue &pro, hipStream_t stream);
 // Whether the set kernel takes rows of K elements at this group size (with x 16-byte aligned).
 bool set_kernel_takes(int K, int group_size);
