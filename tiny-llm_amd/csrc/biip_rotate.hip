@@ -9,7 +9,7 @@
 // 1 / sqrt(block_size). It runs ahead of every matvec of a rotated model.
 //
 // One workgroup takes a chunk of whole blocks (up to 2048 elements) into LDS,
-// runs the butterfly stages there with one barrier per stage, and writes the
+// runs the butterfly stages there, two per barrier, and writes the
 // scaled result. Every element goes through the same fp32 operations in the
 // same order as the scalar reference (one correctly rounded division, the
 // sign product, the adds and subtracts of each stage, the final product), so
@@ -60,7 +60,23 @@ __device__ void rotate_chunk(float *v, const float *x, float *y, int dim, const 
         const int j = base + i;
         v[i] = scale ? (x[j] / scale[j]) * sign[j] : x[j] * sign[j];
     }
-    for (int lg = 0; lg < lg_bs; ++lg) {  // stage h = 2^lg
+    // stages h = 2^lg and 2h together on the four elements j + {0, h, 2h, 3h} of a block: each
+    // element gets the adds and subtracts of the two stages in their order, one barrier for both
+    int lg = 0;
+    for (; lg + 1 < lg_bs; lg += 2) {
+        __syncthreads();
+        const int h = 1 << lg;
+        for (int p = threadIdx.x; p < n / 4; p += kBiipThreads) {
+            const int j = ((p >> lg) << (lg + 2)) + (p & (h - 1));
+            const float x0 = v[j], x1 = v[j + h], x2 = v[j + 2 * h], x3 = v[j + 3 * h];
+            const float y0 = x0 + x1, y1 = x0 - x1, y2 = x2 + x3, y3 = x2 - x3;
+            v[j] = y0 + y2;
+            v[j + h] = y1 + y3;
+            v[j + 2 * h] = y0 - y2;
+            v[j + 3 * h] = y1 - y3;
+        }
+    }
+    if (lg < lg_bs) {  // a last single stage h = 2^lg
         __syncthreads();
         const int h = 1 << lg;
         for (int p = threadIdx.x; p < n / 2; p += kBiipThreads) {

@@ -444,7 +444,23 @@ __global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2StagedArg
     for (int j = 0; j < PER; ++j)
         if (t + T * j < m.K) xs[t + T * j] = v[j];
     if constexpr (ROT) {
-        for (int lg = 0; lg < a.lg_bs; ++lg) {  // stage h = 2^lg: (u, c) at (jj, jj + h) -> (u + c, u - c)
+        // stages h = 2^lg and 2h together on the four elements jj + {0, h, 2h, 3h}: each element
+        // gets the adds and subtracts of the two radix-2 stages in their order, with one barrier
+        int lg = 0;
+        for (; lg + 1 < a.lg_bs; lg += 2) {
+            __syncthreads();
+            const int h = 1 << lg;
+            for (int p = t; p < m.K / 4; p += T) {
+                const int jj = ((p >> lg) << (lg + 2)) + (p & (h - 1));
+                const float x0 = xs[jj], x1 = xs[jj + h], x2 = xs[jj + 2 * h], x3 = xs[jj + 3 * h];
+                const float y0 = x0 + x1, y1 = x0 - x1, y2 = x2 + x3, y3 = x2 - x3;
+                xs[jj] = y0 + y2;
+                xs[jj + h] = y1 + y3;
+                xs[jj + 2 * h] = y0 - y2;
+                xs[jj + 3 * h] = y1 - y3;
+            }
+        }
+        if (lg < a.lg_bs) {  // a last single stage: (u, c) at (jj, jj + h) -> (u + c, u - c)
             __syncthreads();
             const int h = 1 << lg;
             for (int p = t; p < m.K / 2; p += T) {
