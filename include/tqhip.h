@@ -222,6 +222,7 @@ typedef struct tqhip_op {
 #define TQHIP_OP_I4_QKV 5
 #define TQHIP_OP_BIIP_ROTATE 6   /* x -> y, in_dim = dim, group_size = block_size, w2 = scale (or NULL), w3 = sign */
 #define TQHIP_OP_I4_SET 7        /* w = const tqhip_i4_mat * (n matrices, read when the op runs or is captured), group_size */
+#define TQHIP_OP_VQ2_SET 8       /* w = const tqhip_i4_mat * (n VQ2 matrices, read when the op runs or is captured) */
 int tqhip_run_ops(const tqhip_op *ops, int n_ops, int repeats, void *stream);
 /* As tqhip_run_ops, with a HIP event pair around every call; op_ms[i] gets the
  * mean event-to-event time of call i over the repeats (kernel duration as the

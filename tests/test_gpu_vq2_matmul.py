@@ -249,3 +249,41 @@ def test_vq2_set_errors(gpu):
     assert lib.tqhip_matvec_vq2_set_dev(gpu.ctypes.addressof(arr), 1, None) == gpu.EBADSHAPE
     arr = gpu.i4_set([(w, x, y, 0, 64)])
     assert lib.tqhip_matvec_vq2_set_dev(gpu.ctypes.addressof(arr), 1, None) == gpu.EBADSHAPE
+
+
+def test_vq2_set_op_in_a_captured_graph(gpu, orc):
+    """TQHIP_OP_VQ2_SET in an op list: eager run and graph replays agree bit for bit with new
+    activations written before each replay, and with the single-matrix launches."""
+    spec = [(896, 896, "a"), (128, 896, "a"), (128, 896, "a"), (4864, 896, "m"), (4864, 896, "m")]
+    xs, mats = {}, []
+    for i, (M, K, key) in enumerate(spec):
+        if key not in xs:
+            xs[key] = (np.zeros(K, np.float32), gpu.DeviceBuffer(4 * K), K)
+        w = gpu.synth_vq2(M, K, seed=200 + i)
+        mats.append((M, K, w, xs[key], gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer(4 * M)))
+    arr = gpu.i4_set([(dw, x[1], dy, M, K) for M, K, _, x, dw, dy in mats])
+    ops = [gpu.vq2_set_op(arr)]
+    stream = gpu.Stream()
+    graph = gpu.OpsGraph(ops, stream)
+    try:
+        for rep in range(3):
+            for i, (xv, xd, K) in enumerate(xs.values()):
+                xv[:] = gpu.synth_normal(K, seed=210 + 10 * rep + i)
+                xd.upload(xv)
+            gpu.run_ops(ops, 1, stream)
+            stream.synchronize()
+            want = [dy.download(np.float32, M) for M, _, _, _, _, dy in mats]
+            for M, _, _, _, _, dy in mats:
+                gpu.lib().tqhip_memset(dy.ptr, 0xFF, 4 * M)
+            graph.launch()
+            stream.synchronize()
+            for i, ((M, K, w, x, dw, dy), wv) in enumerate(zip(mats, want)):
+                assert np.array_equal(dy.download(np.float32, M).view(np.uint32), wv.view(np.uint32)), (rep, i)
+                alone = gpu.DeviceBuffer(4 * M)
+                assert gpu.lib().tqhip_matvec_vq2_dev(dw.ptr, x[1].ptr, alone.ptr, M, K, None) == 0
+                gpu.synchronize()
+                assert np.array_equal(alone.download(np.float32, M).view(np.uint32), wv.view(np.uint32)), (rep, i)
+        for (M, K, w, x, _, _), wv in zip(mats, want):
+            assert_close(wv, orc.matvec_vq2(w, x[0], M, K, threads=8), 1e-5, f"{M}x{K}")
+    finally:
+        graph.close()

@@ -23,7 +23,7 @@ LIB_PATH = os.path.join(HERE, "libtqhip.so")
 
 OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH, EFILE, EHIP, ENOSCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
 NOALLOC_SCRATCH_BYTES = 16 << 20  # TQHIP_NOALLOC_SCRATCH_BYTES
-OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV, OP_BIIP_ROTATE, OP_I4_SET = 1, 2, 3, 4, 5, 6, 7
+OP_I4_MATVEC, OP_VQ2_MATVEC, OP_I4_MATMUL, OP_I4_PAIR, OP_I4_QKV, OP_BIIP_ROTATE, OP_I4_SET, OP_VQ2_SET = 1, 2, 3, 4, 5, 6, 7, 8
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -52,6 +52,11 @@ def i4_set(mats: list) -> "ctypes.Array":
 def set_op(mats: "ctypes.Array", group_size: int) -> Op:
     """A TQHIP_OP_I4_SET op over a tqhip_i4_mat array; keep the array alive while the op is used."""
     return Op(OP_I4_SET, ctypes.addressof(mats), None, None, 0, 0, len(mats), group_size)
+
+
+def vq2_set_op(mats: "ctypes.Array") -> Op:
+    """A TQHIP_OP_VQ2_SET op over a tqhip_i4_mat array of VQ2 matrices; keep the array alive."""
+    return Op(OP_VQ2_SET, ctypes.addressof(mats), None, None, 0, 0, len(mats), 0)
 
 
 class TensorInfo(ctypes.Structure):

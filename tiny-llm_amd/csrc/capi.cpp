@@ -387,6 +387,7 @@ static int launch_op(const tqhip_op &op, hipStream_t s) {
         case TQHIP_OP_I4_MATMUL: return launch_i4_matmul(w, op.x, op.y, op.out_dim, op.in_dim, op.n, op.group_size, s);
         case TQHIP_OP_I4_SET:
             return launch_i4_matvec_set(op.n, static_cast<const I4Mat *>(op.w), op.group_size, s);
+        case TQHIP_OP_VQ2_SET: return launch_vq2_matvec_set(op.n, static_cast<const I4Mat *>(op.w), s);
         case TQHIP_OP_BIIP_ROTATE:
             return launch_biip_rotate(op.x, op.y, op.in_dim, static_cast<const float *>(op.w2),
                                       static_cast<const float *>(op.w3), op.group_size, s);
