@@ -374,10 +374,13 @@ __global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
 }
 
 // The staged form: 8 rows per workgroup, so that each workgroup's prologue and rotation serve
-// twice the rows. PER: activations per thread (K <= 512 PER). Every load that does not wait for
-// the prologue goes out first: the prologue operands and rotation vectors of the thread's
-// activations, the row's first index dword and then its four codebook entries; the prologue
-// then runs in registers (one barrier for the RMSNorm's sum, one per butterfly stage).
+// twice the rows. PER: activations per thread (K <= 512 PER); a lane's row takes NIT = PER / 2
+// (rounded up) index dwords. Every load that does not wait for the prologue goes out first: the
+// prologue operands and rotation vectors of the thread's activations and all of the lane's index
+// dwords, then every codebook entry they name; the prologue then runs in registers (one barrier
+// for the RMSNorm's sum, one per two butterfly stages) while the entries arrive. (With a loop
+// that loaded an index dword and then its entries per step, the row's round trips followed one
+// another after the build: 896x4864 with SwiGLU and rotation 12.5 us per launch.)
 constexpr int kRotWaves = 8;
 template <int PER, int XM, bool ROT>
 __global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2StagedArgs a) {
@@ -394,8 +397,13 @@ __global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2StagedArg
     const unsigned *qrow =
         reinterpret_cast<const unsigned *>(m.w + kVq2CodebookBytes + static_cast<size_t>(live ? row : 0) * nb);
     const uint2 *cbg = reinterpret_cast<const uint2 *>(m.w);
-    const bool first = live && 4 * lane < nb;
-    const unsigned q0 = first ? qrow[lane] : 0u;
+    constexpr int NIT = (PER + 1) / 2;
+    unsigned qv[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int d = lane + 64 * it;
+        qv[it] = live && 4 * d < nb ? qrow[d] : 0u;
+    }
     float v[PER], p1[PER], p2[PER], p3[PER], sc[PER], sg[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -414,9 +422,11 @@ __global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2StagedArg
             sg[j] = ok ? m.sign[i] : 0.f;
         }
     }
-    uint2 c0[4];
+    uint2 cv[NIT][4];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) c0[jj] = cbg[(q0 >> (8 * jj)) & 0xFFu];
+    for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) cv[it][jj] = cbg[(qv[it] >> (8 * jj)) & 0xFFu];
     if constexpr (XM == 2) {  // add_rmsnorm's operations
         double ss = 0.0;
 #pragma unroll
@@ -476,20 +486,14 @@ __global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2StagedArg
     __syncthreads();
     if (!live) return;
     float acc = 0.f;
-    for (int d = lane; 4 * d < nb; d += 64) {
-        uint2 c[4];
-        if (d == lane) {
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) c[jj] = c0[jj];
-        } else {
-            const unsigned q = qrow[d];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) c[jj] = cbg[(q >> (8 * jj)) & 0xFFu];
-        }
+    for (int it = 0; it < NIT; ++it) {
+        const int d = lane + 64 * it;
+        if (4 * d >= nb) break;
         float4 xv[4];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) xv[jj] = *reinterpret_cast<const float4 *>(xs + 16 * d + 4 * jj);
-        acc = vq2_accum(acc, c, xv);
+        acc = vq2_accum(acc, cv[it], xv);
     }
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
     if (lane == 0) m.y[row] = acc;
