@@ -51,7 +51,19 @@ Printed (one JSON line on stdout):
                kernels/matvec/matvec_i4_ref.cpp built unmodified), row-split
                over host threads, on the same step; the C++ restatement is
                used when the compiled reference is absent
-Progress goes to stderr.
+  verify       the correctness gate (as the reference's bench_kernels checks
+               every variant against `ref` before it reports a time,
+               benchmarks/bench_kernels.cpp:255-259, 472-481): outside the timed
+               regions each section keeps the outputs of its last timed launch,
+               and the CPU-baseline leg checks them -- the step's 169 outputs
+               against the reference outputs the CPU baseline computed on the
+               same inputs, the headline, configs[0]/[2] and VQ2 outputs against
+               the CPU checker, prefill on every 97th row (every row at 32
+               tokens), the decode engines' logits against the reference's own
+               CPU decode of the same file. Each section gets
+               verify: {rel_l2, max_rel, verdict}; a section that fails has its
+               figures reported as null (value too, for the step)
+Progress goes to stderr, with each section's wall-clock seconds.
 """
 from __future__ import annotations
 
@@ -123,6 +135,9 @@ class Workload:
         dx = {k: self._dev(v) for k, v in acts.items()}
         dy = {(layer, name): self._dev(None, 4 * M) for layer in range(N_LAYERS) for name, M, _ in LAYER}
         dx_lm, dy_lm = self._dev(x_lm), self._dev(None, 4 * VOCAB)
+        # every copy writes the same outputs (the copies hold the same weights): one output buffer
+        # per matrix, in the order of self.host, read back for the correctness gate
+        self.outputs = [dy[(layer, name)] for layer in range(N_LAYERS) for name, _, _ in LAYER] + [dy_lm]
         self.set_steps, self.rt_steps = [], []  # per copy: the 25-launch and the 97-launch step
         for _ in range(N_COPIES):
             set_ops, rt_ops = [], []
@@ -165,6 +180,60 @@ class Workload:
 
     def layer_runtime_order(self):
         return [op for c in range(N_COPIES) for op in self.rt_steps[c][:-1]]
+
+    def download_outputs(self):
+        """The step's 169 outputs as its last launches left them (after a synchronisation)."""
+        self.tq.synchronize()
+        return [b.download(np.float32, M) for b, (_, M, _, _, _) in zip(self.outputs, self.host)]
+
+
+# ---- correctness gate -------------------------------------------------------------------------
+# Outputs of the timed sections, checked after all timing by the CPU-baseline leg (gate()).
+PENDING = []
+MATVEC_BAR, PREFILL_BAR, ENGINE_BAR = 1e-5, 2e-3, 1e-4  # rel L2 bars (north star; engine: decode tests)
+FIGURES = ("us", "gbs", "frac", "tflops", "mfma_frac", "us_batch_min", "us_batch_max", "ms_per_token",
+           "tokens_per_s", "value")
+
+
+def compare(got, want, l2_bar, max_bar=1e-3):
+    """rel L2 and max|err| / max|want|, the bars of the parity tests; a non-finite output where the
+    reference is finite (or the reverse) fails."""
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    fin = np.isfinite(want)
+    if not np.array_equal(np.isfinite(got), fin):
+        return {"rel_l2": None, "max_rel": None, "verdict": "FAIL", "why": "finiteness differs"}
+    d = got[fin] - want[fin]
+    den = np.linalg.norm(want[fin])
+    l2 = float(np.linalg.norm(d) / (den if den > 0 else 1.0))
+    sc = float(np.max(np.abs(want[fin]))) if fin.any() else 0.0
+    mx = float(np.max(np.abs(d)) / (sc if sc > 0 else 1.0)) if d.size else 0.0
+    return {"rel_l2": float(f"{l2:.3e}"), "max_rel": float(f"{mx:.3e}"),
+            "verdict": "PASS" if l2 <= l2_bar and mx <= max_bar else "FAIL", "bar": f"rel L2 <= {l2_bar:g}, "
+            f"max|err| <= {max_bar:g} max|y|"}
+
+
+def worst(checks):
+    """One verify record for several outputs: the largest figures, FAIL if any failed."""
+    out = {"rel_l2": None, "max_rel": None, "verdict": "PASS", "outputs": len(checks)}
+    for c in checks:
+        for k in ("rel_l2", "max_rel"):
+            if c[k] is not None and (out[k] is None or c[k] > out[k]):
+                out[k] = c[k]
+        if c["verdict"] != "PASS":
+            out["verdict"] = "FAIL"
+        if "bar" in c:
+            out["bar"] = c["bar"]
+    return out
+
+
+def settle(rec, check):
+    """Attaches a verify record; a failing section reports its figures as null."""
+    rec["verify"] = check
+    if check["verdict"] != "PASS":
+        for k in FIGURES:
+            if k in rec:
+                rec[k] = None
 
 
 def time_ops(tq, ops, reps, warmup, stream, batches=1):
@@ -350,12 +419,16 @@ def headline(tq, stream, reps=20):
         per.append(time_ops(tq, ops, reps, 0, stream) / len(ops))
     ms = float(np.median(per))
     gbs = algo_bytes(M, K) / (ms * 1e-3) / 1e9
+    stream.synchronize()
+    y = dy.download(np.float32, M)
     for c in copies:
         c.free()
-    return {"shape": "151936x2560 G64 (BASELINE configs[2] lm_head)", "us": round(ms * 1e3, 2),
-            "gbs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4), "bytes": algo_bytes(M, K),
-            "us_batch_min": round(min(per) * 1e3, 2), "us_batch_max": round(max(per) * 1e3, 2),
-            "rotation": "3 copies, 657 MB"}
+    rec = {"shape": "151936x2560 G64 (BASELINE configs[2] lm_head)", "us": round(ms * 1e3, 2),
+           "gbs": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4), "bytes": algo_bytes(M, K),
+           "us_batch_min": round(min(per) * 1e3, 2), "us_batch_max": round(max(per) * 1e3, 2),
+           "rotation": "3 copies, 657 MB"}
+    PENDING.append((rec, "i4", (w, x, M, K), y))
+    return rec
 
 
 def prefill(tq, stream, reps=30):
@@ -374,9 +447,12 @@ def prefill(tq, stream, reps=30):
         ms = time_ops(tq, ops, max(1, reps // 10), 1, stream, batches=5) / len(ops)
         fl = 2.0 * M * K * n
         tf = fl / (ms * 1e-3) / 1e12
-        rows.append({"tokens": n, "us": round(ms * 1e3, 2), "tflops": round(tf, 1),
-                     "mfma_frac": round(tf / PEAK_MFMA_TFLOPS, 4),
-                     "gbs": round((M * (K // G) * (4 + G // 2) + 4 * (K + M) * n) / (ms * 1e-3) / 1e9, 1)})
+        rec = {"tokens": n, "us": round(ms * 1e3, 2), "tflops": round(tf, 1),
+               "mfma_frac": round(tf / PEAK_MFMA_TFLOPS, 4),
+               "gbs": round((M * (K // G) * (4 + G // 2) + 4 * (K + M) * n) / (ms * 1e-3) / 1e9, 1)}
+        rows.append(rec)
+        stream.synchronize()
+        PENDING.append((rec, "matmul", (w, x, M, K, n), dy.download(np.float32, M * n)))
         dx.free()
         dy.free()
     for dw in dws:
@@ -399,12 +475,16 @@ def cold_matvec(tq, stream, M, K, tag):
     dx, dy = tq.DeviceBuffer.from_array(x), tq.DeviceBuffer(4 * M)
     ops = [tq.Op(tq.OP_I4_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, G) for c in copies]
     ms = time_ops(tq, ops, max(1, 60 // ncopy), 1, stream, batches=7) / len(ops)
+    stream.synchronize()
+    y = dy.download(np.float32, M)
     for c in copies:
         c.free()
     dx.free()
     dy.free()
-    return {"shape": f"{M}x{K}", "us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
-            "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b, "copies": ncopy}
+    rec = {"shape": f"{M}x{K}", "us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+           "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b, "copies": ncopy}
+    PENDING.append((rec, "i4", (w, x, M, K), y))
+    return rec
 
 
 def configs0(tq, stream):
@@ -421,7 +501,8 @@ def configs2(tq, stream):
     rows = []
     for M, K, role in CONFIGS2:
         r = cold_matvec(tq, stream, M, K, "c2")
-        rows.append({"shape": r["shape"], "role": role, **{k: v for k, v in r.items() if k != "shape"}})
+        r["role"] = role  # the same dict the gate fills in
+        rows.append(r)
     return rows
 
 
@@ -438,8 +519,11 @@ def vq2(tq, stream, reps=20):
         ops = [tq.Op(tq.OP_VQ2_MATVEC, c.ptr, dx.ptr, dy.ptr, M, K, 1, 0) for c in copies]
         ms = time_ops(tq, ops, max(1, reps * 3 // ncopy), 1, stream, batches=7) / len(ops)
         b = 2048 + M * (K // 4) + 4 * (M + K)
-        rows.append({"shape": f"{M}x{K}", "us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
-                     "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b, "copies": ncopy})
+        rec = {"shape": f"{M}x{K}", "us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+               "frac": round(b / (ms * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b, "copies": ncopy}
+        rows.append(rec)
+        stream.synchronize()
+        PENDING.append((rec, "vq2", (w, x, M, K), dy.download(np.float32, M)))
         for c in copies:
             c.free()
         dx.free()
@@ -449,22 +533,38 @@ def vq2(tq, stream, reps=20):
 
 def host_call(tq, reps=50):
     """The reference-signature entry point (tqhip_matvec_i4: host x in, host y out,
-    weights cached in HBM after the first call): PCIe-inclusive latency per call."""
+    weights cached in HBM after the first call): PCIe-inclusive latency per call (median of
+    reps wall-clock calls), then the same calls with HIP events around the x upload, the
+    kernel and the y download (tqhip_host_timing), medians of each."""
     rows = []
+    lib = tq.lib()
     for M, K in ((4864, HIDDEN), (VOCAB, 2560)):
         w = tq.synth_i4(M, K, G, seed=tq.synth_seed(0, -2, f"host_{M}"))
         x = tq.synth_normal(K, seed=tq.synth_seed(0, -2, f"hostx_{M}"))
         y = np.empty(M, np.float32)
-        f = tq.lib().tqhip_matvec_i4
+        f = lib.tqhip_matvec_i4
         args = (w.ctypes.data, x.ctypes.data, y.ctypes.data, M, K, G)
         for _ in range(3):
             f(*args)
-        t0 = time.perf_counter()
+        wall = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            f(*args)
+            wall.append(time.perf_counter() - t0)
+        us = float(np.median(wall)) * 1e6
+        lib.tqhip_host_timing(1)
+        split = []
+        a, b, c = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
         for _ in range(reps):
             f(*args)
-        us = (time.perf_counter() - t0) / reps * 1e6
-        rows.append({"shape": f"{M}x{K}", "us": round(us, 2), "gbs": round(algo_bytes(M, K) / (us * 1e-6) / 1e9, 1)})
-    tq.lib().tqhip_release_weights()
+            lib.tqhip_host_timing_last(ctypes.byref(a), ctypes.byref(b), ctypes.byref(c))
+            split.append((a.value, b.value, c.value))
+        lib.tqhip_host_timing(0)
+        med = np.median(np.array(split), axis=0) * 1e3
+        rows.append({"shape": f"{M}x{K}", "us": round(us, 2), "gbs": round(algo_bytes(M, K) / (us * 1e-6) / 1e9, 1),
+                     "split_us": {"x_upload": round(float(med[0]), 2), "kernel": round(float(med[1]), 2),
+                                  "y_download": round(float(med[2]), 2)}})
+    lib.tqhip_release_weights()
     return rows
 
 

@@ -45,7 +45,8 @@ extern "C" {
 #endif
 
 #define TQHIP_OK 0
-#define TQHIP_EBADSHAPE (-1)    /* a dimension < 1, or in_dim % 4 != 0 for VQ2 */
+#define TQHIP_EBADSHAPE (-1)    /* a dimension < 1, in_dim % 4 != 0 for VQ2, or a null operand pointer
+                                   (checked before anything is launched) */
 #define TQHIP_EBADGROUP (-2)    /* group_size odd or < 2 */
 #define TQHIP_ETOOLARGE (-3)    /* shape exceeds the kernel's 32-bit addressing */
 #define TQHIP_ELAUNCH (-4)      /* the kernel launch failed */
@@ -82,6 +83,13 @@ void tqhip_biip_rotate(const float *x, float *y, int dim, const float *scale, co
 /* Drops every cached device copy of host weights (not in the reference: its
  * CUDA variants keep their cache until exit). */
 void tqhip_release_weights(void);
+
+/* Timing of the host-pointer calls above (not in the reference; its bench_kernels times the
+ * whole call). With timing on, each call records HIP events around its x upload, its
+ * kernels and its y download; tqhip_host_timing_last returns the three intervals of the
+ * last call in milliseconds (0 until a timed call has run). */
+void tqhip_host_timing(int on);
+void tqhip_host_timing_last(float *upload_ms, float *kernel_ms, float *download_ms);
 
 /* ---- 2. device-pointer entry points ------------------------------------- */
 
@@ -132,8 +140,10 @@ int tqhip_matvec_vq2_set_dev(const tqhip_i4_mat *mats, int n, void *stream);
  * device array of TQHIP_NOALLOC_SCRATCH_BYTES (16 MiB) that every GPU the library runs on
  * holds until the process ends; its last 64 KiB hold the few-token kernel's tile counters
  * (zero between calls). A call whose fp16 copy needs more than the rest
- * (((ceil(K/64)*64*2*N + 255) & ~255) + 4*N bytes, e.g. above 3261 tokens at K = 2560)
- * returns TQHIP_ENOSCRATCH before launching anything. Group sizes that are not a
+ * (((ceil(K/64)*64*2*N + 255) & ~255) + 4*N bytes, e.g. above 3261 tokens at K = 2560), or
+ * whose few-token partial products do not fit (16 KiB per 128-row tile and K slice, e.g.
+ * 151936x896 at up to 32 tokens: 38.9 MB), returns TQHIP_ENOSCRATCH before launching
+ * anything; no call is rerouted to another kernel. Group sizes that are not a
  * multiple of 32 run one matvec per token, with kernels that need no scratch. All calls
  * on one GPU share the array: calls that overlap on one GPU (two streams, or two host
  * threads) race and must be ordered by the caller. */

@@ -160,12 +160,26 @@ int main() {
     check(scratch_prefill(stream(5), 1000, &x) == kOk, "alloc_failure", "no recovery");
     std::printf("ok alloc_failure\n");
 
-    // 10. forgetting a stream frees its buffers, unless a graph recorded one
+    // 10. forgetting a stream frees its buffers and its set, unless a graph recorded a buffer
     const size_t l0 = g_live.size();
+    const long n0 = scratch_live_sets();
     scratch_forget_stream(stream(5));
     check(g_live.size() == l0 - 1, "forget", "buffer of a destroyed stream kept");
+    check(scratch_live_sets() == n0 - 1, "forget", "set of a destroyed stream kept");
     scratch_forget_stream(stream(1));  // holds a retired, captured buffer: everything stays
     check(g_live.size() == l0 - 1 && g_live.count(a) == 1, "forget", "a captured buffer was freed");
+    check(scratch_live_sets() == n0 - 1, "forget", "the set of a captured buffer was deleted");
+    scratch_forget_stream(stream(5));  // forgotten twice: nothing left to do
+    check(scratch_live_sets() == n0 - 1, "forget", "second forget changed the sets");
+    {  // a stream used, forgotten, and used again gets a fresh set
+        void *y = nullptr;
+        check(scratch_prefill(stream(6), 10, &y) == kOk, "forget", "alloc");
+        check(scratch_live_sets() == n0, "forget", "no set for a new stream");
+        scratch_forget_stream(stream(6));
+        check(scratch_live_sets() == n0 - 1 && g_live.count(y) == 0, "forget", "set or buffer kept");
+        check(scratch_prefill(stream(6), 10, &y) == kOk && scratch_live_sets() == n0, "forget", "reuse after forget");
+        scratch_forget_stream(stream(6));
+    }
     std::printf("ok forget\n");
 
     // 11. devices are separate: the same stream handle on device 1 gets its own set

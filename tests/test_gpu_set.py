@@ -190,3 +190,22 @@ def test_set_op_in_a_captured_graph(gpu, orc):
             assert_close(wv, orc.matvec_i4(w, x[0], M, K, 64, threads=16), name)
     finally:
         graph.close()
+
+
+def test_non_finite_activation_stays_in_its_matrix(gpu, orc):
+    """A NaN in one activation vector of a set (up's x): every output of the matrices that read it
+    is non-finite, as in the reference, and the matrices with other activation vectors are finite
+    and unchanged (each workgroup converts only its own matrix's activations)."""
+    mats = build(gpu, QWEN25_LAYER, 64, seed=70)
+    clean = run_set(gpu, mats, 64)
+    x_mlp, dx_mlp = next(m[4] for m in mats if m[0] == "gate")
+    poisoned = x_mlp.copy()
+    poisoned[100] = np.nan
+    dx_mlp.upload(poisoned)
+    got = run_set(gpu, mats, 64)
+    for (name, M, K, w, x, _, _), g, c in zip(mats, got, clean):
+        if name in ("gate", "up"):
+            assert not np.any(np.isfinite(orc.matvec_i4(w, poisoned, M, K, 64, threads=16)))
+            assert not np.any(np.isfinite(g)), f"{name}: finite outputs from a NaN activation"
+        else:
+            assert np.array_equal(g, c), f"{name}: changed by another matrix's NaN activation"

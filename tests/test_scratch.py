@@ -49,10 +49,13 @@ def test_dev_entry_points_return_errors_without_a_device(tqa):
         spec = importlib.util.spec_from_file_location("tq", {os.path.join(REPO, "tiny-llm_amd", "__init__.py")!r})
         tq = importlib.util.module_from_spec(spec); spec.loader.exec_module(tq)
         lib = tq.lib()
-        res = [lib.tqhip_matmul_i4_dev(None, None, None, 9728, 2560, 32, 64, None),
-               lib.tqhip_matmul_i4_dev(None, None, None, 64, 100, 3, 6, None),
-               lib.tqhip_matvec_i4_dev(None, None, None, 2560, 9728, 64, None),
-               lib.tqhip_matvec_vq2_dev(None, None, None, 3072, 1024, None)]
+        # non-null stand-ins for device pointers (no device is visible, so nothing can run on
+        # them): the calls get past the operand checks to the scratch allocation and the launch
+        p = 1 << 20
+        res = [lib.tqhip_matmul_i4_dev(p, p, p, 9728, 2560, 32, 64, None),
+               lib.tqhip_matmul_i4_dev(p, p, p, 64, 100, 3, 6, None),
+               lib.tqhip_matvec_i4_dev(p, p, p, 2560, 9728, 64, None),
+               lib.tqhip_matvec_vq2_dev(p, p, p, 3072, 1024, None)]
         print("codes", res)
         sys.exit(0 if all(r < 0 for r in res) else 3)
     """)

@@ -61,7 +61,23 @@ def test_noalloc_matches_dev_entry_point(gpu, orc, kind):
 
 
 def test_noalloc_refuses_calls_beyond_the_static_array(gpu):
-    K = 2560
-    assert gpu.matmul_i4_noalloc_dev(None, None, None, 9728, K, 3262, 64) == gpu.ENOSCRATCH  # 16 MiB - 64 KiB hold 3261
-    assert gpu.matmul_i4_noalloc_dev(None, None, None, 9728, K, 100000, 64) == gpu.ENOSCRATCH
-    assert gpu.matmul_i4_noalloc_dev(None, None, None, 0, K, 8, 64) == gpu.EBADSHAPE
+    """Refusals come before any launch. The operands are real device buffers of the call's size
+    (uninitialised), so a call that were wrongly launched would compute, not touch a null pointer."""
+    def call(M, K, N):
+        dw = gpu.DeviceBuffer(M * gpu.i4_row_bytes(K, 64))
+        dx, dy = gpu.DeviceBuffer(4 * K * N), gpu.DeviceBuffer(4 * M * N)
+        st = gpu.matmul_i4_noalloc_dev(dw, dx, dy, M, K, N, 64)
+        gpu.synchronize()
+        for b in (dw, dx, dy):
+            b.free()
+        return st
+
+    assert call(9728, 2560, 3262) == gpu.ENOSCRATCH  # the fp16 copy: 16 MiB - 64 KiB hold 3261 tokens at K 2560
+    # few tokens whose partial products do not fit (1187 tiles x 2 K slices x 16 KiB = 38.9 MB):
+    # refused, not rerouted to the MFMA GEMM, whose bits differ from tqhip_matmul_i4_dev's
+    assert call(151936, 896, 8) == gpu.ENOSCRATCH
+    # shape and operand checks (nothing to launch on)
+    assert gpu.matmul_i4_noalloc_dev(None, None, None, 0, 2560, 8, 64) == gpu.EBADSHAPE
+    dw, dx, dy = gpu.DeviceBuffer(896 * gpu.i4_row_bytes(896, 64)), gpu.DeviceBuffer(4 * 896 * 8), gpu.DeviceBuffer(4 * 896 * 8)
+    assert gpu.matmul_i4_noalloc_dev(dw, None, dy, 896, 896, 8, 64) == gpu.EBADSHAPE
+    assert gpu.matmul_i4_noalloc_dev(dw, dx, None, 896, 896, 40, 64) == gpu.EBADSHAPE

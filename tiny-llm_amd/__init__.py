@@ -83,6 +83,8 @@ _SIGS = {
     "tqhip_matmul_i4": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "tqhip_biip_rotate": (None, [_vp, _vp, _i, _vp, _vp, _i]),
     "tqhip_release_weights": (None, []),
+    "tqhip_host_timing": (None, [_i]),
+    "tqhip_host_timing_last": (None, [_f32p, _f32p, _f32p]),
     # device-pointer entry points
     "tqhip_matvec_i4_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "tqhip_matvec_i4_generic_dev": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),

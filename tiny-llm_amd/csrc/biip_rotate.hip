@@ -97,6 +97,7 @@ int launch_biip_rotate(const float *x, float *y, int dim, const float *scale, co
     if (dim < 1 || block_size < 1 || (block_size & (block_size - 1)) || block_size > kBiipChunk ||
         dim % block_size)
         return kBadShape;
+    if (!x || !y || !sign) return kBadShape;  // nothing is launched on a null operand (scale may be null)
     int lg = 0;
     while ((1 << lg) < block_size) ++lg;
     // computed on the host exactly as the reference does (float sqrt, then 1.0f / it)
@@ -112,6 +113,7 @@ int launch_biip_rotate_n(int n, const float *x, float *const *y, int dim, const 
     if (n < 1 || n > 3 || dim < 1 || block_size < 1 || (block_size & (block_size - 1)) || block_size > kBiipChunk ||
         dim % block_size)
         return kBadShape;
+    if (!x) return kBadShape;
     int lg = 0;
     while ((1 << lg) < block_size) ++lg;
     const float inv_sqrt = 1.0f / std::sqrt(static_cast<float>(block_size));

@@ -4,11 +4,15 @@
 // (kernels/matvec/matvec_f16_cuda_resident_coal_ws.cu:88-159): weights are
 // copied to HBM once and cached by host pointer + byte size, x/y go through a
 // grow-only device workspace, and the call returns after y is back on the
-// host. One mutex guards the cache and workspace, so concurrent callers (the
-// reference's MoE expert pool calls mv from several threads) are serialised.
+// host. x and y are bounced through grow-only pinned host buffers: a copy from
+// pageable memory is staged and synchronised inside the runtime, one from
+// pinned memory is one DMA. One mutex guards the cache and workspaces, so
+// concurrent callers (the reference's MoE expert pool calls mv from several
+// threads) are serialised.
 
 #include "../../include/tqhip.h"
 
+#include <cstring>
 #include <mutex>
 #include <vector>
 #include <unordered_map>
@@ -50,7 +54,15 @@ struct HostBoundary {
     size_t x_cap = 0;
     float *dy = nullptr;
     size_t y_cap = 0;
+    float *hx = nullptr;  // pinned bounce buffers
+    size_t hx_cap = 0;
+    float *hy = nullptr;
+    size_t hy_cap = 0;
     hipStream_t stream = nullptr;
+    // Optional split of the last call (tqhip_host_timing): events around the copies and launches.
+    bool timing = false;
+    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    float split_ms[3] = {0.f, 0.f, 0.f};
 
     hipStream_t get_stream() {
         if (!stream) TQ_HIP_CHECK(hipStreamCreate(&stream));  // default priority
@@ -75,12 +87,39 @@ struct HostBoundary {
     }
     float *ensure(float *&p, size_t &cap, size_t n) {
         if (n > cap) {
-            if (p) TQ_HIP_CHECK(hipFree(p));
+            if (p) {
+                TQ_HIP_CHECK(hipStreamSynchronize(get_stream()));
+                TQ_HIP_CHECK(hipFree(p));
+            }
             p = nullptr;
             TQ_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&p), n * sizeof(float)));
             cap = n;
         }
         return p;
+    }
+    float *pinned(float *&p, size_t &cap, size_t n) {
+        if (n > cap) {
+            if (p) {
+                TQ_HIP_CHECK(hipStreamSynchronize(get_stream()));
+                TQ_HIP_CHECK(hipHostFree(p));
+            }
+            p = nullptr;
+            TQ_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&p), n * sizeof(float), hipHostMallocDefault));
+            cap = n;
+        }
+        return p;
+    }
+    // Event i (0: before the upload, 1: after it, 2: after the launches, 3: after the download)
+    // when timing is on.
+    void mark(int i) {
+        if (!timing) return;
+        if (!ev[i]) TQ_HIP_CHECK(hipEventCreate(&ev[i]));
+        TQ_HIP_CHECK(hipEventRecord(ev[i], get_stream()));
+    }
+    // After the call's synchronisation: the upload, kernel and download times of the call.
+    void read_split() {
+        if (!timing) return;
+        for (int i = 0; i < 3; ++i) TQ_HIP_CHECK(hipEventElapsedTime(&split_ms[i], ev[i], ev[i + 1]));
     }
     void release() {
         for (auto &kv : weights)
@@ -103,11 +142,29 @@ void check_status(int st, const char *what) {
     die(what, msg);
 }
 
-void upload(float *d, const float *h, size_t n, hipStream_t s) {
-    TQ_HIP_CHECK(hipMemcpyAsync(d, h, n * sizeof(float), hipMemcpyHostToDevice, s));
+// x (n floats) into the device workspace through the pinned bounce buffer.
+void upload(HostBoundary &hb, float *d, const float *h, size_t n, hipStream_t s) {
+    float *p = hb.pinned(hb.hx, hb.hx_cap, n);
+    std::memcpy(p, h, n * sizeof(float));
+    hb.mark(0);
+    TQ_HIP_CHECK(hipMemcpyAsync(d, p, n * sizeof(float), hipMemcpyHostToDevice, s));
+    hb.mark(1);
 }
-void download(float *h, const float *d, size_t n, hipStream_t s) {
-    TQ_HIP_CHECK(hipMemcpyAsync(h, d, n * sizeof(float), hipMemcpyDeviceToHost, s));
+
+// The outputs (pieces of the device workspace) back to the caller's arrays: one copy of the
+// n floats at d into the pinned bounce buffer, a synchronisation, then one host copy per piece.
+struct Piece {
+    float *host;
+    size_t off, n;
+};
+void download(HostBoundary &hb, const float *d, size_t n, const Piece *pieces, int np, hipStream_t s) {
+    float *p = hb.pinned(hb.hy, hb.hy_cap, n);
+    hb.mark(2);
+    TQ_HIP_CHECK(hipMemcpyAsync(p, d, n * sizeof(float), hipMemcpyDeviceToHost, s));
+    hb.mark(3);
+    TQ_HIP_CHECK(hipStreamSynchronize(s));
+    hb.read_split();
+    for (int i = 0; i < np; ++i) std::memcpy(pieces[i].host, p + pieces[i].off, pieces[i].n * sizeof(float));
 }
 
 }  // namespace
@@ -125,10 +182,10 @@ void tqhip_matvec_i4(const uint8_t *w, const float *x, float *y, int out_dim, in
     const uint8_t *dw = hb.resident(w, static_cast<size_t>(out_dim) * i4_row_bytes(in_dim, group_size));
     float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
     float *dy = hb.ensure(hb.dy, hb.y_cap, out_dim);
-    upload(dx, x, in_dim, s);
+    upload(hb, dx, x, in_dim, s);
     check_status(launch_i4_matvec(dw, dx, dy, out_dim, in_dim, group_size, s), "tqhip_matvec_i4");
-    download(y, dy, out_dim, s);
-    TQ_HIP_CHECK(hipStreamSynchronize(s));
+    const Piece out[1] = {{y, 0, static_cast<size_t>(out_dim)}};
+    download(hb, dy, out_dim, out, 1, s);
 }
 
 void tqhip_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, float *y1, float *y2, int out_dim,
@@ -143,14 +200,14 @@ void tqhip_matvec_pair_i4(const uint8_t *w1, const uint8_t *w2, const float *x, 
     const uint8_t *d2 = hb.resident(w2, wb);
     float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
     float *dy = hb.ensure(hb.dy, hb.y_cap, 2 * static_cast<size_t>(out_dim));
-    upload(dx, x, in_dim, s);
+    upload(hb, dx, x, in_dim, s);
     const uint8_t *ws[2] = {d1, d2};
     float *ys[2] = {dy, dy + out_dim};
     const int ms[2] = {out_dim, out_dim};
     check_status(launch_i4_matvec_group(2, ws, ys, ms, dx, in_dim, group_size, s), "tqhip_matvec_pair_i4");
-    download(y1, dy, out_dim, s);
-    download(y2, dy + out_dim, out_dim, s);
-    TQ_HIP_CHECK(hipStreamSynchronize(s));
+    const size_t n = static_cast<size_t>(out_dim);
+    const Piece out[2] = {{y1, 0, n}, {y2, n, n}};
+    download(hb, dy, 2 * n, out, 2, s);
 }
 
 void tqhip_matvec_qkv_i4(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv, const float *x, float *yq,
@@ -166,15 +223,14 @@ void tqhip_matvec_qkv_i4(const uint8_t *wq, const uint8_t *wk, const uint8_t *wv
     const uint8_t *dv = hb.resident(wv, static_cast<size_t>(kv_dim) * rb);
     float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
     float *dy = hb.ensure(hb.dy, hb.y_cap, static_cast<size_t>(q_dim) + 2 * static_cast<size_t>(kv_dim));
-    upload(dx, x, in_dim, s);
+    upload(hb, dx, x, in_dim, s);
     const uint8_t *ws[3] = {dq, dk, dv};
     float *ys[3] = {dy, dy + q_dim, dy + q_dim + kv_dim};
     const int ms[3] = {q_dim, kv_dim, kv_dim};
     check_status(launch_i4_matvec_group(3, ws, ys, ms, dx, in_dim, group_size, s), "tqhip_matvec_qkv_i4");
-    download(yq, dy, q_dim, s);
-    download(yk, dy + q_dim, kv_dim, s);
-    download(yv, dy + q_dim + kv_dim, kv_dim, s);
-    TQ_HIP_CHECK(hipStreamSynchronize(s));
+    const size_t nq = static_cast<size_t>(q_dim), nk = static_cast<size_t>(kv_dim);
+    const Piece out[3] = {{yq, 0, nq}, {yk, nq, nk}, {yv, nq + nk, nk}};
+    download(hb, dy, nq + 2 * nk, out, 3, s);
 }
 
 void tqhip_matvec_vq2(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim) {
@@ -185,10 +241,10 @@ void tqhip_matvec_vq2(const uint8_t *w, const float *x, float *y, int out_dim, i
     const uint8_t *dw = hb.resident(w, vq2_bytes(out_dim, in_dim));
     float *dx = hb.ensure(hb.dx, hb.x_cap, in_dim);
     float *dy = hb.ensure(hb.dy, hb.y_cap, out_dim);
-    upload(dx, x, in_dim, s);
+    upload(hb, dx, x, in_dim, s);
     check_status(launch_vq2_matvec(dw, dx, dy, out_dim, in_dim, s), "tqhip_matvec_vq2");
-    download(y, dy, out_dim, s);
-    TQ_HIP_CHECK(hipStreamSynchronize(s));
+    const Piece out[1] = {{y, 0, static_cast<size_t>(out_dim)}};
+    download(hb, dy, out_dim, out, 1, s);
 }
 
 void tqhip_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size) {
@@ -199,10 +255,10 @@ void tqhip_matmul_i4(const uint8_t *w, const float *x, float *y, int M, int K, i
     const uint8_t *dw = hb.resident(w, static_cast<size_t>(M) * i4_row_bytes(K, group_size));
     float *dx = hb.ensure(hb.dx, hb.x_cap, static_cast<size_t>(K) * N);
     float *dy = hb.ensure(hb.dy, hb.y_cap, static_cast<size_t>(M) * N);
-    upload(dx, x, static_cast<size_t>(K) * N, s);
+    upload(hb, dx, x, static_cast<size_t>(K) * N, s);
     check_status(launch_i4_matmul(dw, dx, dy, M, K, N, group_size, s), "tqhip_matmul_i4");
-    download(y, dy, static_cast<size_t>(M) * N, s);
-    TQ_HIP_CHECK(hipStreamSynchronize(s));
+    const Piece out[1] = {{y, 0, static_cast<size_t>(M) * N}};
+    download(hb, dy, static_cast<size_t>(M) * N, out, 1, s);
 }
 
 void tqhip_biip_rotate(const float *x, float *y, int dim, const float *scale, const float *sign, int block_size) {
@@ -216,10 +272,24 @@ void tqhip_biip_rotate(const float *x, float *y, int dim, const float *scale, co
         scale ? reinterpret_cast<const float *>(hb.resident(scale, static_cast<size_t>(dim) * sizeof(float))) : nullptr;
     const float *dsign = reinterpret_cast<const float *>(hb.resident(sign, static_cast<size_t>(dim) * sizeof(float)));
     float *dx = hb.ensure(hb.dx, hb.x_cap, dim);
-    upload(dx, x, dim, s);
+    upload(hb, dx, x, dim, s);
     check_status(launch_biip_rotate(dx, dx, dim, dscale, dsign, block_size, s), "tqhip_biip_rotate");
-    download(y, dx, dim, s);
-    TQ_HIP_CHECK(hipStreamSynchronize(s));
+    const Piece out[1] = {{y, 0, static_cast<size_t>(dim)}};
+    download(hb, dx, dim, out, 1, s);
+}
+
+void tqhip_host_timing(int on) {
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    hb.timing = on != 0;
+}
+
+void tqhip_host_timing_last(float *upload_ms, float *kernel_ms, float *download_ms) {
+    HostBoundary &hb = boundary();
+    std::lock_guard<std::mutex> lock(hb.mu);
+    if (upload_ms) *upload_ms = hb.split_ms[0];
+    if (kernel_ms) *kernel_ms = hb.split_ms[1];
+    if (download_ms) *download_ms = hb.split_ms[2];
 }
 
 void tqhip_release_weights(void) {

@@ -46,6 +46,7 @@ __global__ __launch_bounds__(256) void i4_embed_rows_kernel(const uint8_t *__res
 int launch_i4_embed_rows(const uint8_t *embed, const int *rows, int n, int dim, int group_size, float *out,
                          hipStream_t stream) {
     if (n < 1 || dim < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+    if (!embed || !rows || !out) return kBadShape;
     hipLaunchKernelGGL(i4_embed_rows_kernel, dim3(n), dim3(256), 0, stream, embed, rows, dim, group_size, out);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }

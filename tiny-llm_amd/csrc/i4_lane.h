@@ -22,6 +22,32 @@ __device__ inline float half_bits(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xFFFFu)));
 }
 
+// The power of two 2^f that puts a group's largest |x| m into [2^21, 2^22): the exact-integer
+// kernels convert the group to X = rint(x * 2^f), |X| <= 2^22. f <= 149, so ldexpf(x, f) (one
+// v_ldexp_f32, exact for every finite x of the group) must scale the value itself: 2^f alone
+// is not a finite float for f >= 128. Zero and non-finite maxima give 0.
+__device__ inline int group_exponent(float m) {
+    if (!(m > 0.f && m <= 3.40282347e38f)) return 0;
+    int e;
+    frexpf(m, &e);  // m in [2^(e-1), 2^e)
+    return min(22 - e, 149);
+}
+
+// |v|, or +inf when v is an infinity or a NaN: a group maximum taken over these with fmaxf is
+// +inf exactly when the group holds a non-finite activation (fmaxf alone drops a NaN).
+__device__ inline float abs_or_inf(float v) {
+    const float a = fabsf(v);
+    return a <= 3.40282347e38f ? a : __builtin_inff();
+}
+
+// The epilogue's 2^-f for a group with maximum m, or NaN when the group holds a non-finite
+// activation (m = +inf): every row's sum then takes the NaN, so each output is non-finite where
+// the reference's double sum of w * x is (an inf or NaN x gives inf or NaN products, w = 0
+// included), instead of a finite value from saturated integer conversions.
+__device__ inline float group_unscale(float m, int f) {
+    return m <= 3.40282347e38f ? ldexpf(1.f, -f) : __builtin_nanf("");
+}
+
 template <int CTRL>
 __device__ inline float dpp_f(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));

@@ -1277,18 +1277,26 @@ int noalloc_scratch(unsigned char **out) {
 int launch_i4_matmul_noalloc(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                              hipStream_t stream) {
     if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+    // (the size checks below come first, so a call's ENOSCRATCH does not depend on its pointers;
+    // every launch below is preceded by the null check)
+    const bool operands = w && x && y;
     if (skinny_applies(x, K, N, group_size)) {
+        // launch_i4_matmul runs the few-token kernel here; another kernel would give other
+        // bits, so a call whose partials do not fit is refused rather than rerouted
+        // (e.g. 151936x896 at up to 32 tokens: 1187 tiles x 2 slices x 16 KiB).
         const SkinnyGeom g = skinny_geom(M, K);
-        if (g.part_bytes <= kNoAllocWorkBytes && static_cast<size_t>(g.tiles) * 8 <= kNoAllocArrivalBytes) {
-            unsigned char *ws = nullptr;
-            const int st = noalloc_scratch(&ws);
-            if (st != kOk) return st;
-            return launch_skinny(w, x, y, M, K, N, g, reinterpret_cast<float *>(ws),
-                                 reinterpret_cast<unsigned long long *>(ws + kNoAllocWorkBytes), stream);
-        }
+        if (g.part_bytes > kNoAllocWorkBytes || static_cast<size_t>(g.tiles) * 8 > kNoAllocArrivalBytes)
+            return kNoScratch;
+        if (!operands) return kBadShape;
+        unsigned char *ws = nullptr;
+        const int st = noalloc_scratch(&ws);
+        if (st != kOk) return st;
+        return launch_skinny(w, x, y, M, K, N, g, reinterpret_cast<float *>(ws),
+                             reinterpret_cast<unsigned long long *>(ws + kNoAllocWorkBytes), stream);
     }
     const bool mfma = mfma_applies(M, K, N, group_size);
     if (mfma && prefill_scratch_bytes(K, N) > kNoAllocWorkBytes) return kNoScratch;
+    if (!operands) return kBadShape;
     unsigned char *ws = nullptr;
     if (mfma) {
         const int st = noalloc_scratch(&ws);
@@ -1305,6 +1313,7 @@ int launch_i4_matmul_noalloc(const uint8_t *w, const float *x, float *y, int M, 
 int launch_i4_matmul(const uint8_t *w, const float *x, float *y, int M, int K, int N, int group_size,
                      hipStream_t stream) {
     if (M < 1 || K < 1 || N < 1 || group_size < 2 || (group_size & 1)) return kBadShape;
+    if (!w || !x || !y) return kBadShape;  // nothing is launched on a null operand
     if (skinny_applies(x, K, N, group_size)) {
         const SkinnyGeom g = skinny_geom(M, K);
         unsigned long long *slots = nullptr;  // zero between launches: the arrival counters

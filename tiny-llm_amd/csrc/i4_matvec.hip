@@ -76,13 +76,6 @@ __device__ inline int plane_pos(int i) {
     return (i & ~7) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
 }
 
-__device__ inline int group_exponent(float m) {
-    if (!(m > 0.f)) return 0;
-    int e;
-    frexpf(m, &e);  // m in [2^(e-1), 2^e)
-    return min(22 - e, 149);
-}
-
 // Three signed base-256 digits of X (|X| <= 2^22): X = d0 + 256*d1 + 65536*d2.
 __device__ inline void planes_of(int X, int &d0, int &d1, int &d2) {
     d0 = ((X + 128) & 255) - 128;
@@ -268,7 +261,7 @@ __device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K,
                     v[i] = xf.v[i];
                 else
                     v[i] = (live && k < K) ? x[k] : 0.f;
-                m = fmaxf(m, fabsf(v[i]));
+                m = fmaxf(m, abs_or_inf(v[i]));
             }
             m = fmaxf(m, dpp_f<kDppXor1>(m));
             m = fmaxf(m, dpp_f<kDppXor2>(m));
@@ -305,13 +298,13 @@ __device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K,
                     lds_write3_u2(xp.pl + 8 * b, Kp, v2u{w[0][0], w[0][1]}, v2u{w[1][0], w[1][1]},
                                   v2u{w[2][0], w[2][1]});
                     lds_write_u32(xp.pre + b, static_cast<unsigned>(s));
-                    if (j == 0) lds_write_u32(xp.gexp + b / LPG, __builtin_bit_cast(unsigned, ldexpf(1.f, -f)));
+                    if (j == 0) lds_write_u32(xp.gexp + b / LPG, __builtin_bit_cast(unsigned, group_unscale(m, f)));
                 } else {
 #pragma unroll
                     for (int p = 0; p < 3; ++p)
                         *reinterpret_cast<uint2 *>(xp.pl + p * Kp + 8 * b) = make_uint2(w[p][0], w[p][1]);
                     xp.pre[b] = s;
-                    if (j == 0) xp.gexp[b / LPG] = ldexpf(1.f, -f);
+                    if (j == 0) xp.gexp[b / LPG] = group_unscale(m, f);
                 }
             }
         }
@@ -325,7 +318,7 @@ __device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K,
             float m = 0.f;
             for (int i = lane; i < G; i += 64) {
                 const int k = base + i;
-                if (k < K) m = fmaxf(m, fabsf(x[k]));
+                if (k < K) m = fmaxf(m, abs_or_inf(x[k]));
             }
             m = wave_max(m);
             const int f = group_exponent(m);
@@ -344,7 +337,7 @@ __device__ void prepare_x(const XPlanes &xp, const float *__restrict__ x, int K,
                 s += __shfl_xor(s, 4);
                 if ((i & 7) == 0) xp.pre[(base + i) >> 3] = s;  // block sum; prefixed below
             }
-            if (lane == 0) xp.gexp[g] = ldexpf(1.f, -f);
+            if (lane == 0) xp.gexp[g] = group_unscale(m, f);
         }
         __syncthreads();
         // turn block sums into per-group inclusive prefixes (one thread per group)
@@ -368,7 +361,7 @@ __device__ void prepare_x_wave(const XPlanes &xp, const float *__restrict__ x, i
     const int j = lane & (LPG - 1);
     float m = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(xf.v[i]));
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, abs_or_inf(xf.v[i]));
     m = fmaxf(m, dpp_f<kDppXor1>(m));
     m = fmaxf(m, dpp_f<kDppXor2>(m));
     m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
@@ -400,7 +393,7 @@ __device__ void prepare_x_wave(const XPlanes &xp, const float *__restrict__ x, i
 #pragma unroll
     for (int p = 0; p < 3; ++p) *reinterpret_cast<uint2 *>(xp.pl + p * xp.stride + 8 * lane) = make_uint2(w[p][0], w[p][1]);
     xp.pre[lane] = s;
-    if (j == 0) xp.gexp[lane / LPG] = ldexpf(1.f, -f);
+    if (j == 0) xp.gexp[lane / LPG] = group_unscale(m, f);
 }
 
 // The 8 activations lane l of a wave-local set-up converts: block l of the
@@ -1461,6 +1454,7 @@ int launch_i4_matvec_generic(const uint8_t *w, const float *x, float *y, int out
                              hipStream_t stream) {
     if (out_dim < 1 || in_dim < 1) return kBadShape;
     if (group_size < 2 || (group_size & 1)) return kBadGroup;
+    if (!w || !x || !y) return kBadShape;  // nothing is launched on a null operand
     const int gb = i4_group_bytes(group_size);
     const int Gr = i4_groups(in_dim, group_size);
     const unsigned long long rb = i4_row_bytes(in_dim, group_size);
@@ -1475,6 +1469,7 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
                      hipStream_t stream) {
     if (out_dim < 1 || in_dim < 1) return kBadShape;
     if (group_size < 2 || (group_size & 1)) return kBadGroup;
+    if (!w || !x || !y) return kBadShape;  // nothing is launched on a null operand
     const size_t rb = i4_row_bytes(in_dim, group_size);
     const bool fast_group = (group_size % 8 == 0) && group_size >= 40;
     if (!fast_group || rb * kTile * 2 >= (1ull << 31))
@@ -1530,8 +1525,9 @@ int launch_i4_matvec_group(int n, const uint8_t *const *w, float *const *y, cons
                            int in_dim, int group_size, hipStream_t stream) {
     if (n < 1 || n > kMaxGroup || in_dim < 1) return kBadShape;
     if (group_size < 2 || (group_size & 1)) return kBadGroup;
+    if (!x) return kBadShape;
     for (int j = 0; j < n; ++j)
-        if (out_dim[j] < 1) return kBadShape;
+        if (out_dim[j] < 1 || !w[j] || !y[j]) return kBadShape;
     const size_t rb = i4_row_bytes(in_dim, group_size);
     const int T = static_cast<int>((rb + kChunk - 1) / kChunk);
     {  // the set kernel takes all n in one launch where it applies (rows sharing x)

@@ -69,13 +69,6 @@ struct SetArgs {
 // Per half-group (32 elements) LDS also holds sum(X) (as a float) and 2^-f.
 constexpr int kBlockBytes = 24;  // one 8-element block: 3 digit planes x (even, odd) dwords
 
-__device__ inline int group_exponent(float m) {
-    if (!(m > 0.f)) return 0;
-    int e;
-    frexpf(m, &e);  // m in [2^(e-1), 2^e)
-    return min(22 - e, 149);
-}
-
 // Round to nearest (ties upward: floor(v + 0.5)), one instruction.
 __device__ inline int round_int(float v) {
     int r;
@@ -88,15 +81,15 @@ __device__ inline int round_int(float v) {
 // chunks of a half-group half of one.
 __device__ __forceinline__ void stage_x(float4 q, int c, int Kc, int C, unsigned char *xp, float2 *hs) {
     if (c >= Kc) q = make_float4(0.f, 0.f, 0.f, 0.f);  // past K: zeros
-    float m = fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w)));
+    float m = fmaxf(fmaxf(abs_or_inf(q.x), abs_or_inf(q.y)), fmaxf(abs_or_inf(q.z), abs_or_inf(q.w)));
     m = fmaxf(m, dpp_f<kDppXor1>(m));
     m = fmaxf(m, dpp_f<kDppXor2>(m));
     m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
-    m = fmaxf(m, dpp_f<kDppMirror>(m));  // the group's largest |x|, in all 16 lanes
+    m = fmaxf(m, dpp_f<kDppMirror>(m));  // the group's largest |x| (inf if any is not finite), in all 16 lanes
     const int f = group_exponent(m);
-    const float up = ldexpf(1.f, f);     // exact power of two (f <= 149)
-    const unsigned X0 = round_int(q.x * up), X1 = round_int(q.y * up);
-    const unsigned X2 = round_int(q.z * up), X3 = round_int(q.w * up);
+    // the value itself is scaled (2^f is not a finite float for f >= 128; x * 2^f is exact)
+    const unsigned X0 = round_int(ldexpf(q.x, f)), X1 = round_int(ldexpf(q.y, f));
+    const unsigned X2 = round_int(ldexpf(q.z, f)), X3 = round_int(ldexpf(q.w, f));
     int sum = static_cast<int>(X0 + X1 + X2 + X3);
     sum += dpp_i<kDppXor1>(sum);
     sum += dpp_i<kDppXor2>(sum);
@@ -111,7 +104,7 @@ __device__ __forceinline__ void stage_x(float4 q, int c, int Kc, int C, unsigned
         *reinterpret_cast<unsigned short *>(blk + 8 * p + 4) =
             static_cast<unsigned short>(__builtin_amdgcn_perm(X3, X1, sel));
     }
-    if ((c & 7) == 0) hs[c >> 3] = make_float2(static_cast<float>(sum), ldexpf(1.f, -f));
+    if ((c & 7) == 0) hs[c >> 3] = make_float2(static_cast<float>(sum), group_unscale(m, f));
 }
 
 // scale * 2^-f * (sum(q * X) - zero * sum(X)) over one half-group: the 16 code bytes cd,
@@ -134,7 +127,10 @@ __device__ __forceinline__ float half_group_int(const v4i &cd, unsigned hd, cons
     }
     const float V = fmaf(static_cast<float>(a2), 65536.f, static_cast<float>(a0 + a1 * 256u));
     const float sc = half_bits(hd), z = half_bits(hd >> 16);
-    return (sc * hs.y) * fmaf(-z, hs.x, V);
+    // 2^-f times the exact integer sum first: for tiny activations (f > 126) 2^-f is subnormal and
+    // sc * 2^-f could lose its digits, while 2^-f * (...) is still a normal float; for normal
+    // products both orders round once and give the same bits.
+    return sc * (hs.y * fmaf(-z, hs.x, V));
 }
 
 // Rows of at most 32 half-groups (S = 0): R rows per half-wave, 2R per wave, 8R per
@@ -481,7 +477,7 @@ int launch_i4_matvec_set(int n, const I4Mat *mats, int group_size, hipStream_t s
     if (n < 0 || (n > 0 && !mats)) return kBadShape;
     if (group_size < 2 || (group_size & 1)) return kBadGroup;
     for (int i = 0; i < n; ++i)
-        if (mats[i].M < 1 || mats[i].K < 1) return kBadShape;
+        if (mats[i].M < 1 || mats[i].K < 1 || !mats[i].w || !mats[i].x || !mats[i].y) return kBadShape;
     // the matrices the set kernel takes, in launches of up to kSetMaxMats; the others alone
     I4Mat batch[kSetMaxMats];
     int shape[kSetMaxMats], nb = 0;

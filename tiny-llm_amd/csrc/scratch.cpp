@@ -20,6 +20,7 @@
 //     not grow: a request beyond them is kTooLarge, which the launchers treat as
 //     "this kernel does not fit" (split-K falls back to a non-split kernel).
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -35,7 +36,15 @@ struct ScratchBuf {
     bool captured = false;  // recorded into a graph: retire on growth, never free
 };
 
+namespace {
+std::atomic<long> g_live_sets{0};
+}  // namespace
+
 struct ScratchSet {
+    ScratchSet() { ++g_live_sets; }
+    ~ScratchSet() { --g_live_sets; }
+    ScratchSet(const ScratchSet &) = delete;
+    ScratchSet &operator=(const ScratchSet &) = delete;
     std::mutex mu;
     ScratchBuf split;  // split-K exchange slots / arrival counters: zero between launches
     ScratchBuf xws;    // prefill workspace
@@ -153,14 +162,21 @@ void scratch_forget_stream(hipStream_t s) {
         set = it->second;
         g_streams.erase(it);
     }
-    // Buffers a foreign graph recorded stay allocated (that graph may outlive the stream).
-    std::lock_guard<std::mutex> lock(set->mu);
-    if (set->split.captured || set->xws.captured || !set->retired.empty()) return;  // leaked on purpose
-    if (set->split.p) (void)hipFree(set->split.p);
-    if (set->xws.p) (void)hipFree(set->xws.p);
-    set->split = ScratchBuf{};
-    set->xws = ScratchBuf{};
+    // Buffers a foreign graph recorded stay allocated (that graph may outlive the stream), and
+    // so does their set. Otherwise the buffers and the set go: the stream is being destroyed,
+    // so no other thread may still launch on it (the caller's contract, as for the stream).
+    {
+        std::lock_guard<std::mutex> lock(set->mu);
+        if (set->split.captured || set->xws.captured || !set->retired.empty()) return;  // leaked on purpose
+        if (set->split.p) (void)hipFree(set->split.p);
+        if (set->xws.p) (void)hipFree(set->xws.p);
+        set->split = ScratchBuf{};
+        set->xws = ScratchBuf{};
+    }
+    delete set;
 }
+
+long scratch_live_sets() { return g_live_sets.load(); }
 
 ScratchStats scratch_stats(hipStream_t s) {
     ScratchStats st{};

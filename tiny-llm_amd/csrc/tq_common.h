@@ -45,7 +45,7 @@ inline void check_hip(hipError_t e, const char *what) {
 // Error codes returned by the device-pointer entry points.
 enum Status : int {
     kOk = 0,
-    kBadShape = -1,      // a dimension is < 1, or in_dim % 4 != 0 for VQ2
+    kBadShape = -1,      // a dimension is < 1, in_dim % 4 != 0 for VQ2, or an operand pointer is null
     kBadGroup = -2,      // group_size is odd or < 2
     kTooLarge = -3,      // a byte offset does not fit the 32-bit buffer range
     kLaunchFailed = -4,  // hipGetLastError after the launch was not hipSuccess
@@ -145,6 +145,7 @@ ScratchSet *scratch_set_new();
 ScratchSet *scratch_set_fixed(void *xws, size_t xws_bytes);
 void scratch_set_free(ScratchSet *set);  // the caller has synchronised every launch that used it
 void scratch_forget_stream(hipStream_t s);  // the stream is being destroyed (synchronised)
+long scratch_live_sets();                    // ScratchSet objects alive (bookkeeping checks)
 class ScratchScope {
   public:
     explicit ScratchScope(ScratchSet *set);

@@ -731,6 +731,7 @@ __global__ __launch_bounds__(64 * kTabWaves) void vq2_matvec_table(const uint8_t
 
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream) {
     if (out_dim < 1 || in_dim < kVq2Dim || in_dim % kVq2Dim) return kBadShape;
+    if (!w || !x || !y) return kBadShape;  // nothing is launched on a null operand
     const int cus = device_cu_count();
     const bool aligned = (in_dim % 16) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0;
     if (rows_kernel_takes(w, out_dim, in_dim)) {
@@ -780,7 +781,8 @@ int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, i
 int launch_vq2_matvec_set(int n, const I4Mat *mats, hipStream_t stream) {
     if (n < 0 || (n > 0 && !mats)) return kBadShape;
     for (int i = 0; i < n; ++i)
-        if (mats[i].M < 1 || mats[i].K < kVq2Dim || mats[i].K % kVq2Dim) return kBadShape;
+        if (mats[i].M < 1 || mats[i].K < kVq2Dim || mats[i].K % kVq2Dim || !mats[i].w || !mats[i].x || !mats[i].y)
+            return kBadShape;
     Vq2SetArgs a{};
     int nb = 0, blocks = 0;
     long long lookups = 0;
