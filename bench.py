@@ -570,9 +570,7 @@ def host_call(tq, reps=50):
 
 def engine(tq, steps, warmup):
     """Decode engine tokens/s on a synthetic Qwen2.5-0.5B-shaped dense i4 model held in memory."""
-    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
-    import tqwen_files
-    img, cfg, _ = tqwen_files.dense_i4_model(hidden=HIDDEN, n_heads=14, n_kv_heads=2, head_dim=64, inter=INTER,
+    img, cfg, _ = tq.tqwen_synth.dense_i4_model(hidden=HIDDEN, n_heads=14, n_kv_heads=2, head_dim=64, inter=INTER,
                                              vocab=VOCAB, layers=N_LAYERS, group_size=G, seed=11,
                                              max_seq_len=4096)
     m = tq.ModelFile.from_image(img)
@@ -587,28 +585,14 @@ def engine(tq, steps, warmup):
     for _ in range(steps):
         tok = eng.step(tok)
     dt = (time.perf_counter() - t0) / steps
+    got = replay(eng, ENGINE_CHECK_TOKENS)  # outside the timed region, for the correctness gate
     eng.close()
     m.close()
-    cpu = None
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    import oracle
-    ref = oracle.ref_lib()
-    if ref is not None:  # the reference's own CPU decode (QwenModel::forward_token, `ref` kernels) on the same file
-        import tempfile
-        with tempfile.TemporaryDirectory() as d:
-            path = os.path.join(d, "bench.tqwen")
-            with open(path, "wb") as f:
-                f.write(img)
-            err = ctypes.create_string_buffer(512)
-            if ref.tqref_decode_create(path.encode(), 16, err, len(err)):
-                ref.tqref_decode_step(1)
-                n, t0 = 3, time.perf_counter()
-                for t in range(n):
-                    ref.tqref_decode_step(t + 2)
-                cpu = {"ms_per_token": round((time.perf_counter() - t0) / n * 1e3, 1), "tokens": n, "cores": 1,
-                       "kind": "reference"}
+    # the reference's own CPU decode (QwenModel::forward_token, `ref` kernels) on the same file: its
+    # time per token (a CPU baseline) and its logits for the gate
+    cpu, want = ref_decode(img, ENGINE_CHECK_TOKENS, timed=3)
     # the same shape as a BiIP-rotated VQ2 file (VQ2 projections, fp16 vectors, compact-i4 embedding)
-    img2, _, _ = tqwen_files.dense_i4_model(hidden=HIDDEN, n_heads=14, n_kv_heads=2, head_dim=64, inter=INTER,
+    img2, _, _ = tq.tqwen_synth.dense_i4_model(hidden=HIDDEN, n_heads=14, n_kv_heads=2, head_dim=64, inter=INTER,
                                             vocab=VOCAB, layers=N_LAYERS, group_size=G, seed=12, max_seq_len=4096,
                                             vq2=True, rotated=True)
     m2 = tq.ModelFile.from_image(img2)
@@ -620,14 +604,85 @@ def engine(tq, steps, warmup):
     for _ in range(steps):
         tok = eng2.step(tok)
     dt2 = (time.perf_counter() - t0) / steps
+    got2 = replay(eng2, ENGINE_CHECK_TOKENS[:2])
     eng2.close()
     m2.close()
+    _, want2 = ref_decode(img2, ENGINE_CHECK_TOKENS[:2], timed=0)
     vq2 = {"model": "the same shape as a BiIP-rotated VQ2 file", "file_bytes": len(img2),
            "ms_per_token": round(dt2 * 1e3, 4), "tokens_per_s": round(1.0 / dt2, 1)}
-    return {"model": "Qwen2.5-0.5B-shaped dense i4 HQQ@64 (24 layers, hidden 896, 14/2 heads, inter 4864, "
-                     "vocab 151936, tied i4 embedding), random weights", "vq2_rotated": vq2,
-            "file_bytes": len(img), "upload_s": round(upload_s, 3), "positions": f"{warmup}..{warmup + steps - 1}",
-            "ms_per_token": round(dt * 1e3, 4), "tokens_per_s": round(1.0 / dt, 1), "cpu_reference": cpu}
+    rec = {"model": "Qwen2.5-0.5B-shaped dense i4 HQQ@64 (24 layers, hidden 896, 14/2 heads, inter 4864, "
+                    "vocab 151936, tied i4 embedding), random weights", "vq2_rotated": vq2,
+           "file_bytes": len(img), "upload_s": round(upload_s, 3), "positions": f"{warmup}..{warmup + steps - 1}",
+           "ms_per_token": round(dt * 1e3, 4), "tokens_per_s": round(1.0 / dt, 1), "cpu_reference": cpu}
+    if want is not None:
+        settle(rec, check_logits(got, want))
+    if want2 is not None:
+        settle(vq2, check_logits(got2, want2))
+    return rec
+
+
+ENGINE_CHECK_TOKENS = (1, 2, 3, 4)
+
+
+def replay(eng, tokens):
+    """The engine from position 0 again on a fixed token sequence: (next token, logits) per step."""
+    eng.reset()
+    out = []
+    for t in tokens:
+        nxt = eng.step(t)
+        out.append((nxt, eng.logits().copy()))
+    return out
+
+
+def ref_decode(img, tokens, timed):
+    """The reference's own CPU decode (oracle/_ref: QwenModel::forward_token with the `ref` kernels,
+    one thread) of a model image on a token sequence: its ms per token over the last `timed`
+    steps (None when timed is 0), and its logits per step. (None, None) when the compiled reference
+    is absent."""
+    sys.path.insert(0, REPO)
+    import oracle  # the CPU baseline and checker
+    ref = oracle.ref_lib()
+    if ref is None:
+        return None, None
+    import tempfile
+    logits, t0 = [], None
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "bench.tqwen")
+        with open(path, "wb") as f:
+            f.write(img)
+        err = ctypes.create_string_buffer(512)
+        if not ref.tqref_decode_create(path.encode(), 16, err, len(err)):
+            log(f"[bench] reference decode unavailable: {err.value.decode(errors='replace')}")
+            return None, None
+        for i, t in enumerate(tokens):
+            if i == len(tokens) - timed:
+                t0 = time.perf_counter()
+            ref.tqref_decode_step(t)
+            lg = np.empty(VOCAB, np.float32)
+            ref.tqref_decode_logits(lg.ctypes.data, VOCAB)
+            logits.append(lg)
+        el = time.perf_counter() - t0 if timed else 0.0
+    cpu = None
+    if timed:
+        cpu = {"ms_per_token": round(el / timed * 1e3, 1), "tokens": timed, "cores": 1, "kind": "reference"}
+    return cpu, logits
+
+
+def check_logits(got, want):
+    """Engine logits per step against the reference decode's: rel L2 <= 1e-4 (the decode tests' bar:
+    fp32 sums where the reference sums in double, a two-pass softmax), and the same next token
+    wherever the reference's top two logits are more than 1e-3 of the logit scale apart."""
+    checks = []
+    for (tok, g), w in zip(got, want):
+        c = compare(g, w, ENGINE_BAR, max_bar=1e-2)
+        top = np.sort(w)[-2:]
+        if top[1] - top[0] > 1e-3 * np.max(np.abs(w)) and tok != int(np.argmax(w)):
+            c["verdict"] = "FAIL"
+        checks.append(c)
+    out = worst(checks)
+    out["tokens"] = len(checks)
+    out["bar"] = f"rel L2 <= {ENGINE_BAR:g} per step, same greedy token where the top-2 gap > 1e-3 of the scale"
+    return out
 
 
 def cpu_baseline(work, budget_s=12.0):
@@ -688,7 +743,39 @@ def cpu_baseline(work, budget_s=12.0):
     return {"value": round(work.bytes / (ms * 1e-3) / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
             "ms_per_step": round(ms, 2), "cpu": cpu, "host_cpus": host_cpus, "usable_cpus": usable,
             "threads_why": "all usable CPUs up to the 16-thread share a one-GPU job has on the GPU box",
-            "sample": f"{n} full steps (all 169 matvecs, {work.bytes / 1e6:.0f} MB), rows split over {threads} threads"}
+            "sample": f"{n} full steps (all 169 matvecs, {work.bytes / 1e6:.0f} MB), rows split over {threads} threads"}, outs
+
+
+def gate(pending, threads=16):
+    """The correctness gate over the outputs the timed sections kept: each against the CPU checker
+    (the restatement of the reference's ref kernels, pinned bit for bit to the compiled reference;
+    row-split over threads). i4 and VQ2 matvecs at the matvec bar, the prefill GEMM at the prefill
+    bar on every 97th row (every row at 32 tokens)."""
+    sys.path.insert(0, REPO)
+    import oracle  # the checker
+    for rec, kind, args, got in pending:
+        if kind == "i4":
+            w, x, M, K = args
+            c = compare(got, oracle.matvec_i4(w, x, M, K, G, threads=threads), MATVEC_BAR)
+        elif kind == "vq2":
+            w, x, M, K = args
+            c = compare(got, oracle.matvec_vq2(w, x, M, K, threads=threads), MATVEC_BAR)
+        else:
+            w, x, M, K, n = args
+            rows = np.arange(M) if n <= 32 else np.arange(0, M, 97)
+            rb = w.size // M
+            want = oracle.matmul_i4(np.ascontiguousarray(w.reshape(M, rb)[rows]).ravel(), x, rows.size, K, n, G,
+                                    threads=threads)
+            c = compare(got.reshape(n, M)[:, rows], want, PREFILL_BAR)
+            c["rows_checked"] = int(rows.size)
+        settle(rec, c)
+
+
+def check_step(work, ref_outs):
+    """The step's 169 outputs (as its last timed launches left them) against the reference outputs
+    the CPU baseline computed on the same inputs."""
+    got = work.download_outputs()
+    return worst([compare(g, w, MATVEC_BAR) for g, w in zip(got, ref_outs)])
 
 
 def main():
@@ -718,6 +805,13 @@ def main():
         sys.exit(2)
 
     tq = load_pkg()
+    t_section = [time.perf_counter()]
+
+    def took(name):  # wall-clock seconds of each section, on stderr
+        now = time.perf_counter()
+        log(f"[bench] ({name}: {now - t_section[0]:.1f} s)")
+        t_section[0] = now
+
     if tq.device_count() < 1:
         print("no HIP device visible", file=sys.stderr)
         sys.exit(1)
@@ -754,14 +848,26 @@ def main():
           "launches_per_step": len(work.rt_steps[0])}
     log(f"[bench] step in the runtime's call order ({rt['launches_per_step']} launches): {ms_rt * 1e3:.1f} us, "
         f"{rt['value']} GB/s")
+    took("steps")
     ls = layer_set(tq, work, stream, max(2, args.steps // N_COPIES))
     log(f"[bench] layer set: {ls['us']} us as one launch ({ls['us_graph']} us from a HIP graph), "
         f"{ls['us_4launch']} us as 4 dependency-ordered launches")
+    took("layer set")
+    step_outputs = work.download_outputs()  # the outputs of the set launches just timed, for the gate
     graph = None
     if not args.no_graph:  # the step captured into one HIP graph (three steps, one per copy) and replayed
         ms_graph = time_graph(tq, work.steps(N_COPIES), max(1, args.steps // N_COPIES), 1, stream) / N_COPIES
         graph = {"ms_per_step": round(ms_graph, 4), "value": round(work.bytes / (ms_graph * 1e-3) / 1e9, 1)}
         log(f"[bench] step as a HIP graph replay: {ms_graph * 1e3:.1f} us, {graph['value']} GB/s")
+    # The host-pointer call before the sections that allocate and free hundreds of weight copies:
+    # measured after them (the VQ2 section's 716), its 4864x896 call once took 132 us against
+    # 25-27 us in a fresh process, with the same HIP-event split (not reproduced in isolation).
+    host = None if args.no_host_call else host_call(tq)
+    if host:
+        log(f"[bench] host-pointer call (x H2D + kernel + y D2H, weights cached): " +
+            ", ".join(f"{r['shape']} {r['us']} us (upload {r['split_us']['x_upload']}, kernel "
+                      f"{r['split_us']['kernel']}, download {r['split_us']['y_download']})" for r in host))
+        took("host call")
     roof = roofline(ls["us"])
     log(f"[bench] dominant kernel (set): {roof['avg_launch_us']} us per launch, {roof['achieved']} GB/s "
         f"({100 * roof['frac']:.1f}% of 8 TB/s)")
@@ -769,48 +875,75 @@ def main():
     if ceil:
         log(f"[bench] ceilings: stream read {ceil['stream_read_gbs']} GB/s, empty launch {ceil['empty_launch_us']} us, "
             f"fp16 MFMA {ceil['mfma_f16_tflops']} TFLOP/s")
+        took("ceilings")
 
     head = None if args.no_headline else headline(tq, stream)
     if head:
         log(f"[bench] headline 151936x2560: {head['us']} us, {head['gbs']} GB/s ({100 * head['frac']:.1f}% of 8 TB/s)")
+        took("headline")
     c0 = None if args.no_configs2 else configs0(tq, stream)
     if c0:
         log(f"[bench] configs[0] matvec {c0['shape']}: {c0['us']} us, {c0['gbs']} GB/s (one cold launch)")
     c2 = None if args.no_configs2 else configs2(tq, stream)
     if c2:
         log("[bench] configs[2] matvecs: " + ", ".join(f"{r['shape']} {r['us']} us {r['gbs']} GB/s" for r in c2))
+        took("configs0/2")
     pre = None if args.no_prefill else prefill(tq, stream)
     if pre:
         for r in pre["tokens"]:
             log(f"[bench] prefill 9728x2560 x{r['tokens']}: {r['us']} us, {r['tflops']} TFLOP/s "
                 f"({100 * r['mfma_frac']:.1f}% of dense fp16 MFMA)")
+        took("prefill")
 
     v = None if args.no_vq2 else vq2(tq, stream)
     if v:
         log("[bench] vq2 matvec: " + ", ".join(f"{r['shape']} {r['us']} us {r['gbs']} GB/s" for r in v))
-    host = None if args.no_host_call else host_call(tq)
-    if host:
-        log(f"[bench] host-pointer call (x H2D + kernel + y D2H, weights cached): " +
-            ", ".join(f"{r['shape']} {r['us']} us" for r in host))
+        took("vq2")
 
     eng = None if args.no_engine else engine(tq, args.steps, args.warmup)
     if eng:
         log(f"[bench] decode engine: {eng['ms_per_token']} ms/token, {eng['tokens_per_s']} tokens/s "
             f"(positions {eng['positions']}); rotated VQ2 file: {eng['vq2_rotated']['ms_per_token']} ms/token")
+        took("engine")
 
-    cpu = None
+    # The CPU leg: the reference's own kernels timed on the host (the CPU baseline), then the
+    # correctness gate with the reference outputs and the checker.
+    cpu, verify = None, None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(work)
+        cpu, ref_outs = cpu_baseline(work)
         log(f"[bench] cpu baseline ({cpu['kind']}, {cpu['cores']} threads of {cpu['host_cpus']}): "
             f"{cpu['ms_per_step']} ms/step, {cpu['value']} GB/s")
+        took("cpu baseline")
+        step_check = worst([compare(g, w, MATVEC_BAR) for g, w in zip(step_outputs, ref_outs)])
+        gate(PENDING)
+        verify = {"step": step_check}
+        for name, sec in (("headline", head), ("configs0", c0)):
+            if sec:
+                verify[name] = sec["verify"]
+        if c2:
+            verify["configs2"] = worst([r["verify"] for r in c2])
+        if pre:
+            verify["prefill"] = worst([r["verify"] for r in pre["tokens"]])
+        if v:
+            verify["vq2"] = worst([r["verify"] for r in v])
+        if eng and "verify" in eng:
+            verify["engine"] = eng["verify"]
+        if eng and "verify" in eng["vq2_rotated"]:
+            verify["engine_vq2_rotated"] = eng["vq2_rotated"]["verify"]
+        for name, c in verify.items():
+            log(f"[bench] verify {name}: {c['verdict']} (rel L2 {c['rel_l2']}, max rel {c['max_rel']})")
+        took("gate")
+        if step_check["verdict"] != "PASS":  # a step whose outputs fail the gate has no figure
+            value, ms_step = None, None
 
     out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": None if value is None else round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": None if ms_step is None else round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "u4 codes x f32 activations (i8 digit planes of the activations, exact integer "
                  "dot products, f32 epilogue)",
         "data": "synthetic (BASELINE distributions, seeded); weights read cold (3 rotated copies)",
-        "pct_of_peak": round(100 * value / PEAK_GBS, 2),
+        "pct_of_peak": None if value is None else round(100 * value / PEAK_GBS, 2),
         "us_per_layer_set": ls["us"],
         "layer_set": ls,
         "step_runtime_order": rt,
@@ -830,6 +963,7 @@ def main():
         "host_call": host,
         "engine": eng,
         "cpu_baseline": cpu,
+        "verify": verify,
     }
     print(json.dumps(out), flush=True)
 

@@ -9,8 +9,9 @@ import ctypes
 import numpy as np
 import pytest
 
-import tqwen_files as tf
-from conftest import rel_l2
+from conftest import load_package, rel_l2
+
+tf = load_package().tqwen_synth  # synthetic .tqwen images
 
 CASES = {
     "qwen2_gqa7": dict(hidden=256, n_heads=7, n_kv_heads=1, head_dim=64, inter=512, vocab=300, layers=2),

@@ -10,8 +10,9 @@ bit-identical."""
 import numpy as np
 import pytest
 
-import tqwen_files as tf
-from conftest import rel_l2
+from conftest import load_package, rel_l2
+
+tf = load_package().tqwen_synth  # synthetic .tqwen images
 
 pytestmark = pytest.mark.gpu
 

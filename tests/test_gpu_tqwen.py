@@ -8,8 +8,9 @@ and match the oracle on the file's bytes (rel L2 <= 1e-5, embeddings bit-exact).
 import numpy as np
 import pytest
 
-import tqwen_files as tf
-from conftest import rel_l2
+from conftest import load_package, rel_l2
+
+tf = load_package().tqwen_synth  # synthetic .tqwen images
 
 pytestmark = pytest.mark.gpu
 

@@ -19,7 +19,10 @@ import re
 import numpy as np
 import pytest
 
-import tqwen_files as tf
+from conftest import load_package
+
+tf = load_package().tqwen_synth  # synthetic .tqwen images
+
 
 
 def write(tmp_path, image, name="m.tqwen"):

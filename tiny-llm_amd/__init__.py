@@ -13,6 +13,7 @@ The directory name is not a valid module name, so load it by path::
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
 import weakref
 
@@ -20,6 +21,18 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtqhip.so")
+
+
+def _load_sibling(name: str):
+    """A module file of this directory (the directory is loaded by path, not as a package)."""
+    spec = importlib.util.spec_from_file_location(f"tiny_llm_amd_{name}", os.path.join(HERE, name + ".py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+# synthetic .tqwen model images (the decode engine's benchmark and smoke models, the loader tests' files)
+tqwen_synth = _load_sibling("tqwen_synth")
 
 OK, EBADSHAPE, EBADGROUP, ETOOLARGE, ELAUNCH, EFILE, EHIP, ENOSCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
 NOALLOC_SCRATCH_BYTES = 16 << 20  # TQHIP_NOALLOC_SCRATCH_BYTES

@@ -1,4 +1,5 @@
-"""Writes .tqwen files for the loader tests (test helper, not a test module).
+"""Writes synthetic .tqwen model images: the models the decode engine is benchmarked and
+smoke-tested on (random weights of a named architecture) and the files the loader tests feed.
 
 The layout is runtime/tiny_format.h:219-315 of tiny-llm: a 192-byte header, a
 table of 120-byte entries, then tensor payloads at 64-byte aligned offsets; the
