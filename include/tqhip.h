@@ -316,13 +316,28 @@ void tqhip_model_free(void *model);                   /* frees the HBM copy too 
  * step: QwenModel::forward_token (runtime/qwen_forward_token.cpp:83) at position
  * seq_len: returns the argmax token of the logits, or TQHIP_EBADSHAPE for a token outside
  * [0, vocab) or a full cache (the reference aborts there), TQHIP_ELAUNCH on a HIP failure.
- * logits: device pointer to the last step's vocab_size logits (valid until destroy). */
+ * logits: device pointer to the last step's vocab_size logits (valid until destroy).
+ *
+ * Engines of i4 files whose projections the set kernel takes (group size 64, no rotations) run
+ * each layer's residual adds, RMSNorms and SwiGLU inside its projection launches ("fused"),
+ * and, with TQHIP_DECODE_FLOW=1 in the environment at create, run a step as one cooperative
+ * launch of the whole layer stack whose phases wait for each other's outputs through tagged
+ * vectors in HBM, then the lm_head and the argmax ("flow"; the default is the graph, which is
+ * as fast or faster on MI355X). The flow step gives the graph step's logits bit for bit; if
+ * one of its waits runs out (100 ms), the engine reports it on stderr, runs that token through
+ * the graph and keeps to the graph. */
 int tqhip_decode_create(void *model, int max_seq_len, char *err, int err_len, void **engine);
 int tqhip_decode_step(void *engine, int token_id);
 void tqhip_decode_reset(void *engine);      /* back to position 0 (KvCache::reset) */
 void tqhip_decode_destroy(void *engine);
 const float *tqhip_decode_logits(const void *engine);
 int tqhip_decode_seq_len(const void *engine);
+/* How the engine runs a step (no counterpart in the reference): TQHIP_DECODE_FUSED |
+ * TQHIP_DECODE_FLOW | TQHIP_DECODE_EAGER bits, -1 for a null engine. */
+#define TQHIP_DECODE_FUSED 1
+#define TQHIP_DECODE_FLOW 2
+#define TQHIP_DECODE_EAGER 4
+int tqhip_decode_mode(const void *engine);
 
 /* ---- 6. synthetic inputs (portable generator, identical on every host) -- */
 

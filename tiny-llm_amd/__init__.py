@@ -171,6 +171,7 @@ _SIGS = {
     "tqhip_decode_destroy": (None, [_vp]),
     "tqhip_decode_logits": (_vp, [_vp]),
     "tqhip_decode_seq_len": (_i, [_vp]),
+    "tqhip_decode_mode": (_i, [_vp]),
     # synthetic inputs
     "tq_synth_seed": (ctypes.c_uint64, [ctypes.c_uint64, _i, ctypes.c_char_p]),
     "tq_synth_i4": (None, [_vp, _i, _i, _i, ctypes.c_uint64, ctypes.c_float, ctypes.c_float,
@@ -675,6 +676,12 @@ class DecodeEngine:
     @property
     def seq_len(self) -> int:
         return int(lib().tqhip_decode_seq_len(self._h))
+
+    @property
+    def mode(self) -> set:
+        """How a step runs: a subset of {"fused", "flow", "eager"} (tqhip_decode_mode)."""
+        m = int(lib().tqhip_decode_mode(self._h))
+        return {name for bit, name in ((1, "fused"), (2, "flow"), (4, "eager")) if m & bit}
 
     def close(self) -> None:
         if getattr(self, "_h", None):

@@ -30,6 +30,8 @@
 #include <string>
 #include <vector>
 
+#include "decode_attn.h"
+#include "decode_flow.h"
 #include "tq_common.h"
 
 // The elementwise steps below round every product and sum separately, as the
@@ -37,12 +39,11 @@
 #pragma clang fp contract(off)
 
 namespace tqhip {
+
 namespace {
 
 constexpr int kNormThreads = 1024;
 constexpr int kMaxHidden = 16 * kNormThreads;  // values per thread kept in registers
-constexpr int kAttnThreads = 256;
-constexpr int kAttnChunk = 4096;               // scores of one chunk of positions in LDS
 constexpr int kArgmaxThreads = 256, kArgmaxPerThread = 8;
 constexpr int kArgmaxPerBlock = kArgmaxThreads * kArgmaxPerThread;
 
@@ -55,17 +56,6 @@ __device__ double block_sum(double v, double *red) {
     __syncthreads();
     double t = 0.0;
     for (int w = 0; w < NT / 64; ++w) t += red[w];
-    __syncthreads();
-    return t;
-}
-
-template <int NT>
-__device__ float block_max(float v, float *red) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int w = 1; w < NT / 64; ++w) t = fmaxf(t, red[w]);
     __syncthreads();
     return t;
 }
@@ -128,199 +118,27 @@ __global__ void embed_f32_row(const float *table, const int *token, float *out, 
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = table[base + i];
 }
 
-// 1 / rms of one head in LDS (rmsnorm_ref on a head slice), summed by one wave.
-__device__ float head_rms_scale(const float *x, int hd, float eps) {
-    const int lane = threadIdx.x & 63;
-    double ss = 0.0;
-    for (int i = lane; i < hd; i += 64) ss += static_cast<double>(x[i]) * static_cast<double>(x[i]);
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    return 1.0f / sqrtf(static_cast<float>(ss / hd) + eps);
-}
-
-// One workgroup per query head: finishes its q head and the k / v head of its
-// group from the raw projections (biases, optional per-head RMSNorm for q and
-// k, RoPE as rope_ref, kernels/rope/rope_ref.cpp: pairs (i, i + half),
-// inv_freq = theta^(-2i/d), angle = pos * inv_freq), writes k and v at `*pos`
-// into the cache (the group's first head only), then attends over positions
-// 0..pos (attention_decode_ref, kernels/attention/attention_decode_ref.cpp:
-// scores q.k * scale, softmax, sum of p * v). Every head of a group computes
-// the new k / v itself and uses its own copy at position pos, so no head reads
-// a cache row another workgroup is writing.
-//
-// Latency is the cost here (14 workgroups at Qwen2.5-0.5B), so the memory
-// round trips are overlapped: the q / k / v loads, thread t's key row for
-// position t (head_dim <= 128) and the first eight value rows of its slice are
-// all issued at entry, and the RoPE angles are computed while they are in
-// flight. Thread j scores position j of a chunk of up to 4096 positions; the
-// softmax over a chunk is max / exp / sum, and across chunks the running max
-// rescales the partial sums. Thread t accumulates dimension t % hd over every
-// (NT / hd)-th position, in position order.
+// One workgroup per query head: attention_head (decode_attn.h) on the raw q / k / v
+// projections, biases added at entry.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_step(
     const float *q, const float *k, const float *v, const float *qb, const float *kb, const float *vb,
     const float *qn, const float *kn, float *kcache, float *vcache, float *out, const int *pos_ptr, int heads_per_kv,
     int max_seq, float theta, float eps, float scale) {
-    constexpr int hd = HD, half = HD / 2, slices = kAttnThreads / HD;
-    constexpr bool kPrefetchKey = HD <= 128;
-    __shared__ __align__(16) float qs[HD];
-    __shared__ __align__(16) float ks[HD];
-    __shared__ float vs[HD];
-    __shared__ float sc[kAttnChunk];
-    __shared__ float part[kAttnThreads];
-    __shared__ float norm_scale[2];
-    __shared__ double dred[kAttnThreads / 64];
-    __shared__ float fred[kAttnThreads / 64];
+    __shared__ AttnShared sh;
     const int t = threadIdx.x;
     const int head = blockIdx.x, kvh = head / heads_per_kv;
-    const int pos = *pos_ptr, seq = pos + 1;
-    const int d = t % hd, slice = t / hd;
-    const float *kh = kcache + static_cast<size_t>(kvh) * max_seq * hd;
-    const float *vh = vcache + static_cast<size_t>(kvh) * max_seq * hd;
-
-    float qv = 0.0f, kv = 0.0f, vv = 0.0f;
-    if (t < hd) {
-        const int qi = head * hd + t, ki = kvh * hd + t;
-        qv = qb ? q[qi] + qb[qi] : q[qi];
-        kv = kb ? k[ki] + kb[ki] : k[ki];
-        vv = vb ? v[ki] + vb[ki] : v[ki];
-    }
-    float4 kreg[kPrefetchKey ? HD / 4 : 1];
-    const bool key_pre = kPrefetchKey && t < seq && t != pos && t < kAttnChunk;
-    if constexpr (kPrefetchKey) {
-        if (key_pre) {
-            const float4 *kr = reinterpret_cast<const float4 *>(kh + static_cast<size_t>(t) * hd);
-#pragma unroll
-            for (int i = 0; i < HD / 4; ++i) kreg[i] = kr[i];
+    const auto fetch = [&](float &qv, float &kv, float &vv) {
+        if (t < HD) {
+            const int qi = head * HD + t, ki = kvh * HD + t;
+            qv = qb ? q[qi] + qb[qi] : q[qi];
+            kv = kb ? k[ki] + kb[ki] : k[ki];
+            vv = vb ? v[ki] + vb[ki] : v[ki];
         }
-    }
-    float vreg[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int p = slice + u * slices;
-        vreg[u] = p < seq && p != pos ? vh[static_cast<size_t>(p) * hd + d] : 0.0f;
-    }
-    float c = 0.0f, s = 0.0f;
-    if (t < half) {
-        const float inv_freq = powf(theta, -static_cast<float>(2 * t) / static_cast<float>(hd));
-        const float angle = static_cast<float>(pos) * inv_freq;
-        c = cosf(angle);
-        s = sinf(angle);
-    }
-    if (t < hd) {
-        qs[t] = qv;
-        ks[t] = kv;
-        vs[t] = vv;
-    }
-    __syncthreads();
-    if (qn) {
-        const int wave = t >> 6;
-        if (wave < 2) {
-            const float s0 = head_rms_scale(wave == 0 ? qs : ks, hd, eps);
-            if ((t & 63) == 0) norm_scale[wave] = s0;
-        }
-        __syncthreads();
-        if (t < hd) {
-            qs[t] = (qs[t] * norm_scale[0]) * qn[t];
-            ks[t] = (ks[t] * norm_scale[1]) * kn[t];
-        }
-        __syncthreads();
-    }
-    if (t < half) {
-        float *xs[2] = {qs, ks};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float *x = xs[h];
-            const float x0 = x[t], x1 = x[t + half];
-            const float r0 = x0 * c - x1 * s;
-            const float r1 = x1 * c + x0 * s;
-            x[t] = r0;
-            x[t + half] = r1;
-        }
-    }
-    __syncthreads();
-    if (head % heads_per_kv == 0 && t < hd) {
-        kcache[(static_cast<size_t>(kvh) * max_seq + pos) * hd + t] = ks[t];
-        vcache[(static_cast<size_t>(kvh) * max_seq + pos) * hd + t] = vs[t];
-    }
-
-    float m = -INFINITY, l = 0.0f, acc = 0.0f;
-    const float4 *q4 = reinterpret_cast<const float4 *>(qs);
-    for (int c0 = 0; c0 < seq; c0 += kAttnChunk) {
-        const int len = min(kAttnChunk, seq - c0);
-        for (int j = t; j < len; j += kAttnThreads) {
-            const int p = c0 + j;
-            float dot = 0.0f;
-            if (kPrefetchKey && p == t && key_pre) {
-#pragma unroll
-                for (int i = 0; i < HD / 4; ++i) {
-                    const float4 a = q4[i], b = kreg[kPrefetchKey ? i : 0];
-                    dot += a.x * b.x;
-                    dot += a.y * b.y;
-                    dot += a.z * b.z;
-                    dot += a.w * b.w;
-                }
-            } else {
-                const float4 *kr = reinterpret_cast<const float4 *>(p == pos ? ks : kh + static_cast<size_t>(p) * hd);
-#pragma unroll
-                for (int i = 0; i < HD / 4; ++i) {
-                    const float4 a = q4[i], b = kr[i];
-                    dot += a.x * b.x;
-                    dot += a.y * b.y;
-                    dot += a.z * b.z;
-                    dot += a.w * b.w;
-                }
-            }
-            sc[j] = dot * scale;
-        }
-        __syncthreads();
-        float cmax = -INFINITY;
-        for (int j = t; j < len; j += kAttnThreads) cmax = fmaxf(cmax, sc[j]);
-        cmax = block_max<kAttnThreads>(cmax, fred);
-        const float m_new = fmaxf(m, cmax);
-        double csum = 0.0;
-        for (int j = t; j < len; j += kAttnThreads) {
-            const float p = expf(sc[j] - m_new);
-            sc[j] = p;
-            csum += p;
-        }
-        csum = block_sum<kAttnThreads>(csum, dred);
-        const float rescale = expf(m - m_new);
-        l = l * rescale + static_cast<float>(csum);
-        acc = acc * rescale;
-        int j = slice;
-        if (c0 == 0) {  // the first eight positions of the slice, loaded at entry
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int jj = slice + u * slices;
-                if (jj < len) acc += sc[jj] * (jj == pos ? vs[d] : vreg[u]);
-            }
-            j = slice + 8 * slices;
-        }
-        // Eight positions' loads issued together, then added in position order.
-        for (; j + 7 * slices < len; j += 8 * slices) {
-            float vb8[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int p = c0 + j + u * slices;
-                vb8[u] = p == pos ? vs[d] : vh[static_cast<size_t>(p) * hd + d];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc += sc[j + u * slices] * vb8[u];
-        }
-        for (; j < len; j += slices) {
-            const int p = c0 + j;
-            acc += sc[j] * (p == pos ? vs[d] : vh[static_cast<size_t>(p) * hd + d]);
-        }
-        m = m_new;
-        __syncthreads();
-    }
-    part[t] = acc;
-    __syncthreads();
-    if (slice == 0) {
-        float o = part[d];
-        for (int s2 = 1; s2 < slices; ++s2) o += part[s2 * hd + d];
-        out[head * hd + d] = o * (1.0f / l);
-    }
+        return true;
+    };
+    attention_head<HD>(sh, t, head, heads_per_kv, fetch, qn, kn, kcache, vcache, *pos_ptr, max_seq, theta, eps, scale,
+                       true, [&](int i, float o) { out[i] = o; });
 }
 
 // gate = silu(gate) * up (swiglu_ref, kernels/silu/swiglu_ref.cpp).
@@ -422,8 +240,15 @@ struct Engine {
     bool fused_rot = false;  // VQ2 rotations inside the matvec launches (unless TQHIP_DECODE_UNFUSED)
     float *hidden2 = nullptr;
     size_t rotbuf_floats = 0;
-    int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next
+    int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next, run, flow error
     int *host_io = nullptr;                     // pinned mirror of dev_io
+    // The data-flow step (decode_flow.hip): one cooperative launch for the layers, then the
+    // lm_head and the argmax; the graph above stays as the fallback.
+    bool flow = false;
+    FlowArgs fa{};
+    void *flow_mem = nullptr;  // HBM: the launch's FlowArgs, then the per-layer pointers
+    size_t flow_lds = 0;
+    unsigned run = 0;
     size_t layer_stride = 0;                    // floats per layer and plane: n_kv_heads * max_seq * head_dim
     void *arena = nullptr;
     hipStream_t stream = nullptr;
@@ -600,6 +425,96 @@ int eager_forward(Engine &e) {
     return forward(e);
 }
 
+// The data-flow step: the layers and the final norm as one cooperative launch, then the lm_head
+// and the argmax as in the graph.
+int flow_forward(Engine &e) {
+    hipStream_t s = e.stream;
+    const FlowArgs *dev_args = static_cast<const FlowArgs *>(e.flow_mem);
+    void *args[] = {&dev_args};
+    if (hipLaunchCooperativeKernel(flow_kernel(e.c.head_dim), dim3(e.fa.plan.wgs), dim3(512), args,
+                                   static_cast<unsigned>(e.flow_lds), s) != hipSuccess)
+        return kLaunchFailed;
+    ScratchScope scope(e.scratch);
+    const int st = mv(e, e.lm_head, e.lm_dtype, e.normed, e.logits, e.c.vocab_size, e.c.hidden_size, s);
+    if (st != kOk) return st;
+    argmax_partial<<<e.amax_blocks, kArgmaxThreads, 0, s>>>(e.logits, e.c.vocab_size, e.amax_v, e.amax_i);
+    argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, e.amax_blocks, e.dev_io + 2);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
+}
+
+// Sets up the data-flow step for an engine of fused i4 layers when TQHIP_DECODE_FLOW=1 (the
+// graph stays the default: measured on MI355X, the flow step takes 0.65-0.71 ms per token of
+// the Qwen2.5-0.5B-shaped file against 0.63-0.66 ms for the graph, the same logits): the
+// per-layer pointer table in HBM, one 512-thread workgroup per CU (all resident at once;
+// TQHIP_FLOW_WGS overrides the count, up to what fits), the task plan, the wait limit. Leaves
+// e->flow false, with nothing to undo, wherever it does not apply.
+int flow_setup(Engine *e) {
+    const char *env = std::getenv("TQHIP_DECODE_FLOW");
+    if (!env || env[0] != '1' || !e->fused || e->pd != 3 || e->eager) return kOk;
+    const void *fn = flow_kernel(e->c.head_dim);
+    const int H = e->c.hidden_size, I = e->c.intermediate_size, qd = e->q_dim;
+    if (!fn || !set_kernel_takes(qd, e->gs) || !flow_shapes_ok(H, qd) || (!e->embed_i4 && H % 4 != 0)) return kOk;
+    int dev = 0, coop = 0, cus = 0, rate_khz = 0, occ = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || rate_khz <= 0)
+        return kOk;
+    const size_t lds = flow_lds_table(H, qd, I) + e->layers.size() * sizeof(FlowLayerPtrs);
+    if (lds > 64 * 1024 || hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, 512, lds) != hipSuccess || occ < 1)
+        return kOk;
+    int wgs = cus;
+    if (const char *w = std::getenv("TQHIP_FLOW_WGS")) wgs = std::max(1, std::atoi(w));
+    wgs = std::min(wgs, occ * cus);
+    std::vector<FlowLayerPtrs> lp(e->layers.size());
+    for (size_t i = 0; i < e->layers.size(); ++i) {
+        const Layer &L = e->layers[i];
+        lp[i] = FlowLayerPtrs{L.q, L.k, L.v, L.o, L.gate, L.up, L.down, L.in_ln, L.post_ln, L.qb, L.kb, L.vb, L.qn,
+                              L.kn, e->kv + (2 * i) * e->layer_stride, e->kv + (2 * i + 1) * e->layer_stride};
+    }
+    const size_t head = (sizeof(FlowArgs) + 255) / 256 * 256, bytes = lp.size() * sizeof(FlowLayerPtrs);
+    if (hipMalloc(&e->flow_mem, head + bytes) != hipSuccess) return kHipFailed;
+    FlowLayerPtrs *dev_layers = reinterpret_cast<FlowLayerPtrs *>(static_cast<uint8_t *>(e->flow_mem) + head);
+    if (hipMemcpy(dev_layers, lp.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) return kHipFailed;
+    const auto shape = [](int K) { return K <= 1024 ? 0 : (K + 2047) / 2048; };
+    FlowArgs &a = e->fa;  // (a.vec was set with the arena)
+    a.layers = dev_layers;
+    a.n_layers = e->c.n_layers;
+    a.H = H;
+    a.I = I;
+    a.q_dim = qd;
+    a.kv_dim = e->kv_dim;
+    a.n_heads = e->c.n_heads;
+    a.heads_per_kv = e->c.n_heads / e->c.n_kv_heads;
+    a.max_seq = e->max_seq;
+    a.eps = e->c.rms_norm_eps;
+    a.theta = e->c.rope_theta;
+    a.attn_scale = e->attn_scale;
+    a.embed_i4 = e->embed_i4 ? static_cast<const uint8_t *>(e->embed) : nullptr;
+    a.embed_f32 = e->embed_i4 ? nullptr : static_cast<const float *>(e->embed);
+    a.embed_gs = e->gs;
+    a.final_norm = e->final_norm;
+    a.normed = e->normed;
+    a.io = e->dev_io;
+    a.shape_h = shape(H);
+    a.shape_q = shape(qd);
+    a.shape_i = shape(I);
+    a.rd = a.shape_h == 0 ? 2 : 1;  // gate/up row pairs per half-wave, or per wave for longer rows
+    // 100 ms per wait; TQHIP_FLOW_TIMEOUT_US sets another limit (tests force the fallback with 0)
+    long long us = 100000;
+    if (const char *t = std::getenv("TQHIP_FLOW_TIMEOUT_US")) us = std::max(0LL, std::atoll(t));
+    a.timeout = static_cast<long long>(rate_khz) * us / 1000;
+    int tasks[kFlowPhases];
+    for (int k = 0; k < kFlowPhases; ++k)
+        tasks[k] = flow_tasks(k, H, qd, e->kv_dim, I, e->c.n_heads, a.shape_h, a.shape_q, a.shape_i, a.rd);
+    a.plan = flow_plan(wgs, tasks);
+    a.lds_table = static_cast<int>(flow_lds_table(H, qd, I));
+    if (hipMemcpy(e->flow_mem, &a, sizeof(FlowArgs), hipMemcpyHostToDevice) != hipSuccess) return kHipFailed;
+    e->flow_lds = lds;
+    e->flow = true;
+    return kOk;
+}
+
 void release(Engine *e) {
     if (e->stream) (void)hipStreamSynchronize(e->stream);
     if (e->exec) (void)hipGraphExecDestroy(e->exec);
@@ -607,6 +522,7 @@ void release(Engine *e) {
     scratch_set_free(e->scratch);
     if (e->arena) (void)hipFree(e->arena);
     if (e->host_io) (void)hipHostFree(e->host_io);
+    if (e->flow_mem) (void)hipFree(e->flow_mem);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
 }
@@ -785,17 +701,23 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     const size_t counts[] = {H, H, static_cast<size_t>(e->q_dim), static_cast<size_t>(e->kv_dim),
                              static_cast<size_t>(e->kv_dim), static_cast<size_t>(e->q_dim), H, I, I, H, V,
                              2 * static_cast<size_t>(c.n_layers) * e->layer_stride,
-                             static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 4,
-                             f16_floats, std::max<size_t>(std::max<size_t>(3 * H, I), e->q_dim), H};
+                             static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 8,
+                             f16_floats, std::max<size_t>(std::max<size_t>(3 * H, I), e->q_dim), H,
+                             // the data-flow step's tagged vectors (8 bytes per element): h0, h1, q, k, v,
+                             // attn, o, act, ffn
+                             2 * H, 2 * H, 2 * static_cast<size_t>(e->q_dim), 2 * static_cast<size_t>(e->kv_dim),
+                             2 * static_cast<size_t>(e->kv_dim), 2 * static_cast<size_t>(e->q_dim), 2 * H, 2 * I,
+                             2 * H};
     float **slots[] = {&e->hidden, &e->normed, &e->q, &e->k, &e->v, &e->attn, &e->o, &e->gate, &e->up, &e->ffn,
                        &e->logits, &e->kv, &e->amax_v};
-    size_t offs[18], total = 0;
-    for (int i = 0; i < 18; ++i) {
+    constexpr int kSlots = 18 + kFlowVecs;
+    size_t offs[kSlots], total = 0;
+    for (int i = 0; i < kSlots; ++i) {
         offs[i] = total;
         total += (counts[i] * 4 + 255) / 256 * 256;
     }
     if (hipMalloc(&e->arena, total) != hipSuccess || hipStreamCreate(&e->stream) != hipSuccess ||
-        hipHostMalloc(reinterpret_cast<void **>(&e->host_io), 4 * sizeof(int)) != hipSuccess) {
+        hipHostMalloc(reinterpret_cast<void **>(&e->host_io), 8 * sizeof(int)) != hipSuccess) {
         *err = "gpu engine: HIP allocation failed";
         release(e);
         return kHipFailed;
@@ -812,6 +734,7 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     e->rotbuf = reinterpret_cast<float *>(base + offs[16]);
     e->rotbuf_floats = counts[16];
     e->hidden2 = reinterpret_cast<float *>(base + offs[17]);
+    for (int i = 0; i < kFlowVecs; ++i) e->fa.vec[i] = reinterpret_cast<uint2 *>(base + offs[18 + i]);
     // fused layers where the set kernel takes every projection around a residual add, an
     // RMSNorm or SwiGLU: q/k/v and gate/up (rows of hidden_size) and down (intermediate_size)
     bool any_rot = false, aligned = true, rot_sets = true;
@@ -859,6 +782,11 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         release(e);
         return rc;
     }
+    if ((rc = flow_setup(e)) != kOk) {
+        *err = "gpu engine: setting up the data-flow step failed";
+        release(e);
+        return rc;
+    }
     *out = e;
     return kOk;
 }
@@ -893,6 +821,24 @@ int tqhip_decode_step(void *engine, int token_id) {
     if (!e || token_id < 0 || token_id >= e->c.vocab_size || e->seq_len >= e->max_seq) return kBadShape;
     e->host_io[0] = e->seq_len;
     e->host_io[1] = token_id;
+    if (e->flow) {
+        e->host_io[3] = static_cast<int>(++e->run);
+        e->host_io[4] = 0;
+        if (hipMemcpyAsync(e->dev_io, e->host_io, 5 * sizeof(int), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+            flow_forward(*e) != kOk ||
+            hipMemcpyAsync(e->host_io + 2, e->dev_io + 2, 3 * sizeof(int), hipMemcpyDeviceToHost, e->stream) !=
+                hipSuccess ||
+            hipStreamSynchronize(e->stream) != hipSuccess)
+            return kLaunchFailed;
+        if (e->host_io[4] == 0) {
+            e->seq_len += 1;
+            return e->host_io[2];
+        }
+        // A wait of the data-flow step ran out: this engine keeps to its graph from now on, and
+        // the token runs again through it (it rewrites every KV row at this position).
+        std::fprintf(stderr, "tqhip: decode engine: the data-flow step timed out; using the step graph\n");
+        e->flow = false;
+    }
     if (hipMemcpyAsync(e->dev_io, e->host_io, 2 * sizeof(int), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
         (e->eager ? eager_forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) ||
         hipMemcpyAsync(e->host_io + 2, e->dev_io + 2, sizeof(int), hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
@@ -918,5 +864,12 @@ const float *tqhip_decode_logits(const void *engine) {
 }
 
 int tqhip_decode_seq_len(const void *engine) { return engine ? static_cast<const Engine *>(engine)->seq_len : -1; }
+
+int tqhip_decode_mode(const void *engine) {
+    if (!engine) return -1;
+    const Engine *e = static_cast<const Engine *>(engine);
+    return (e->fused ? TQHIP_DECODE_FUSED : 0) | (e->flow ? TQHIP_DECODE_FLOW : 0) |
+           (e->eager ? TQHIP_DECODE_EAGER : 0);
+}
 
 }  // extern "C"

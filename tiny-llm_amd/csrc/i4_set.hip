@@ -25,19 +25,12 @@
 // Numerics: the only rounding before the epilogue is x -> X (relative 2^-23 of the
 // group's largest |x|); measured rel L2 ~4e-7 against the double-accumulating reference
 // (kernels/matvec/matvec_i4_ref.cpp:45-103).
-#include "i4_lane.h"
+#include "i4_set_core.h"
 
 #include <algorithm>
 
 namespace tqhip {
 namespace {
-
-#ifndef TQ_SET_WAVES
-#define TQ_SET_WAVES 8
-#endif
-constexpr int kSetWaves = TQ_SET_WAVES;     // waves per workgroup
-constexpr int kSetThreads = 64 * kSetWaves;
-constexpr int kSetMaxSlots = 5;   // wave-per-row slots of 64 half-groups: K <= 5 * 64 * 32
 
 struct SetMat {
     const uint8_t *w;
@@ -57,100 +50,6 @@ struct SetArgs {
     int n;
     SetPrologue pro;  // XM != 0 instances only
 };
-
-// ---- activations as exact integers -------------------------------------------------------
-// Every group of 64 activations is scaled by its own power of two 2^f (its largest |x|
-// lands in [2^21, 2^22)) and rounded to the nearest integer: X = x * 2^f rounded,
-// |X| <= 2^22, the only rounding before the epilogue. X's two's-complement bytes are its
-// digits, X = b0 + 256 b1 + 65536 s2 with b0, b1 unsigned and s2 the signed third byte
-// (exact while |X| < 2^23). They go to LDS as the byte operands of v_dot4: per 8-element
-// block six dwords [byte p][even | odd], "even" holding elements 0, 2, 4, 6 and "odd" 1,
-// 3, 5, 7 -- the order in which a code dword's low and high nibbles present the weights.
-// Per half-group (32 elements) LDS also holds sum(X) (as a float) and 2^-f.
-constexpr int kBlockBytes = 24;  // one 8-element block: 3 digit planes x (even, odd) dwords
-
-// Round to nearest (ties upward: floor(v + 0.5)), one instruction.
-__device__ inline int round_int(float v) {
-    int r;
-    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-
-// Thread t converts 16-byte chunk c = t + kSetThreads i (elements 4c .. 4c + 3) of every chunk
-// the rows read (c < C): the 16 chunks of a group are one DPP row (16 lanes), the 8
-// chunks of a half-group half of one.
-__device__ __forceinline__ void stage_x(float4 q, int c, int Kc, int C, unsigned char *xp, float2 *hs) {
-    if (c >= Kc) q = make_float4(0.f, 0.f, 0.f, 0.f);  // past K: zeros
-    float m = fmaxf(fmaxf(abs_or_inf(q.x), abs_or_inf(q.y)), fmaxf(abs_or_inf(q.z), abs_or_inf(q.w)));
-    m = fmaxf(m, dpp_f<kDppXor1>(m));
-    m = fmaxf(m, dpp_f<kDppXor2>(m));
-    m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
-    m = fmaxf(m, dpp_f<kDppMirror>(m));  // the group's largest |x| (inf if any is not finite), in all 16 lanes
-    const int f = group_exponent(m);
-    // the value itself is scaled (2^f is not a finite float for f >= 128; x * 2^f is exact)
-    const unsigned X0 = round_int(ldexpf(q.x, f)), X1 = round_int(ldexpf(q.y, f));
-    const unsigned X2 = round_int(ldexpf(q.z, f)), X3 = round_int(ldexpf(q.w, f));
-    int sum = static_cast<int>(X0 + X1 + X2 + X3);
-    sum += dpp_i<kDppXor1>(sum);
-    sum += dpp_i<kDppXor2>(sum);
-    sum += dpp_i<kDppHalfMirror>(sum);  // the half-group's sum(X), in its 8 lanes
-    if (c >= C) return;
-    // elements 4c + 0, 2 are "even" bytes 2 (c & 1) + 0, 1 of the block; 4c + 1, 3 "odd"
-    unsigned char *blk = xp + (c >> 1) * kBlockBytes + 2 * (c & 1);
-#pragma unroll
-    for (int p = 0; p < 3; ++p) {
-        const unsigned sel = 0x0C0C0000u | ((4u + p) << 8) | p;  // byte p of the second, byte p of the first
-        *reinterpret_cast<unsigned short *>(blk + 8 * p) = static_cast<unsigned short>(__builtin_amdgcn_perm(X2, X0, sel));
-        *reinterpret_cast<unsigned short *>(blk + 8 * p + 4) =
-            static_cast<unsigned short>(__builtin_amdgcn_perm(X3, X1, sel));
-    }
-    if ((c & 7) == 0) hs[c >> 3] = make_float2(static_cast<float>(sum), group_unscale(m, f));
-}
-
-// scale * 2^-f * (sum(q * X) - zero * sum(X)) over one half-group: the 16 code bytes cd,
-// the group header hd, the half-group's 24 operand dwords xv (4 blocks) and its
-// (sum(X), 2^-f). The digit sums are exact integers (v_dot4: unsigned for b0 and b1,
-// signed for s2); sum(q * X) = (a0 + 256 a1) + 65536 a2 is formed in fp32.
-__device__ __forceinline__ float half_group_int(const v4i &cd, unsigned hd, const unsigned (&xv)[24], float2 hs) {
-    unsigned a0 = 0, a1 = 0;
-    int a2 = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const unsigned d = static_cast<unsigned>(cd[j]);
-        const unsigned lo = d & kNibbles, hi = (d >> 4) & kNibbles;
-        a0 = __builtin_amdgcn_udot4(lo, xv[6 * j + 0], a0, false);
-        a0 = __builtin_amdgcn_udot4(hi, xv[6 * j + 1], a0, false);
-        a1 = __builtin_amdgcn_udot4(lo, xv[6 * j + 2], a1, false);
-        a1 = __builtin_amdgcn_udot4(hi, xv[6 * j + 3], a1, false);
-        a2 = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(xv[6 * j + 4]), a2, false);
-        a2 = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xv[6 * j + 5]), a2, false);
-    }
-    const float V = fmaf(static_cast<float>(a2), 65536.f, static_cast<float>(a0 + a1 * 256u));
-    const float sc = half_bits(hd), z = half_bits(hd >> 16);
-    // 2^-f times the exact integer sum first: for tiny activations (f > 126) 2^-f is subnormal and
-    // sc * 2^-f could lose its digits, while 2^-f * (...) is still a normal float; for normal
-    // products both orders round once and give the same bits.
-    return sc * (hs.y * fmaf(-z, hs.x, V));
-}
-
-// Rows of at most 32 half-groups (S = 0): R rows per half-wave, 2R per wave, 8R per
-// workgroup. Rows of more: R per wave over S slots, kSetWaves R per workgroup.
-// Sum of v over the workgroup, in double, in a fixed order (each wave by shuffles, then the
-// kSetWaves wave sums in wave order).
-__device__ inline double set_block_sum(double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    __shared__ double red[kSetWaves];
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    double t = red[0];
-#pragma unroll
-    for (int w = 1; w < kSetWaves; ++w) t += red[w];
-    return t;
-}
-
-__device__ inline float4 add4(float4 a, float4 b) {
-    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
 
 // XM: the activation prologue (0 none; 1 x = silu(x) * x2; 2 x = rmsnorm((x + d1) + d2) * nw,
 // workgroup 0 storing the sum to hout), with its operands in pro.
@@ -229,13 +128,7 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
     // compiler sink the later activation loads behind the weight loads.
     if constexpr (XM == 1) {  // swiglu_ref (kernels/silu/swiglu_ref.cpp): silu(g) * u
 #pragma unroll
-        for (int i = 0; i < NX; ++i) {
-            float e[4] = {xq[i].x, xq[i].y, xq[i].z, xq[i].w};
-            const float u[4] = {pa[i].x, pa[i].y, pa[i].z, pa[i].w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) e[c] = (e[c] / (1.0f + expf(-e[c]))) * u[c];
-            xq[i] = make_float4(e[0], e[1], e[2], e[3]);
-        }
+        for (int i = 0; i < NX; ++i) xq[i] = swiglu4(xq[i], pa[i]);
     } else if constexpr (XM == 2) {
         // hidden + delta(s) in the runtime's order, then rmsnorm_ref (kernels/rmsnorm/rmsnorm_ref.cpp):
         // a double sum of squares, a float mean, 1 / sqrt(mean + eps), (h * scale) * w
@@ -244,11 +137,7 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
         for (int i = 0; i < NX; ++i) {
             if (pro.d1) xq[i] = add4(xq[i], pa[i]);
             if (pro.d2) xq[i] = add4(xq[i], pb[i]);
-            if (t + kSetThreads * i < Kc) {
-                const float4 h = xq[i];
-                ss += static_cast<double>(h.x) * h.x + static_cast<double>(h.y) * h.y +
-                      static_cast<double>(h.z) * h.z + static_cast<double>(h.w) * h.w;
-            }
+            if (t + kSetThreads * i < Kc) ss += sq4(xq[i]);
         }
         if (pro.hout && blockIdx.x == 0) {
             float4 *h4 = reinterpret_cast<float4 *>(pro.hout);
@@ -257,12 +146,9 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
                 if (t + kSetThreads * i < Kc) h4[t + kSetThreads * i] = xq[i];
         }
         ss = set_block_sum(ss);
-        const float mean_sq = static_cast<float>(ss / m.K);
-        const float scale = 1.0f / sqrtf(mean_sq + pro.eps);
+        const float scale = rms_scale(ss, m.K, pro.eps);
 #pragma unroll
-        for (int i = 0; i < NX; ++i)
-            xq[i] = make_float4((xq[i].x * scale) * pw[i].x, (xq[i].y * scale) * pw[i].y, (xq[i].z * scale) * pw[i].z,
-                                (xq[i].w * scale) * pw[i].w);
+        for (int i = 0; i < NX; ++i) xq[i] = rms_apply(xq[i], scale, pw[i]);
     }
 #pragma unroll
     for (int i = 0; i < NX; ++i) stage_x(xq[i], t + kSetThreads * i, Kc, C, xp, hs);
