@@ -11,7 +11,6 @@ that libtqhip.so's own copy of the registry does not interpose on tiny-llm's. No
 runs on a GPU. It needs the reference tree, so it runs in the development container only.
 """
 import os
-import re
 import shutil
 import subprocess
 
@@ -31,11 +30,8 @@ pytestmark = pytest.mark.skipif(
 
 def binding_source():
     """The C++ blocks of the integration guide that make up hip_variants.cpp (its sections 1 and 4)."""
-    text = open(os.path.join(REPO, "INTEGRATION.md")).read()
-    blocks = [re.sub(r"^  ", "", b, flags=re.M) for b in re.findall(r"```cpp\n(.*?)```", text, flags=re.S)]
-    parts = [b for b in blocks if "TINYQWEN_" in b and "VARIANT" in b]
-    assert len(parts) == 2, "expected the registry block and the gpu_decode block"
-    return "\n".join(parts)
+    from oracle.extract_binding import binding_source as extract
+    return extract(open(os.path.join(REPO, "INTEGRATION.md")).read())
 
 
 def test_binding_compiles_links_and_selects(tmp_path):
@@ -52,3 +48,30 @@ def test_binding_compiles_links_and_selects(tmp_path):
                          env=dict(os.environ, HIP_VISIBLE_DEVICES="-1"))
     assert out.returncode == 0, out.stdout + out.stderr
     assert out.stdout.endswith("all ok\n"), out.stdout
+
+
+def test_reference_runtime_driver_on_ref(tmp_path):
+    """oracle/_ref/tqref_runtime (the reference's QwenModel with its own kernels, driven by
+    tests/hip_runtime_driver.cpp) runs the three legs the GPU test compares against."""
+    exe = os.path.join(REPO, "oracle", "_ref", "tqref_runtime")
+    if not os.access(exe, os.X_OK):
+        pytest.skip("make -C oracle runtime")
+    from conftest import load_package
+    img, cfg, _ = load_package().tqwen_synth.dense_i4_model(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64,
+                                                           inter=512, vocab=300, layers=2, seed=2)
+    model, out = tmp_path / "m.tqwen", tmp_path / "l.bin"
+    model.write_bytes(bytes(img))
+    res = subprocess.run([exe, str(model), "ref", str(out), "5", "33"], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    lines = res.stdout.splitlines()
+    assert lines[0] == "impl i4=ref vq2=ref"
+    assert lines[1].startswith("decode ") and len(lines[1].split()) == 6
+    assert lines[2].startswith("prefill ") and len(lines[2].split()) == 6
+    import numpy as np
+    logits = np.fromfile(out, dtype=np.float32).reshape(-1, cfg["vocab_size"])
+    assert logits.shape[0] == 5 + 5 and np.all(np.isfinite(logits))
+    # the returned tokens are the argmax of the logits written for the same step
+    toks = [int(t) for t in lines[1].split()[1:]] + [int(t) for t in lines[2].split()[1:]]
+    assert toks == [int(np.argmax(r)) for r in logits]
+    res = subprocess.run([exe, str(model), "no_such_impl", str(out), "1", "2"], capture_output=True, text=True)
+    assert res.returncode == 1 and "no implementation named no_such_impl" in res.stderr
