@@ -167,21 +167,16 @@ def test_matmul_i4_per_token_scale_extremes(gpu, orc):
         assert_close(got[n], want[n], 2e-3, f"column {n}")
 
 
-def test_matmul_i4_prefill_shape_sampled_rows(gpu, orc):
-    """The prefill configuration (9728 weight rows, K 2560, 512 tokens) in one
-    launch; rows are independent, so three 64-row blocks are checked against
-    the oracle run on those rows alone."""
+def test_matmul_i4_prefill_shape_every_output(gpu, orc):
+    """The prefill configuration (9728 weight rows, K 2560, 512 tokens) in
+    one launch, every one of its 5.0M outputs against the oracle (a few seconds on 16 threads)."""
     M, K, N, G = 9728, 2560, 512, 64
     w = gpu.synth_i4(M, K, G, seed=11)
     x = gpu.synth_normal(K * N, seed=12)
     dw, dx, dy = gpu.DeviceBuffer.from_array(w), gpu.DeviceBuffer.from_array(x), gpu.DeviceBuffer(4 * M * N)
     gpu.matmul_i4_dev(dw, dx, dy, M, K, N, G)
-    got = dy.download(np.float32, M * N).reshape(N, M)
-    rb = orc.i4_row_bytes(K, G)
-    for r0 in (0, 4800, M - 64):
-        sub = np.ascontiguousarray(w[r0 * rb:(r0 + 64) * rb])
-        want = orc.matmul_i4(sub, x, 64, K, N, G, threads=16).reshape(N, 64)
-        assert_close(got[:, r0:r0 + 64], want, 2e-3, f"rows {r0}..{r0 + 63}")
+    want = orc.matmul_i4(w, x, M, K, N, G, threads=16)
+    assert_close(dy.download(np.float32, M * N), want, 2e-3, "9728x2560x512")
 
 
 def test_matmul_i4_prefill_rows_full_shape_128_tokens(gpu, orc):

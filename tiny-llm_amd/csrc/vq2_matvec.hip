@@ -26,6 +26,7 @@
 //   (launch_vq2_matvec_set: a decoder layer's q/k/v or gate/up).
 // All accumulate in fp32.
 
+#include "lane_sum.h"
 #include "tq_common.h"
 
 #include <algorithm>
@@ -349,8 +350,7 @@ __device__ inline float vq2_row(const uint8_t *w, const float *x, int K, int row
         for (int jj = 0; jj < 4; ++jj) c[jj] = cbg[(q >> (8 * jj)) & 0xFFu];
         acc = vq2_accum(acc, c, xv);
     }
-    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    return acc;
+    return sum_wave(acc);  // DPP and row swaps in registers, a fixed order
 }
 
 // One matrix per launch (32 bytes of kernel arguments: the set form's 8 records and their
@@ -373,130 +373,161 @@ __global__ __launch_bounds__(256) void vq2_matvec_rows(Vq2SetArgs a) {
     if ((threadIdx.x & 63) == 0) m.y[row] = acc;
 }
 
-// The staged form: 8 rows per workgroup, so that each workgroup's prologue and rotation serve
-// twice the rows. PER: activations per thread (K <= 512 PER); a lane's row takes NIT = PER / 2
-// (rounded up) index dwords. Every load that does not wait for the prologue goes out first: the
-// prologue operands and rotation vectors of the thread's activations and all of the lane's index
-// dwords, then every codebook entry they name; the prologue then runs in registers (one barrier
-// for the RMSNorm's sum, one per two butterfly stages) while the entries arrive. (With a loop
-// that loaded an index dword and then its entries per step, the row's round trips followed one
-// another after the build: 896x4864 with SwiGLU and rotation 12.5 us per launch.)
+// The staged form: 8 waves, each taking RPW rows, so that a workgroup's activation build serves
+// 8 RPW rows. Lane l of wave w holds activations 256 (8 p + w) + 4 l + 0..3 in pass p (NP
+// passes of 2048 cover K): 16-byte loads of every prologue operand, and a BiIP block (at most
+// 256 activations, a power of two dividing K) lies within one wave, so the rotation's radix-2
+// stages run in registers -- stage h < 4 inside the lane, stage h >= 4 against lane l ^ (h / 4)
+// -- with no barrier. Each stage makes the same adds and subtracts, in the same order, as
+// biip_rotate_kernel (whose radix-4 form is two radix-2 stages), so the values match its bits.
+// The 2 KB codebook goes to LDS once per workgroup and the lookups read it there. Every load
+// that does not wait for the prologue goes out first (the codebook, the rows' index dwords, the
+// prologue operands); the prologue runs in registers (one barrier for the RMSNorm's sum) while
+// they arrive. Measured on MI355X at the Qwen2.5-0.5B rotated-VQ2 shapes against the previous
+// form (one activation per thread and pass, LDS butterfly with a barrier per two stages,
+// codebook entries gathered from global memory, one row per wave): see the launcher.
 constexpr int kRotWaves = 8;
-template <int PER, int XM, bool ROT>
+constexpr int kStagedPass = 64 * kRotWaves * 4;  // activations per pass
+template <int NP, int XM, bool ROT, int RPW>
 __global__ __launch_bounds__(64 * kRotWaves) void vq2_matvec_staged(Vq2StagedArgs a) {
     extern __shared__ __align__(16) float xs[];  // the matrix's activations
-    constexpr int T = 64 * kRotWaves;
+    __shared__ uint2 cbl[256];                   // its codebook's fp16 entries
+    constexpr int NIT = 2 * NP;                  // index dwords per lane and row (K / 16 <= 128 NP)
     TQ_VQ2_SELECT(a, m, kStagedMaxMats);
     const float *const d1 = a.pro.d1, *const d2 = a.pro.d2, *const nw = a.pro.nw, *const x2 = a.pro.x2;
     float *const hout = a.pro.hout;
     const float eps = a.pro.eps;
-    const int t = threadIdx.x, lane = t & 63;
-    const int row = (static_cast<int>(blockIdx.x) - m.blk0) * kRotWaves + (t >> 6);
-    const bool live = row < m.M;  // no early return: every thread takes part in the barriers
-    const int nb = m.K / kVq2Dim;
-    const unsigned *qrow =
-        reinterpret_cast<const unsigned *>(m.w + kVq2CodebookBytes + static_cast<size_t>(live ? row : 0) * nb);
-    const uint2 *cbg = reinterpret_cast<const uint2 *>(m.w);
-    constexpr int NIT = (PER + 1) / 2;
-    unsigned qv[NIT];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int blk = static_cast<int>(blockIdx.x) - m.blk0;
+    const int K = m.K, M = m.M, nb = K / kVq2Dim;
+    if (t < 256) cbl[t] = reinterpret_cast<const uint2 *>(m.w)[t];
+    unsigned qv[RPW][NIT];
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int d = lane + 64 * it;
-        qv[it] = live && 4 * d < nb ? qrow[d] : 0u;
+    for (int r = 0; r < RPW; ++r) {
+        const int row = (blk * RPW + r) * kRotWaves + wave;
+        const unsigned *qrow =
+            reinterpret_cast<const unsigned *>(m.w + kVq2CodebookBytes + static_cast<size_t>(row < M ? row : 0) * nb);
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int d = lane + 64 * it;
+            qv[r][it] = row < M && 4 * d < nb ? qrow[d] : 0u;
+        }
     }
-    float v[PER], p1[PER], p2[PER], p3[PER], sc[PER], sg[PER];
+    // activations 4 e .. 4 e + 3 of pass p, e = 64 (8 p + w) + l (whole float4s: K % 16 == 0)
+    typedef float f4e __attribute__((ext_vector_type(4)));
+    f4e v[NP], p1[NP], p2[NP], p3[NP], sc[NP], sg[NP];
+    const f4e zero = {0.f, 0.f, 0.f, 0.f}, one = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-        const int i = t + T * j;
-        const bool ok = i < m.K;
-        v[j] = ok ? m.x[i] : 0.f;
+    for (int p = 0; p < NP; ++p) {
+        const int e = 64 * (kRotWaves * p + wave) + lane;
+        const bool ok = 4 * e < K;
+        v[p] = ok ? reinterpret_cast<const f4e *>(m.x)[e] : zero;
         if constexpr (XM == 2) {
-            p1[j] = ok && d1 ? d1[i] : 0.f;
-            p2[j] = ok && d2 ? d2[i] : 0.f;
-            p3[j] = ok ? nw[i] : 0.f;
+            p1[p] = ok && d1 ? reinterpret_cast<const f4e *>(d1)[e] : zero;
+            p2[p] = ok && d2 ? reinterpret_cast<const f4e *>(d2)[e] : zero;
+            p3[p] = ok ? reinterpret_cast<const f4e *>(nw)[e] : zero;
         } else if constexpr (XM == 1) {
-            p1[j] = ok ? x2[i] : 0.f;
+            p1[p] = ok ? reinterpret_cast<const f4e *>(x2)[e] : zero;
         }
         if constexpr (ROT) {
-            sc[j] = ok && m.scale ? m.scale[i] : 1.f;
-            sg[j] = ok ? m.sign[i] : 0.f;
+            sc[p] = ok && m.scale ? reinterpret_cast<const f4e *>(m.scale)[e] : one;
+            sg[p] = ok ? reinterpret_cast<const f4e *>(m.sign)[e] : zero;
         }
     }
-    uint2 cv[NIT][4];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) cv[it][jj] = cbg[(qv[it] >> (8 * jj)) & 0xFFu];
     if constexpr (XM == 2) {  // add_rmsnorm's operations
         double ss = 0.0;
 #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            if (d1) v[j] = v[j] + p1[j];
-            if (d2) v[j] = v[j] + p2[j];
-            const int i = t + T * j;
-            if (hout && blockIdx.x == 0 && i < m.K) hout[i] = v[j];
-            ss += static_cast<double>(v[j]) * static_cast<double>(v[j]);
+        for (int p = 0; p < NP; ++p) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (d1) v[p][c] = v[p][c] + p1[p][c];
+                if (d2) v[p][c] = v[p][c] + p2[p][c];
+                ss += static_cast<double>(v[p][c]) * static_cast<double>(v[p][c]);
+            }
+            const int e = 64 * (kRotWaves * p + wave) + lane;
+            if (hout && blockIdx.x == 0 && 4 * e < K) reinterpret_cast<f4e *>(hout)[e] = v[p];
         }
         ss = vq2_block_sum<kRotWaves>(ss);
-        const float mean_sq = static_cast<float>(ss / m.K);
+        const float mean_sq = static_cast<float>(ss / K);
         const float scale = 1.0f / sqrtf(mean_sq + eps);
 #pragma unroll
-        for (int j = 0; j < PER; ++j) v[j] = (v[j] * scale) * p3[j];
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[p][c] = (v[p][c] * scale) * p3[p][c];
     } else if constexpr (XM == 1) {  // swiglu's operations
 #pragma unroll
-        for (int j = 0; j < PER; ++j) v[j] = (v[j] / (1.0f + expf(-v[j]))) * p1[j];
-    }
-    if constexpr (ROT) {  // biip_rotate_kernel's operations
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
-        for (int j = 0; j < PER; ++j) v[j] = m.scale ? (v[j] / sc[j]) * sg[j] : v[j] * sg[j];
+            for (int c = 0; c < 4; ++c) v[p][c] = (v[p][c] / (1.0f + expf(-v[p][c]))) * p1[p][c];
     }
+    {
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-        if (t + T * j < m.K) xs[t + T * j] = v[j];
-    if constexpr (ROT) {
-        // stages h = 2^lg and 2h together on the four elements jj + {0, h, 2h, 3h}: each element
-        // gets the adds and subtracts of the two radix-2 stages in their order, with one barrier
-        int lg = 0;
-        for (; lg + 1 < a.lg_bs; lg += 2) {
-            __syncthreads();
-            const int h = 1 << lg;
-            for (int p = t; p < m.K / 4; p += T) {
-                const int jj = ((p >> lg) << (lg + 2)) + (p & (h - 1));
-                const float x0 = xs[jj], x1 = xs[jj + h], x2 = xs[jj + 2 * h], x3 = xs[jj + 3 * h];
-                const float y0 = x0 + x1, y1 = x0 - x1, y2 = x2 + x3, y3 = x2 - x3;
-                xs[jj] = y0 + y2;
-                xs[jj + h] = y1 + y3;
-                xs[jj + 2 * h] = y0 - y2;
-                xs[jj + 3 * h] = y1 - y3;
+        for (int p = 0; p < NP; ++p) {
+            f4e f = v[p];
+            if constexpr (ROT) {  // biip_rotate_kernel's operations
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    f[c] = m.scale ? (f[c] / sc[p][c]) * sg[p][c] : f[c] * sg[p][c];
+                // stage h: (u, c) at (j, j + h) of a block -> (u + c, u - c)
+                if (a.lg_bs > 0) {
+                    const float u0 = f[0], u1 = f[1], u2 = f[2], u3 = f[3];
+                    f[0] = u0 + u1;
+                    f[1] = u0 - u1;
+                    f[2] = u2 + u3;
+                    f[3] = u2 - u3;
+                }
+                if (a.lg_bs > 1) {
+                    const float u0 = f[0], u1 = f[1], u2 = f[2], u3 = f[3];
+                    f[0] = u0 + u2;
+                    f[1] = u1 + u3;
+                    f[2] = u0 - u2;
+                    f[3] = u1 - u3;
+                }
+                // stages h = 4 .. 128: the pair's other elements are in lane l ^ (h / 4); the lane
+                // with that bit set holds the second ones (u - c, c its own)
+                auto stage = [&](auto dlc) {
+                    constexpr int DL = decltype(dlc)::value;
+                    const bool hi = lane & DL;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float o = lane_xor<DL>(f[c], lane);
+                        f[c] = hi ? o - f[c] : f[c] + o;
+                    }
+                };
+                if (a.lg_bs > 2) stage(std::integral_constant<int, 1>{});
+                if (a.lg_bs > 3) stage(std::integral_constant<int, 2>{});
+                if (a.lg_bs > 4) stage(std::integral_constant<int, 4>{});
+                if (a.lg_bs > 5) stage(std::integral_constant<int, 8>{});
+                if (a.lg_bs > 6) stage(std::integral_constant<int, 16>{});
+                if (a.lg_bs > 7) stage(std::integral_constant<int, 32>{});
+#pragma unroll
+                for (int c = 0; c < 4; ++c) f[c] = f[c] * a.inv_sqrt;
             }
+            const int e = 64 * (kRotWaves * p + wave) + lane;
+            if (4 * e < K) reinterpret_cast<f4e *>(xs)[e] = f;
         }
-        if (lg < a.lg_bs) {  // a last single stage: (u, c) at (jj, jj + h) -> (u + c, u - c)
-            __syncthreads();
-            const int h = 1 << lg;
-            for (int p = t; p < m.K / 2; p += T) {
-                const int jj = ((p >> lg) << (lg + 1)) + (p & (h - 1));
-                const float u = xs[jj], c = xs[jj + h];
-                xs[jj] = u + c;
-                xs[jj + h] = u - c;
-            }
-        }
-        __syncthreads();
-        for (int i = t; i < m.K; i += T) xs[i] = xs[i] * a.inv_sqrt;
     }
     __syncthreads();
-    if (!live) return;
-    float acc = 0.f;
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int d = lane + 64 * it;
-        if (4 * d >= nb) break;
-        float4 xv[4];
+    for (int r = 0; r < RPW; ++r) {
+        const int row = (blk * RPW + r) * kRotWaves + wave;
+        if (row >= M) break;
+        float acc = 0.f;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) xv[jj] = *reinterpret_cast<const float4 *>(xs + 16 * d + 4 * jj);
-        acc = vq2_accum(acc, cv[it], xv);
+        for (int it = 0; it < NIT; ++it) {
+            const int d = lane + 64 * it;
+            if (4 * d >= nb) break;
+            uint2 cv[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) cv[jj] = cbl[(qv[r][it] >> (8 * jj)) & 0xFFu];
+            float4 xv[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) xv[jj] = *reinterpret_cast<const float4 *>(xs + 16 * d + 4 * jj);
+            acc = vq2_accum(acc, cv, xv);
+        }
+        acc = sum_wave(acc);  // vq2_row's order
+        if (lane == 0) m.y[row] = acc;
     }
-    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0) m.y[row] = acc;
 }
 
 // The matrix the one-wave-per-row kernel takes: index rows dword-aligned, at most
@@ -823,22 +854,36 @@ int launch_vq2_matvec_set_pro(int n, const I4Mat *mats, const float *const *scal
     if (n < 1 || n > kStagedMaxMats || xm < 0 || xm > 2 || (!sign && !xm)) return kNotFused;
     if (xm == 1 && !pro->x2) return kNotFused;
     if (xm == 2 && !pro->nw) return kNotFused;
-    if (sign && (block_size < 1 || (block_size & (block_size - 1)))) return kNotFused;
+    // a rotation block lies within one wave's 256 activations
+    if (sign && (block_size < 1 || block_size > 256 || (block_size & (block_size - 1)))) return kNotFused;
+    auto a16 = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };  // null passes
+    if (pro && !(a16(pro->x2) && a16(pro->d1) && a16(pro->d2) && a16(pro->nw) && a16(pro->hout))) return kNotFused;
     Vq2StagedArgs a{};
-    int blocks = 0, kmax = 0;
+    int rows = 0, kmax = 0;
     long long lookups = 0;
     for (int i = 0; i < n; ++i) {
         const I4Mat &mt = mats[i];
-        if (mt.M < 1 || mt.K < kVq2Dim || mt.K % kVq2Dim || !rows_kernel_takes(mt.w, mt.M, mt.K)) return kNotFused;
-        if (sign && (!sign[i] || mt.K % block_size)) return kNotFused;
+        if (mt.M < 1 || mt.K < kVq2Dim || mt.K % kVq2Dim || !rows_kernel_takes(mt.w, mt.M, mt.K) || !a16(mt.x))
+            return kNotFused;
+        if (sign && (!sign[i] || mt.K % block_size || !a16(sign[i]) || !a16(scale[i]))) return kNotFused;
         if (xm && (mt.x != mats[0].x || mt.K != mats[0].K)) return kNotFused;
-        a.m[i] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, sign ? scale[i] : nullptr, sign ? sign[i] : nullptr};
-        blocks += (mt.M + kRotWaves - 1) / kRotWaves;
+        rows += mt.M;
         lookups += static_cast<long long>(mt.M) * (mt.K / kVq2Dim);
         kmax = std::max(kmax, mt.K);
     }
-    // the staged kernel holds up to 20 activations per thread (10 with the RMSNorm's operands)
-    if (lookups > 2 * kDirectLookups || kmax > (xm == 2 ? 5120 : 10240)) return kNotFused;
+    // up to 5 passes of 2048 activations (the RMSNorm's operands: 3)
+    if (lookups > 2 * kDirectLookups || kmax > (xm == 2 ? 6144 : 10240)) return kNotFused;
+    // Rows per wave: 4 when the set has enough rows to keep 300 workgroups (the build is then
+    // shared by 32 rows) and K <= 6144 (with 5 passes the index dwords of 4 rows went to
+    // scratch memory), else 1.
+    const int passes = (kmax + kStagedPass - 1) / kStagedPass;
+    const int rpw = passes <= 3 && rows >= 4 * kRotWaves * 300 ? 4 : 1;
+    int blocks = 0;
+    for (int i = 0; i < n; ++i) {
+        const I4Mat &mt = mats[i];
+        a.m[i] = Vq2Mat{mt.w, mt.x, mt.y, mt.M, mt.K, blocks, sign ? scale[i] : nullptr, sign ? sign[i] : nullptr};
+        blocks += (mt.M + kRotWaves * rpw - 1) / (kRotWaves * rpw);
+    }
     for (int k = n; k < kStagedMaxMats; ++k) a.m[k] = a.m[n - 1];  // never selected (k >= n)
     a.n = n;
     if (pro) a.pro = *pro;
@@ -850,28 +895,33 @@ int launch_vq2_matvec_set_pro(int n, const I4Mat *mats, const float *const *scal
     }
     const dim3 grid(blocks), block(64 * kRotWaves);
     const size_t lds = static_cast<size_t>(kmax) * 4;
-    const int per = kmax <= 1024 ? 2 : kmax <= 2048 ? 4 : kmax <= 5120 ? 10 : 20;
-    auto go = [&](auto perc) {  // the instance of (xm, rotation); xm was checked above
-        constexpr int P = decltype(perc)::value;
+    auto go = [&](auto npc, auto rc) {  // the instance of (xm, rotation); xm was checked above
+        constexpr int NP = decltype(npc)::value, R = decltype(rc)::value;
         if (xm == 0)
-            hipLaunchKernelGGL((vq2_matvec_staged<P, 0, true>), grid, block, lds, stream, a);
+            hipLaunchKernelGGL((vq2_matvec_staged<NP, 0, true, R>), grid, block, lds, stream, a);
         else if (xm == 1 && sign)
-            hipLaunchKernelGGL((vq2_matvec_staged<P, 1, true>), grid, block, lds, stream, a);
+            hipLaunchKernelGGL((vq2_matvec_staged<NP, 1, true, R>), grid, block, lds, stream, a);
         else if (xm == 1)
-            hipLaunchKernelGGL((vq2_matvec_staged<P, 1, false>), grid, block, lds, stream, a);
+            hipLaunchKernelGGL((vq2_matvec_staged<NP, 1, false, R>), grid, block, lds, stream, a);
         else if (sign)
-            hipLaunchKernelGGL((vq2_matvec_staged<P, 2, true>), grid, block, lds, stream, a);
+            hipLaunchKernelGGL((vq2_matvec_staged<NP, 2, true, R>), grid, block, lds, stream, a);
         else
-            hipLaunchKernelGGL((vq2_matvec_staged<P, 2, false>), grid, block, lds, stream, a);
+            hipLaunchKernelGGL((vq2_matvec_staged<NP, 2, false, R>), grid, block, lds, stream, a);
     };
-    if (per == 2)
-        go(std::integral_constant<int, 2>{});
-    else if (per == 4)
-        go(std::integral_constant<int, 4>{});
-    else if (per == 10)
-        go(std::integral_constant<int, 10>{});
+    auto go_np = [&](auto rc) {
+        if (passes <= 1)
+            go(std::integral_constant<int, 1>{}, rc);
+        else if (passes == 2)
+            go(std::integral_constant<int, 2>{}, rc);
+        else if (passes == 3)
+            go(std::integral_constant<int, 3>{}, rc);
+        else if constexpr (decltype(rc)::value == 1)
+            go(std::integral_constant<int, 5>{}, rc);
+    };
+    if (rpw == 4)
+        go_np(std::integral_constant<int, 4>{});
     else
-        go(std::integral_constant<int, 20>{});
+        go_np(std::integral_constant<int, 1>{});
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -889,7 +939,7 @@ bool vq2_set_takes(int n, const int *M, int K, int xm) {
         if (M[i] < 1 || K % 16 || static_cast<long long>(M[i]) * (K / kVq2Dim) > kDirectLookups) return false;
         lookups += static_cast<long long>(M[i]) * (K / kVq2Dim);
     }
-    return n >= 1 && n <= kStagedMaxMats && lookups <= 2 * kDirectLookups && K <= (xm == 2 ? 5120 : 10240);
+    return n >= 1 && n <= kStagedMaxMats && lookups <= 2 * kDirectLookups && K <= (xm == 2 ? 6144 : 10240);
 }
 
 }  // namespace tqhip
