@@ -23,6 +23,8 @@
 
 #include <cmath>
 
+#include "lane_sum.h"
+
 namespace tqhip {
 namespace {
 
@@ -46,7 +48,7 @@ struct AttnShared {
 // order: a 64-lane butterfly, then the four wave results in wave order. Every thread of the
 // workgroup must call them (they hold a workgroup barrier).
 __device__ inline double attn_sum(double v, double *red, int t) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = xor_sum_wave(v);
     if ((t & 63) == 0) red[t >> 6] = v;
     __syncthreads();
     double r = 0.0;
@@ -56,7 +58,7 @@ __device__ inline double attn_sum(double v, double *red, int t) {
 }
 
 __device__ inline float attn_max(float v, float *red, int t) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = xor_max_wave(v);
     if ((t & 63) == 0) red[t >> 6] = v;
     __syncthreads();
     float r = red[0];
@@ -81,7 +83,7 @@ __device__ inline float head_rms_scale(const float *x, int hd, float eps) {
     const int lane = threadIdx.x & 63;
     double ss = 0.0;
     for (int i = lane; i < hd; i += 64) ss += static_cast<double>(x[i]) * static_cast<double>(x[i]);
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    ss = xor_sum_wave(ss);
     return 1.0f / sqrtf(static_cast<float>(ss / hd) + eps);
 }
 

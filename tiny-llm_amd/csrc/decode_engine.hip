@@ -28,10 +28,12 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "decode_attn.h"
 #include "decode_flow.h"
+#include "lane_sum.h"
 #include "tq_common.h"
 
 // The elementwise steps below round every product and sum separately, as the
@@ -51,7 +53,7 @@ constexpr int kArgmaxPerBlock = kArgmaxThreads * kArgmaxPerThread;
 // totals in wave order, so all threads hold the same value.
 template <int NT>
 __device__ double block_sum(double v, double *red) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = xor_sum_wave(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     double t = 0.0;
@@ -164,7 +166,17 @@ __device__ void better(float &bv, int &bi, float v, int i) {
 __device__ void block_argmax(float &bv, int &bi) {
     __shared__ float rv[kArgmaxThreads / 64];
     __shared__ int ri[kArgmaxThreads / 64];
-    for (int o = 32; o > 0; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    const int lane = threadIdx.x & 63;
+    const auto step = [&](auto dl) {  // lane l ^ dl's candidate, exchanged in registers
+        constexpr int DL = decltype(dl)::value;
+        better(bv, bi, lane_xor<DL>(bv, lane), __float_as_int(lane_xor<DL>(__int_as_float(bi), lane)));
+    };
+    step(std::integral_constant<int, 32>{});
+    step(std::integral_constant<int, 16>{});
+    step(std::integral_constant<int, 8>{});
+    step(std::integral_constant<int, 4>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 1>{});
     if ((threadIdx.x & 63) == 0) {
         rv[threadIdx.x >> 6] = bv;
         ri[threadIdx.x >> 6] = bi;

@@ -399,7 +399,7 @@ __device__ __attribute__((always_inline)) bool flow_final_norm(const FlowArgs &a
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
         for (int q = 0; q < PER; ++q) ss[s] += static_cast<double>(h[s][q]) * static_cast<double>(h[s][q]);
-        for (int o = 32; o > 0; o >>= 1) ss[s] += __shfl_xor(ss[s], o, 64);
+        ss[s] = xor_sum_wave(ss[s]);
         if ((threadIdx.x & 63) == 0) red[(threadIdx.x >> 6) + 8 * s] = ss[s];
     }
     __syncthreads();

@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void x_to_f16(const float *__restrict__ x, int
         v[i] = k < K ? xc[k] : 0.f;
         m = fmaxf(m, fabsf(v[i]));
     }
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = xor_max_wave(m);
     __shared__ float wm[4];
     if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
     __syncthreads();
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256) void x_to_f16_vec(const float *__restrict__ x,
 #pragma unroll
         for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[i][e]));
     }
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = xor_max_wave(m);
     __shared__ float wm[4];
     if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
     __syncthreads();
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void x_to_f16_long(const float *__restrict__ x
     const float *xc = x + static_cast<size_t>(n) * K;
     float m = 0.f;
     for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(xc[k]));
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = xor_max_wave(m);
     __shared__ float wm[4];
     if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
     __syncthreads();

@@ -59,15 +59,9 @@ constexpr size_t kLdsBytes = 160 * 1024;  // LDS per CU (gfx950)
 constexpr int kMaxDepth = 8;              // DMA ring slots at most
 constexpr int kMaxGroup = 3;              // matrices sharing x in one DMA-staged launch (qkv)
 
-__device__ inline float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
+__device__ inline float wave_max(float v) { return xor_max_wave(v); }
 
-__device__ inline float wave_sum(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
+__device__ inline float wave_sum(float v) { return xor_sum_wave(v); }
 
 // Position of element i of a group inside its 8-element block, in the order
 // the weight operand presents it: even elements (low nibbles) first, then odd.

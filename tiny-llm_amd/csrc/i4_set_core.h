@@ -97,7 +97,7 @@ __device__ __forceinline__ float half_group_int(const v4i &cd, unsigned hd, cons
 // Sum of v over the workgroup, in double, in a fixed order (each wave by shuffles, then the
 // kSetWaves wave sums in wave order).
 __device__ inline double set_block_sum(double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = xor_sum_wave(v);
     __shared__ double red[kSetWaves];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();

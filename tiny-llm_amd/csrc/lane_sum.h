@@ -88,5 +88,51 @@ __device__ __forceinline__ float lane_xor(float v, int lane) {
     }
 }
 
+// The value of lane l ^ DL for a double: both 32-bit halves moved by lane_xor (moves only).
+template <int DL>
+__device__ __forceinline__ double lane_xor_d(double v, int lane) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    const float lo = lane_xor<DL>(__builtin_bit_cast(float, static_cast<unsigned>(b)), lane);
+    const float hi = lane_xor<DL>(__builtin_bit_cast(float, static_cast<unsigned>(b >> 32)), lane);
+    return __builtin_bit_cast(double, (static_cast<unsigned long long>(__builtin_bit_cast(unsigned, hi)) << 32) |
+                                          __builtin_bit_cast(unsigned, lo));
+}
+
+// for (o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o): the same additions in the same order (each
+// lane adds the value of lane l ^ o), with the exchanges in registers instead of LDS permutes.
+__device__ __forceinline__ float xor_sum_wave(float v) {
+    const int lane = threadIdx.x & 63;
+    v += lane_xor<32>(v, lane);
+    v += lane_xor<16>(v, lane);
+    v += lane_xor<8>(v, lane);
+    v += lane_xor<4>(v, lane);
+    v += lane_xor<2>(v, lane);
+    v += lane_xor<1>(v, lane);
+    return v;
+}
+
+// The largest of the wave's 64 values, in every lane.
+__device__ __forceinline__ float xor_max_wave(float v) {
+    const int lane = threadIdx.x & 63;
+    v = fmaxf(v, lane_xor<32>(v, lane));
+    v = fmaxf(v, lane_xor<16>(v, lane));
+    v = fmaxf(v, lane_xor<8>(v, lane));
+    v = fmaxf(v, lane_xor<4>(v, lane));
+    v = fmaxf(v, lane_xor<2>(v, lane));
+    v = fmaxf(v, lane_xor<1>(v, lane));
+    return v;
+}
+
+__device__ __forceinline__ double xor_sum_wave(double v) {
+    const int lane = threadIdx.x & 63;
+    v += lane_xor_d<32>(v, lane);
+    v += lane_xor_d<16>(v, lane);
+    v += lane_xor_d<8>(v, lane);
+    v += lane_xor_d<4>(v, lane);
+    v += lane_xor_d<2>(v, lane);
+    v += lane_xor_d<1>(v, lane);
+    return v;
+}
+
 }  // namespace
 }  // namespace tqhip

@@ -297,7 +297,7 @@ struct Vq2StagedArgs {
 };
 template <int WAVES>
 __device__ inline double vq2_block_sum(double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = xor_sum_wave(v);
     __shared__ double red[WAVES];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
