@@ -32,6 +32,10 @@ CASES = {
     "i4_rotated": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1200, vocab=300, layers=1,
                        rotated=True),
     "head_dim256": dict(hidden=512, n_heads=2, n_kv_heads=1, head_dim=256, inter=768, vocab=300, layers=1),
+    # three layers: the fused layers' hidden state alternates hidden -> hidden2 -> hidden
+    "i4_3layers": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=400, layers=3),
+    "vq2_3layers": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=400, layers=3,
+                        vq2=True),
 }
 PROMPT = [11, 257, 3, 3, 0, 199, 42, 5, 123, 7, 64, 99]
 

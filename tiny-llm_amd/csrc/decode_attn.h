@@ -225,29 +225,43 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
         const float rescale = expf(m - m_new);
         l = l * rescale + static_cast<float>(csum);
         acc = acc * rescale;
+        // The slice's positions j = slice, slice + slices, ... < len, added to acc in position
+        // order (acc + p * v each). Branch-free, eight positions at a time: their LDS reads and
+        // cache loads all go out before the first add (with a branch per position each LDS read
+        // was waited for before the next was issued), reads past the chunk are clamped to its
+        // last score, and the terms of positions past it are dropped by a select.
+        const float vpos = S.vs[d];  // position pos: this step's own value row, from LDS
         int j = slice;
         if (c0 == 0) {  // the first eight positions of the slice, loaded at entry
+            float sc8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) sc8[u] = S.sc[min(slice + u * slices, len - 1)];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int jj = slice + u * slices;
-                if (jj < len) acc += S.sc[jj] * (jj == pos ? S.vs[d] : vreg[u]);
+                const float term = sc8[u] * (jj == pos ? vpos : vreg[u]);
+                acc = jj < len ? acc + term : acc;
             }
             j = slice + 8 * slices;
         }
-        // Eight positions' loads issued together, then added in position order.
-        for (; j + 7 * slices < len; j += 8 * slices) {
-            float vb8[8];
+        for (; j < len; j += 8 * slices) {
+            float vb8[8], sc8[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int p = c0 + j + u * slices;
-                vb8[u] = p == pos ? S.vs[d] : attn_ld(vh + static_cast<size_t>(p) * hd + d);
+                const int jj = j + u * slices, p = c0 + jj;
+                // rows past the chunk and row pos (being written by this step) are not read: row 0
+                // instead, whose term is dropped (pos > 0 whenever a position past the first
+                // eight exists)
+                const bool use = jj < len && p != pos;
+                vb8[u] = attn_ld(vh + static_cast<size_t>(use ? p : 0) * hd + d);
+                sc8[u] = S.sc[min(jj, len - 1)];
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc += S.sc[j + u * slices] * vb8[u];
-        }
-        for (; j < len; j += slices) {
-            const int p = c0 + j;
-            acc += S.sc[j] * (p == pos ? S.vs[d] : attn_ld(vh + static_cast<size_t>(p) * hd + d));
+            for (int u = 0; u < 8; ++u) {
+                const int jj = j + u * slices;
+                const float term = sc8[u] * (c0 + jj == pos ? vpos : vb8[u]);
+                acc = jj < len ? acc + term : acc;
+            }
         }
         m = m_new;
         __syncthreads();
