@@ -109,21 +109,24 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
     const float *kh = kcache + static_cast<size_t>(kvh) * max_seq * hd;
     const float *vh = vcache + static_cast<size_t>(kvh) * max_seq * hd;
 
+    // The prefetch loads are unconditional (a thread without a row to prefetch reads row 0, which
+    // every step before this one has written, and never uses it): loads under branches leave the
+    // compiler unable to count them, and its waits for q / k / v then wait for every load.
     float4 kreg[kPrefetchKey ? HD / 4 : 1];
     const bool key_pre = kPrefetchKey && t < seq && t != pos && t < kAttnChunk;
     if constexpr (kPrefetchKey) {
-        if (key_pre) {
-            const float *kr = kh + static_cast<size_t>(t) * hd;
+        const float *kr = kh + static_cast<size_t>(key_pre ? t : 0) * hd;
 #pragma unroll
-            for (int i = 0; i < HD / 4; ++i) kreg[i] = attn_ld4(kr + 4 * i);
-        }
+        for (int i = 0; i < HD / 4; ++i) kreg[i] = attn_ld4(kr + 4 * i);
     }
     float vreg[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int p = slice + u * slices;
-        vreg[u] = p < seq && p != pos ? attn_ld(vh + static_cast<size_t>(p) * hd + d) : 0.0f;
+        vreg[u] = attn_ld(vh + static_cast<size_t>(p < seq && p != pos ? p : 0) * hd + d);
     }
+    // the q / k norm weights of element t (files without them: the key cache instead, unused)
+    const float qnw = attn_ld((qn ? qn : kh) + (t < hd ? t : 0)), knw = attn_ld((kn ? kn : kh) + (t < hd ? t : 0));
     float c = 0.0f, s = 0.0f;
     if (t < half) {
         const float inv_freq = powf(theta, -static_cast<float>(2 * t) / static_cast<float>(hd));
@@ -148,8 +151,8 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
         }
         __syncthreads();
         if (t < hd) {
-            S.qs[t] = (S.qs[t] * S.norm_scale[0]) * qn[t];
-            S.ks[t] = (S.ks[t] * S.norm_scale[1]) * kn[t];
+            S.qs[t] = (S.qs[t] * S.norm_scale[0]) * qnw;
+            S.ks[t] = (S.ks[t] * S.norm_scale[1]) * knw;
         }
         __syncthreads();
     }

@@ -130,12 +130,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step(
     __shared__ AttnShared sh;
     const int t = threadIdx.x;
     const int head = blockIdx.x, kvh = head / heads_per_kv;
+    // q / k / v and their biases do not depend on the position: their loads go out before the
+    // position's, and the fetch below only adds the biases (the KV-cache prefetch, which needs
+    // the position, then does not delay them)
+    // (unconditional loads, so that the compiler can count them: threads past the head and absent
+    // biases read element 0 of the projection instead, which they never use)
+    const int qi = t < HD ? head * HD + t : 0, ki = t < HD ? kvh * HD + t : 0;
+    const float rq = q[qi], rk = k[ki], rv = v[ki];
+    const float bq = (qb ? qb : q)[qi], bk = (kb ? kb : k)[ki], bv = (vb ? vb : v)[ki];
+    __builtin_amdgcn_sched_barrier(0);
     const auto fetch = [&](float &qv, float &kv, float &vv) {
         if (t < HD) {
-            const int qi = head * HD + t, ki = kvh * HD + t;
-            qv = qb ? q[qi] + qb[qi] : q[qi];
-            kv = kb ? k[ki] + kb[ki] : k[ki];
-            vv = vb ? v[ki] + vb[ki] : v[ki];
+            qv = qb ? rq + bq : rq;
+            kv = kb ? rk + bk : rk;
+            vv = vb ? rv + bv : rv;
         }
         return true;
     };
