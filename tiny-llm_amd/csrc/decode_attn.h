@@ -96,7 +96,7 @@ __device__ inline float head_rms_scale(const float *x, int hd, float eps) {
 // keeps a workgroup's barriers in step. out(i, value) stores output element i of the
 // attention vector (head * HD + d). PREFETCH_KEY: thread t loads its key row at entry into
 // registers (HD / 4 of them); the dot products are the same either way.
-template <int HD, bool PREFETCH_KEY = (HD <= 128), typename Fetch, typename Out>
+template <int HD, bool PREFETCH_KEY = (HD <= 128), int NV = 8, typename Fetch, typename Out>
 __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_per_kv, Fetch fetch, const float *qn,
                                       const float *kn, float *kcache, float *vcache, int pos, int max_seq, float theta,
                                       float eps, float scale, bool writes, Out out) {
@@ -119,7 +119,8 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
 #pragma unroll
         for (int i = 0; i < HD / 4; ++i) kreg[i] = attn_ld4(kr + 4 * i);
     }
-    float vreg[8];
+    static_assert(NV == 8 || NV == 16, "value rows loaded ahead: 8 at entry, 8 more after q / k / v");
+    float vreg[NV];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int p = slice + u * slices;
@@ -137,6 +138,11 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
     float qv = 0.0f, kv = 0.0f, vv = 0.0f;
     __builtin_amdgcn_sched_barrier(0);  // the cache loads above stay ahead of fetch's waits
     if (!fetch(qv, kv, vv)) return false;
+#pragma unroll
+    for (int u = 8; u < NV; ++u) {  // the next value rows, in flight through the scores and the softmax
+        const int p = slice + u * slices;
+        vreg[u] = attn_ld(vh + static_cast<size_t>(p < seq && p != pos ? p : 0) * hd + d);
+    }
     if (t < hd) {
         S.qs[t] = qv;
         S.ks[t] = kv;
@@ -235,17 +241,17 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
         // last score, and the terms of positions past it are dropped by a select.
         const float vpos = S.vs[d];  // position pos: this step's own value row, from LDS
         int j = slice;
-        if (c0 == 0) {  // the first eight positions of the slice, loaded at entry
-            float sc8[8];
+        if (c0 == 0) {  // the first NV positions of the slice, loaded ahead
+            float scv[NV];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) sc8[u] = S.sc[min(slice + u * slices, len - 1)];
+            for (int u = 0; u < NV; ++u) scv[u] = S.sc[min(slice + u * slices, len - 1)];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < NV; ++u) {
                 const int jj = slice + u * slices;
-                const float term = sc8[u] * (jj == pos ? vpos : vreg[u]);
+                const float term = scv[u] * (jj == pos ? vpos : vreg[u]);
                 acc = jj < len ? acc + term : acc;
             }
-            j = slice + 8 * slices;
+            j = slice + NV * slices;
         }
         for (; j < len; j += 8 * slices) {
             float vb8[8], sc8[8];
@@ -254,7 +260,7 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
                 const int jj = j + u * slices, p = c0 + jj;
                 // rows past the chunk and row pos (being written by this step) are not read: row 0
                 // instead, whose term is dropped (pos > 0 whenever a position past the first
-                // eight exists)
+                // NV exists)
                 const bool use = jj < len && p != pos;
                 vb8[u] = attn_ld(vh + static_cast<size_t>(use ? p : 0) * hd + d);
                 sc8[u] = S.sc[min(jj, len - 1)];

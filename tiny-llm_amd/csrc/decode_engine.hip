@@ -147,8 +147,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step(
         }
         return true;
     };
-    attention_head<HD>(sh, t, head, heads_per_kv, fetch, qn, kn, kcache, vcache, *pos_ptr, max_seq, theta, eps, scale,
-                       true, [&](int i, float o) { out[i] = o; });
+    attention_head<HD, (HD <= 128), 16>(sh, t, head, heads_per_kv, fetch, qn, kn, kcache, vcache, *pos_ptr, max_seq,
+                                        theta, eps, scale, true, [&](int i, float o) { out[i] = o; });
 }
 
 // gate = silu(gate) * up (swiglu_ref, kernels/silu/swiglu_ref.cpp).
