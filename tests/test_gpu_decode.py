@@ -36,6 +36,8 @@ CASES = {
     "i4_3layers": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=400, layers=3),
     "vq2_3layers": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=400, layers=3,
                         vq2=True),
+    # rows of more than 1024 elements everywhere (the set kernel's long-row shapes)
+    "wide_h1536": dict(hidden=1536, n_heads=12, n_kv_heads=2, head_dim=128, inter=2048, vocab=400, layers=2),
 }
 PROMPT = [11, 257, 3, 3, 0, 199, 42, 5, 123, 7, 64, 99]
 
@@ -101,6 +103,27 @@ def test_fused_layers_match_unfused(gpu, tmp_path, monkeypatch, case):
         assert same == len(PROMPT), case
     fused.close()
     plain.close()
+
+
+@pytest.mark.parametrize("case", ["qwen25_0p5b_2layers", "qwen3_qknorm_hd128", "i4_3layers", "wide_h1536"])
+def test_glu_gate_up_matches_separate(gpu, tmp_path, monkeypatch, case):
+    """Fused i4 layers run gate/up as one launch that stores silu(gate) * up (each workgroup
+    computes a row of gate and the same row of up), and down with no prologue. With
+    TQHIP_DECODE_NO_GLU=1 the engine stores gate and up and forms SwiGLU in down's prologue
+    instead. The rows and SwiGLU are the same arithmetic either way, so every step's logits must
+    be the same bits."""
+    m, cfg, _ = open_model(gpu, tmp_path, case)
+    glu = gpu.DecodeEngine(m, 32)
+    monkeypatch.setenv("TQHIP_DECODE_NO_GLU", "1")
+    sep = gpu.DecodeEngine(m, 32)
+    monkeypatch.delenv("TQHIP_DECODE_NO_GLU")
+    for i, t in enumerate(PROMPT):
+        t %= cfg["vocab_size"]
+        a, b = glu.step(t), sep.step(t)
+        assert a == b, (case, i)
+        assert np.array_equal(glu.logits().view(np.uint32), sep.logits().view(np.uint32)), (case, i)
+    glu.close()
+    sep.close()
 
 
 def test_greedy_generation_and_reset_replay(gpu, tmp_path):

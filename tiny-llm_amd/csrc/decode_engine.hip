@@ -258,6 +258,9 @@ struct Engine {
     // activation prologue), and the layers' hidden states alternate between hidden and hidden2.
     bool fused = false;
     bool fused_rot = false;  // VQ2 rotations inside the matvec launches (unless TQHIP_DECODE_UNFUSED)
+    // Fused i4 layers: gate/up as one launch storing silu(gate) * up, down without a prologue
+    // (TQHIP_DECODE_NO_GLU=1: gate and up stored, SwiGLU in down's prologue; the same bits)
+    bool glu = false;
     float *hidden2 = nullptr;
     size_t rotbuf_floats = 0;
     int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next, run, flow error
@@ -402,8 +405,16 @@ int forward(Engine &e) {
             // gate/up read rmsnorm(cur + o) * post_ln; down reads silu(gate) * up
             const I4Mat m2[2] = {{L.gate, cur, e.gate, I, H}, {L.up, cur, e.up, I, H}};
             const Rot *r2[2] = {&L.rg, &L.ru}, *r1[1] = {&L.rd};
-            if ((st = fused_set(2, m2, r2, SetPrologue{2, nullptr, e.o, nullptr, L.post_ln, nullptr, eps})) != kOk)
-                return st;
+            const SetPrologue post{2, nullptr, e.o, nullptr, L.post_ln, nullptr, eps};
+            if (e.glu) {  // i4: silu(gate) * up formed by the gate/up launch, down without a prologue
+                st = launch_i4_matvec_glu(m2[0], m2[1], e.gs, post, s);
+                if (st != kOk) return st == kNotFused ? static_cast<int>(kLaunchFailed) : st;
+                const I4Mat m1{L.down, e.gate, e.ffn, H, I};
+                st = launch_i4_matvec_set_fit(1, &m1, e.gs, s);
+                if (st != kOk) return st == kNotFused ? static_cast<int>(kLaunchFailed) : st;
+                continue;
+            }
+            if ((st = fused_set(2, m2, r2, post)) != kOk) return st;
             const I4Mat m1[1] = {{L.down, e.gate, e.ffn, H, I}};
             if ((st = fused_set(1, m1, r1, SetPrologue{1, e.up, nullptr, nullptr, nullptr, nullptr, eps})) != kOk)
                 return st;
@@ -774,6 +785,8 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
                              set_kernel_takes(is, e->gs)) ||
                             (e->pd == 4 && rot_sets && vq2_sets));
     e->fused_rot = e->pd == 4 && !unfused;
+    const char *no_glu = std::getenv("TQHIP_DECODE_NO_GLU");
+    e->glu = e->fused && e->pd == 3 && !(no_glu && no_glu[0] == '1');
     float *conv = reinterpret_cast<float *>(base + offs[15]);
     for (const F16Vec &f : f16s) {
         f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);

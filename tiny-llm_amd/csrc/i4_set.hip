@@ -52,12 +52,15 @@ struct SetArgs {
 };
 
 // XM: the activation prologue (0 none; 1 x = silu(x) * x2; 2 x = rmsnorm((x + d1) + d2) * nw,
-// workgroup 0 storing the sum to hout), with its operands in pro.
-template <int S, int R, int XM>
-__device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char *lds, const SetPrologue &pro) {
+// workgroup 0 storing the sum to hout), with its operands in pro. GLU: every row of m is computed
+// together with the same row of w2 (a matrix of m's shape reading the same x), and the row's
+// output is swiglu(m row, w2 row), as the separate outputs would give it in a SwiGLU prologue.
+template <int S, int R, int XM, bool GLU = false>
+__device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char *lds, const SetPrologue &pro,
+                                         const uint8_t *w2 = nullptr) {
     // 16-byte activation loads per thread: the chunks of the widest row of this shape
     constexpr int NX = ((S == 0 ? 256 : 512 * S) + kSetThreads - 1) / kSetThreads;
-    constexpr int NR = R;                   // rows per lane
+    constexpr int NR = GLU ? 2 * R : R;     // rows per lane (GLU: R of m, then the same R of w2)
     constexpr int NS = S == 0 ? 1 : S;      // half-group slots per lane
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -101,6 +104,7 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
     // half-wave's row goes into the per-lane offset
     const int base = S == 0 ? (blk * kSetWaves + wave) * 2 * R : (blk * kSetWaves + wave) * R;
     const __amdgpu_buffer_rsrc_t wr = rows_rsrc(m.w, m.M, rb, base);  // rows past the matrix read 0
+    const __amdgpu_buffer_rsrc_t wr2 = rows_rsrc(GLU ? w2 : m.w, m.M, rb, base);
     // Half of the lane's (row, slot) loads go out now, the other half once the activations
     // are converted. The activations are cold (a step's weights stream through every cache),
     // so their read waits in the memory queues behind whatever weight reads went out before
@@ -112,10 +116,12 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
     constexpr int NU = NR * NS, NFIRST = NU > 1 ? NU / 2 : 1;
     auto issue = [&](int q) {  // row q / NS, slot q % NS
         const int r = q / NS, sl = q % NS;
+        const int rr = GLU ? r % R : r;  // GLU: rows R.. are the same rows of w2
         const int unit = u + 64 * sl;
-        const int off = (S == 0 ? 2 * r + half : r) * rb + (kI4Header + 32) * (unit >> 1);
-        hd[q] = __builtin_amdgcn_raw_buffer_load_b32(wr, off, 0, 0);
-        cd[q] = __builtin_amdgcn_raw_buffer_load_b128(wr, off + kI4Header + 16 * (unit & 1), 0, 0);
+        const int off = (S == 0 ? 2 * rr + half : rr) * rb + (kI4Header + 32) * (unit >> 1);
+        const __amdgpu_buffer_rsrc_t rs = GLU && r >= R ? wr2 : wr;
+        hd[q] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        cd[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + kI4Header + 16 * (unit & 1), 0, 0);
     };
 #pragma unroll
     for (int q = 0; q < NFIRST; ++q) issue(q);
@@ -184,10 +190,15 @@ __device__ __forceinline__ void set_rows(const SetMat &m, int blk, unsigned char
         }
     }
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
+    for (int r = 0; r < R; ++r) {
         const int row = base + (S == 0 ? 2 * r + half : r);
         const float sum = S == 0 ? sum_half_wave(p[r]) : sum_wave(p[r]);
-        if (u == 0 && row < m.M) store_y(m.y + row, sum);
+        if constexpr (GLU) {
+            const float sum2 = S == 0 ? sum_half_wave(p[R + r]) : sum_wave(p[R + r]);
+            if (u == 0 && row < m.M) store_y(m.y + row, swiglu1(sum, sum2));
+        } else {
+            if (u == 0 && row < m.M) store_y(m.y + row, sum);
+        }
     }
 }
 
@@ -219,6 +230,17 @@ __global__ __launch_bounds__(kSetThreads) void i4_matvec_set(SetArgs<C> a) {
     } else {
         set_rows<5, RL, XM>(m, blk, lds, a.pro);
     }
+}
+
+// A fused decode layer's gate / up pair as one launch with SwiGLU applied to its outputs: each
+// workgroup computes rows of gate (m[0]) and the same rows of up (m[1]) from the shared x with the
+// prologue pro, and stores act = silu(gate) * up to m[0].y, which the down projection then reads
+// with no prologue. Every row has the bits its set launch gives it, and act the bits the SwiGLU
+// prologue forms from the two outputs (the same swiglu1).
+template <int S, int XM>
+__global__ __launch_bounds__(kSetThreads) void i4_matvec_glu(SetArgs<2> a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    set_rows<S, 1, XM, true>(a.m[0], blockIdx.x, lds, a.pro, a.m[1].w);
 }
 
 // Shape of a matrix in the set kernel, or -1 when the kernel does not take it:
@@ -357,6 +379,33 @@ int launch_i4_matvec_set_pro(int n, const I4Mat *mats, int group_size, const Set
         if (shape[i] < 0 || mats[i].M < 1 || mats[i].x != mats[0].x || mats[i].K != mats[0].K) return kNotFused;
     }
     return launch_set(mats, shape, n, stream, &pro);
+}
+
+int launch_i4_matvec_glu(const I4Mat &gate, const I4Mat &up, int group_size, const SetPrologue &pro,
+                         hipStream_t stream) {
+    const auto al = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const int shape = set_shape(gate, group_size);
+    if (shape < 0 || set_shape(up, group_size) != shape || gate.M < 1 || up.M != gate.M || up.K != gate.K ||
+        up.x != gate.x || !gate.w || !up.w || !gate.x || !gate.y || pro.kind != 2 || !pro.nw || !al(pro.d1) ||
+        !al(pro.d2) || !al(pro.nw) || !al(pro.hout))
+        return kNotFused;
+    SetArgs<2> a{};
+    a.m[0] = SetMat{gate.w, gate.x, gate.y, gate.M, gate.K, 0, shape};
+    a.m[1] = SetMat{up.w, up.x, nullptr, up.M, up.K, 0, shape};
+    a.n = 2;
+    a.pro = pro;
+    const int per = shape == 0 ? 2 * kSetWaves : kSetWaves;  // rows (pairs) per workgroup
+    const dim3 grid((gate.M + per - 1) / per), block(kSetThreads);
+    const size_t lds = static_cast<size_t>(2 * ((gate.K + 63) / 64)) * (4 * kBlockBytes + 8);
+    switch (shape) {
+        case 0: hipLaunchKernelGGL((i4_matvec_glu<0, 2>), grid, block, lds, stream, a); break;
+        case 1: hipLaunchKernelGGL((i4_matvec_glu<1, 2>), grid, block, lds, stream, a); break;
+        case 2: hipLaunchKernelGGL((i4_matvec_glu<2, 2>), grid, block, lds, stream, a); break;
+        case 3: hipLaunchKernelGGL((i4_matvec_glu<3, 2>), grid, block, lds, stream, a); break;
+        case 4: hipLaunchKernelGGL((i4_matvec_glu<4, 2>), grid, block, lds, stream, a); break;
+        default: hipLaunchKernelGGL((i4_matvec_glu<5, 2>), grid, block, lds, stream, a); break;
+    }
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
 int launch_i4_matvec_set(int n, const I4Mat *mats, int group_size, hipStream_t stream) {

@@ -93,6 +93,12 @@ struct SetPrologue {
 int launch_i4_matvec_set_pro(int n, const I4Mat *mats, int group_size, const SetPrologue &pro, hipStream_t stream);
 // Whether the set kernel takes rows of K elements at this group size (with x 16-byte aligned).
 bool set_kernel_takes(int K, int group_size);
+// A decode layer's gate / up pair (same shape, same x) with the kind-2 prologue pro, as one launch
+// storing act = silu(gate) * up to gate.y (up.y is not written): each value has the bits of the
+// set launch of the pair followed by a kind-1 (SwiGLU) prologue. kNotFused when the set kernel
+// does not take the shape or an operand is misaligned.
+int launch_i4_matvec_glu(const I4Mat &gate, const I4Mat &up, int group_size, const SetPrologue &pro,
+                         hipStream_t stream);
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
 // n independent VQ2 matvecs (I4Mat: weights, activations, output, shape) in as few launches as
 // the one-wave-per-row kernel allows; each output has the bits launch_vq2_matvec gives it.
