@@ -112,19 +112,25 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
     // The prefetch loads are unconditional (a thread without a row to prefetch reads row 0, which
     // every step before this one has written, and never uses it): loads under branches leave the
     // compiler unable to count them, and its waits for q / k / v then wait for every load.
+    // The first wave's key rows (positions 0..63) and the first eight value rows of each slice are
+    // requested without waiting for the position, whose load is a round trip of its own: rows past
+    // it (but below max_seq) are read and never used. The other waves' key rows go out after q / k /
+    // v, once the position is known, so that a long cache is not read beyond the sequence.
     float4 kreg[kPrefetchKey ? HD / 4 : 1];
     const bool key_pre = kPrefetchKey && t < seq && t != pos && t < kAttnChunk;
     if constexpr (kPrefetchKey) {
-        const float *kr = kh + static_cast<size_t>(key_pre ? t : 0) * hd;
+        if (t < 64) {  // (wave-uniform) the other waves' rows go out once q / k / v are in, below
+            const float *kr = kh + static_cast<size_t>(t < max_seq ? t : 0) * hd;
 #pragma unroll
-        for (int i = 0; i < HD / 4; ++i) kreg[i] = attn_ld4(kr + 4 * i);
+            for (int i = 0; i < HD / 4; ++i) kreg[i] = attn_ld4(kr + 4 * i);
+        }
     }
     static_assert(NV == 8 || NV == 16, "value rows loaded ahead: 8 at entry, 8 more after q / k / v");
     float vreg[NV];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
         const int p = slice + u * slices;
-        vreg[u] = attn_ld(vh + static_cast<size_t>(p < seq && p != pos ? p : 0) * hd + d);
+        vreg[u] = attn_ld(vh + static_cast<size_t>(p < max_seq ? p : 0) * hd + d);
     }
     // the q / k norm weights of element t (files without them: the key cache instead, unused)
     const float qnw = attn_ld((qn ? qn : kh) + (t < hd ? t : 0)), knw = attn_ld((kn ? kn : kh) + (t < hd ? t : 0));
@@ -138,10 +144,17 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
     float qv = 0.0f, kv = 0.0f, vv = 0.0f;
     __builtin_amdgcn_sched_barrier(0);  // the cache loads above stay ahead of fetch's waits
     if (!fetch(qv, kv, vv)) return false;
+    if constexpr (kPrefetchKey) {
+        if (t >= 64) {  // (wave-uniform) rows 64.. of the sequence, now that the position is known
+            const float *kr = kh + static_cast<size_t>(key_pre ? t : 0) * hd;
+#pragma unroll
+            for (int i = 0; i < HD / 4; ++i) kreg[i] = attn_ld4(kr + 4 * i);
+        }
+    }
 #pragma unroll
     for (int u = 8; u < NV; ++u) {  // the next value rows, in flight through the scores and the softmax
         const int p = slice + u * slices;
-        vreg[u] = attn_ld(vh + static_cast<size_t>(p < seq && p != pos ? p : 0) * hd + d);
+        vreg[u] = attn_ld(vh + static_cast<size_t>(p < max_seq ? p : 0) * hd + d);
     }
     if (t < hd) {
         S.qs[t] = qv;

@@ -124,9 +124,9 @@ __global__ void embed_f32_row(const float *table, const int *token, float *out, 
 // projections, biases added at entry.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_step(
-    const float *q, const float *k, const float *v, const float *qb, const float *kb, const float *vb,
-    const float *qn, const float *kn, float *kcache, float *vcache, float *out, const int *pos_ptr, int heads_per_kv,
-    int max_seq, float theta, float eps, float scale) {
+    int heads_per_kv, int max_seq, float theta, float eps, float scale, const int *pos_ptr, const float *q,
+    const float *k, const float *v, const float *qb, const float *kb, const float *vb, const float *qn,
+    const float *kn, float *kcache, float *vcache, float *out) {
     __shared__ AttnShared sh;
     const int t = threadIdx.x;
     const int head = blockIdx.x, kvh = head / heads_per_kv;
@@ -397,9 +397,9 @@ int forward(Engine &e) {
         }
         auto attn = e.c.head_dim == 64 ? attention_step<64> : e.c.head_dim == 128 ? attention_step<128>
                                                                                   : attention_step<256>;
-        attn<<<e.c.n_heads, kAttnThreads, 0, s>>>(e.q, e.k, e.v, L.qb, L.kb, L.vb, L.qn, L.kn, kc, vc, e.attn,
-                                                  e.dev_io, e.c.n_heads / e.c.n_kv_heads, e.max_seq, e.c.rope_theta,
-                                                  e.c.rms_norm_eps, e.attn_scale);
+        attn<<<e.c.n_heads, kAttnThreads, 0, s>>>(e.c.n_heads / e.c.n_kv_heads, e.max_seq, e.c.rope_theta,
+                                                  e.c.rms_norm_eps, e.attn_scale, e.dev_io, e.q, e.k, e.v, L.qb,
+                                                  L.kb, L.vb, L.qn, L.kn, kc, vc, e.attn);
         if ((st = mvr(e, L.o, e.pd, e.attn, e.o, H, e.q_dim, L.ro, s)) != kOk) return st;
         if (e.fused) {
             // gate/up read rmsnorm(cur + o) * post_ln; down reads silu(gate) * up
