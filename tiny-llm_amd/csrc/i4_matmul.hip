@@ -656,12 +656,15 @@ __global__ __launch_bounds__(kThreads) void i4_matmul_mfma2(const uint8_t *__res
 //   the work: without the MFMAs or without the dequantization the time hardly
 //   changes; without the loads of W and X it drops by three quarters. The loop is
 //   bound by the time each workgroup's loads take to arrive, not by arithmetic.
-__device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char *st, const int *xvo, int nx, int xso,
-                                        int wave) {
+// The X DMAs d0 .. d0 + nx - 1 of a step (1 KB each, at byte 1024 d of the stage); nx <= ND.
+template <int ND>
+__device__ __forceinline__ void issue_x(__amdgpu_buffer_rsrc_t xr, unsigned char *st, const int *xvo, int nx, int d0,
+                                        int xso) {
 #pragma unroll
-    for (int q = 0; q < nx; ++q)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xr, (__attribute__((address_space(3))) void *)(st + 1024 * (nx * wave + q)), 16, xvo[q], xso, 0, 0);
+    for (int q = 0; q < ND; ++q)
+        if (q < nx)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void *)(st + 1024 * (d0 + q)), 16, xvo[q], xso, 0, 0);
 }
 
 template <int WN, int S, int NWV>
@@ -672,9 +675,10 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
     constexpr int BN = 32 * WN;
     constexpr int BM = 32 * NWV;
     constexpr int XStage = BN * 128;
-    constexpr int XD = 4 * WN / NWV;  // X DMAs per wave per step
-    constexpr int P = 2 + XD;         // loads per wave per step: W 4 + 16 bytes, the X DMAs
-    static_assert(4 * WN % NWV == 0, "X DMAs split evenly over the waves");
+    // The step's 4 WN X DMAs (1 KB each) are dealt out in order: waves below XR issue XA + 1 of
+    // them, the others XA. P: this wave's loads per step (W 4 + 16 bytes, its X DMAs).
+    constexpr int XA = 4 * WN / NWV, XR = 4 * WN % NWV;
+    constexpr int XD = XA + (XR ? 1 : 0);
     constexpr int kGroupBytes = 36;
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
@@ -692,10 +696,11 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
     // 32 h + 8 kk + e, p = pk_slot(e), on the A (W) and the B (X) side.
     const int li = lane & 31, h = lane >> 5;
     const int wvo = (32 * wave + li) * row_bytes;
-    int xvo[XD];
+    const int nx = XA + (wave < XR ? 1 : 0), d0 = XA * wave + min(wave, XR);
+    int xvo[XD > 0 ? XD : 1];
 #pragma unroll
     for (int q = 0; q < XD; ++q) {
-        const int p = 64 * (XD * wave + q) + lane;
+        const int p = 64 * min(d0 + q, 4 * WN - 1) + lane;
         const int r = p >> 3, c = (p & 7) ^ ((r >> 1) & 7);
         xvo[q] = r * Kp * 2 + 16 * c;
     }
@@ -716,7 +721,7 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
         const int so = kGroupBytes * min(s, groups - 1);  // (past the last step: in-row bytes, never used)
         hd[u] = __builtin_amdgcn_raw_buffer_load_b32(wr, wvo, so, 0);
         cd[u] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(wr, wvo + 4 + 16 * h, so, 0));
-        issue_x(xr, smem + u * XStage, xvo, XD, s * kStepK * 2, wave);
+        issue_x<XD>(xr, smem + u * XStage, xvo, nx, d0, s * kStepK * 2);
     };
     f16x acc[WN];
 #pragma unroll
@@ -742,8 +747,11 @@ __global__ __launch_bounds__(64 * NWV) void i4_matmul_g64(const uint8_t *__restr
     // memory pipeline has MFMAs in flight.
     auto round_step = [&](auto uc, int s, auto full) {
         constexpr int u = decltype(uc)::value;
-        wait_vm((S - 2) * P);  // this wave's loads of step s have landed
-        lds_barrier();         // every wave's X part has; step s - 1's stage is free
+        if (XR == 0 || wave < XR)  // this wave's loads of step s have landed
+            wait_vm((S - 2) * (2 + XD));
+        else
+            wait_vm((S - 2) * (2 + XA));
+        lds_barrier();  // every wave's X part has; step s - 1's stage is free
         if constexpr (decltype(full)::value) {
             compute(uc, 0, 2);
             issue(std::integral_constant<int, (u + S - 1) % S>{}, s + S - 1);
@@ -1196,7 +1204,7 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
     // The G = 64 kernel (packed-fp16 dequantization) takes X in its k-slot order; the other
     // kernels in natural order. Its workgroups address 32 NWV rows and 32 WN token rows of X
     // with 32-bit offsets.
-    const int g64_bm = wn == 1 ? 32 : 128;
+    const int g64_bm = wn == 1 ? 32 : wn == 2 ? 128 : 256;
     const bool g64 = group_size == 64 && static_cast<size_t>(g64_bm) * rb + Kp * 2 * 32 * wn < (1ull << 31);
     const bool lng = Kp > static_cast<size_t>(256 * kXRegs);
     const bool vec = !lng && K % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;  // 16-byte loads
@@ -1217,9 +1225,15 @@ int matmul_mfma(const uint8_t *w, const float *x, float *y, int M, int K, int N,
         // through LDS in 3-step chunks did not beat the loads straight into registers.
         // (At 512 tokens, 128 x 160 tiles with 1 wave per SIMD, 256 x 128 tiles of 8 waves and
         // W staged through LDS in 4-step chunks by 16-byte DMAs were no faster either.)
+        // Above 128 tokens: 256 x 96 tiles of 8 waves (one 32-row block each, W in registers)
+        // with a 3-step ring, 228 workgroups at 9728 x 512: 44.6-45.1 us per call against
+        // 46.3-47.2 for 128 x 96 tiles of 4 waves with a 4-step ring (a 4-step ring with 8 waves:
+        // 45.7-46.4; a 2-step ring: 60; the token tiles of a row tile on one XCD: no change).
+        // At 128 tokens the 4-step ring of 4 waves stays (3 steps: 26.2 us, 2: 41.1, 128 x 32
+        // tiles: 25.2, 256 x 32 tiles of 8 waves: 34.3, against 24.0).
         return wn == 1   ? launch_g64<1, 4, 1>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
                : wn == 2 ? launch_g64<2, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream)
-                         : launch_g64<3, 4, 4>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
+                         : launch_g64<3, 3, 8>(w, xh, xinv, y, M, N, K, ikp, irb, stream);
     }
     if (group_size == 64) {
         st = wn == 1   ? launch_tiles2<1, 64, 4>(w, xh, xinv, y, M, N, K, ikp, group_size, irb, stream)
