@@ -38,6 +38,9 @@ CASES = {
                         vq2=True),
     # rows of more than 1024 elements everywhere (the set kernel's long-row shapes)
     "wide_h1536": dict(hidden=1536, n_heads=12, n_kv_heads=2, head_dim=128, inter=2048, vocab=400, layers=2),
+    # a vocabulary past the set kernel's reach: the lm_head takes the register-path kernel, which
+    # forms each workgroup's argmax as it stores the logits
+    "vocab_70000": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=70000, layers=1),
 }
 PROMPT = [11, 257, 3, 3, 0, 199, 42, 5, 123, 7, 64, 99]
 
@@ -124,6 +127,28 @@ def test_glu_gate_up_matches_separate(gpu, tmp_path, monkeypatch, case):
         assert np.array_equal(glu.logits().view(np.uint32), sep.logits().view(np.uint32)), (case, i)
     glu.close()
     sep.close()
+
+
+@pytest.mark.parametrize("case", ["vocab_70000", "qwen25_0p5b_2layers"])
+def test_lm_head_argmax_matches_two_launch_argmax(gpu, tmp_path, monkeypatch, case):
+    """Where the i4 lm_head runs on the register-path kernel (vocabularies past the set kernel's
+    reach), each of its workgroups keeps the first row of its largest logit and one launch reduces
+    the partials; TQHIP_DECODE_NO_AMAX=1 keeps the two argmax launches over the stored logits.
+    Both take the first index of the largest value, so every token and every logit must agree
+    (at vocab 2000 both engines run the two-launch argmax)."""
+    m, cfg, _ = open_model(gpu, tmp_path, case)
+    fused = gpu.DecodeEngine(m, 32)
+    monkeypatch.setenv("TQHIP_DECODE_NO_AMAX", "1")
+    plain = gpu.DecodeEngine(m, 32)
+    monkeypatch.delenv("TQHIP_DECODE_NO_AMAX")
+    for i, t in enumerate(PROMPT):
+        t %= cfg["vocab_size"]
+        a, b = fused.step(t), plain.step(t)
+        lg = fused.logits()
+        assert np.array_equal(lg.view(np.uint32), plain.logits().view(np.uint32)), (case, i)
+        assert a == b == int(np.argmax(lg)), (case, i)
+    fused.close()
+    plain.close()
 
 
 def test_greedy_generation_and_reset_replay(gpu, tmp_path):

@@ -48,6 +48,7 @@ constexpr int kNormThreads = 1024;
 constexpr int kMaxHidden = 16 * kNormThreads;  // values per thread kept in registers
 constexpr int kArgmaxThreads = 256, kArgmaxPerThread = 8;
 constexpr int kArgmaxPerBlock = kArgmaxThreads * kArgmaxPerThread;
+constexpr int kArgmaxParts = 4096;  // argmax partial slots: blocks of argmax_partial or lm_head workgroups
 
 // Fixed-order block sum: a 64-lane butterfly, then every thread adds the wave
 // totals in wave order, so all threads hold the same value.
@@ -261,6 +262,10 @@ struct Engine {
     // Fused i4 layers: gate/up as one launch storing silu(gate) * up, down without a prologue
     // (TQHIP_DECODE_NO_GLU=1: gate and up stored, SwiGLU in down's prologue; the same bits)
     bool glu = false;
+    // An i4 lm_head on the register-path kernel forms each workgroup's argmax as it stores the
+    // logits, and one launch reduces the partials (TQHIP_DECODE_NO_AMAX=1: the two-launch argmax
+    // over the logits; the same token)
+    bool amax_fused = false;
     float *hidden2 = nullptr;
     size_t rotbuf_floats = 0;
     int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next, run, flow error
@@ -444,6 +449,14 @@ int forward(Engine &e) {
     if (e.fused) {  // the last layer's (cur + o) + ffn, normed with the final norm
         float *last = ((e.layers.size() - 1) & 1) ? e.hidden2 : e.hidden;
         launch_add_rmsnorm(last, e.o, e.ffn, e.final_norm, e.normed, H, eps, s);
+    }
+    if (e.amax_fused) {
+        int parts = 0;
+        st = launch_i4_matvec_amax(e.lm_head, e.normed, e.logits, e.c.vocab_size, H, e.gs, e.amax_v, e.amax_i,
+                                   kArgmaxParts, &parts, s);
+        if (st != kOk) return st == kNotFused ? kLaunchFailed : st;  // (chosen at create where it applies)
+        argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, parts, e.dev_io + 2);
+        return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
     }
     if ((st = mv(e, e.lm_head, e.lm_dtype, e.normed, e.logits, e.c.vocab_size, H, s)) != kOk) return st;
     argmax_partial<<<e.amax_blocks, kArgmaxThreads, 0, s>>>(e.logits, e.c.vocab_size, e.amax_v, e.amax_i);
@@ -732,7 +745,7 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     const size_t counts[] = {H, H, static_cast<size_t>(e->q_dim), static_cast<size_t>(e->kv_dim),
                              static_cast<size_t>(e->kv_dim), static_cast<size_t>(e->q_dim), H, I, I, H, V,
                              2 * static_cast<size_t>(c.n_layers) * e->layer_stride,
-                             static_cast<size_t>(e->amax_blocks), static_cast<size_t>(e->amax_blocks), 8,
+                             static_cast<size_t>(kArgmaxParts), static_cast<size_t>(kArgmaxParts), 8,
                              f16_floats, std::max<size_t>(std::max<size_t>(3 * H, I), e->q_dim), H,
                              // the data-flow step's tagged vectors (8 bytes per element): h0, h1, q, k, v,
                              // attn, o, act, ffn
@@ -787,6 +800,9 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
     e->fused_rot = e->pd == 4 && !unfused;
     const char *no_glu = std::getenv("TQHIP_DECODE_NO_GLU");
     e->glu = e->fused && e->pd == 3 && !(no_glu && no_glu[0] == '1');
+    const char *no_amax = std::getenv("TQHIP_DECODE_NO_AMAX");
+    e->amax_fused = e->lm_dtype == 3 && !(no_amax && no_amax[0] == '1') &&
+                    i4_matvec_amax_takes(e->lm_head, e->normed, e->logits, c.vocab_size, H, e->gs, kArgmaxParts);
     float *conv = reinterpret_cast<float *>(base + offs[15]);
     for (const F16Vec &f : f16s) {
         f16_to_f32<<<(f.n + 255) / 256, 256, 0, e->stream>>>(static_cast<const _Float16 *>(f.src), conv, f.n);

@@ -33,6 +33,7 @@
 #include "i4_lane.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace tqhip {
 namespace {
@@ -88,6 +89,10 @@ struct Geom {
     // DMA-staged kernel: 1..3 matrices sharing x (pair / qkv), their tiles
     // numbered one after the other; tile_end[j] = tiles of matrices 0..j.
     int ksplit;  // split-K kernel: workgroups (row-window parts) per tile
+    // register-path kernel with AMAX: each workgroup's largest output and its row (first row of
+    // equal values) at amax_v / amax_i [blockIdx.x]
+    float *amax_v;
+    int *amax_i;
     int nmat;
     int tile_end[kMaxGroup];
     int mrows[kMaxGroup];
@@ -707,12 +712,17 @@ __global__ __launch_bounds__(64 * NWMAX, dma_waves_per_simd(CPW)) void i4_matvec
 // workgroups (blockIdx.x + k * gridDim.x) across the 1..3 matrices of gm.
 // Every wave issues the same loads for every tile slot (zero-length loads past
 // its last tile), so the compiler's waits count exactly the loads in flight.
-template <int GT, int CPW, int NWMAX, int P, bool GROUP>
+template <int GT, int CPW, int NWMAX, int P, bool GROUP, bool AMAX = false>
 __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(const uint8_t *__restrict__ w,
                                                                          const float *__restrict__ x,
                                                                          float *__restrict__ y, Geom gm) {
     // GROUP: 1..3 matrices through gm.mw / gm.my / gm.mrows; else the one
     // matrix w -> y of gm.M rows (fewer scalar instructions per tile)
+    // AMAX (one matrix): the workgroup's argmax as well (argmax_ref: the first row of the
+    // largest value; a NaN is never taken), one partial per workgroup
+    static_assert(!(AMAX && GROUP), "argmax of one matrix");
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -834,7 +844,37 @@ __global__ __launch_bounds__(64 * NWMAX, kPipeWavesPerSimd) void i4_matvec_pipe(
                 }
                 const TileRef r = tile_of(wg + k * nwg);
                 const int row = r.tile * kTile + lane;
-                if (row < r.M) store_y(r.y + row, sum);
+                if (row < r.M) {
+                    store_y(r.y + row, sum);
+                    if constexpr (AMAX) {
+                        if (sum > bv || (sum == bv && row < bi)) {
+                            bv = sum;
+                            bi = row;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (AMAX) {
+        static_assert(kTile == 16, "candidates in lanes 0..15");
+        if (wave == 0) {  // lanes 0..15 hold the candidates, the others (-inf, max)
+            const auto step = [&](auto dl) {
+                constexpr int DL = decltype(dl)::value;
+                const float v = lane_xor<DL>(bv, lane);
+                const int i = __float_as_int(lane_xor<DL>(__int_as_float(bi), lane));
+                if (v > bv || (v == bv && i < bi)) {
+                    bv = v;
+                    bi = i;
+                }
+            };
+            step(std::integral_constant<int, 8>{});
+            step(std::integral_constant<int, 4>{});
+            step(std::integral_constant<int, 2>{});
+            step(std::integral_constant<int, 1>{});
+            if (lane == 0) {
+                gm.amax_v[blockIdx.x] = bv;
+                gm.amax_i[blockIdx.x] = bi;
             }
         }
     }
@@ -1242,15 +1282,25 @@ int launch_with_lds(KernelT kernel, int grid, int threads, size_t lds, const uin
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
-template <int GT, int CPW, int NWMAX>
+int pipe_grid(int tiles) { return std::max(1, std::min(tiles, device_cu_count() * kPipeWgsPerCu)); }
+
+template <int GT, int CPW, int NWMAX, bool AMAX = false>
 int launch_pipe(const uint8_t *w, const float *x, float *y, const Geom &gm, hipStream_t stream) {
     const int tiles = gm.tile_end[gm.nmat - 1];
     const int NWP = (gm.NW + 3) & ~3;
     const size_t lds = static_cast<size_t>(2 * kTile * NWP) * 4 + xplanes_bytes(gm) + 16;
-    const int grid = std::max(1, std::min(tiles, device_cu_count() * kPipeWgsPerCu));
+    const int grid = pipe_grid(tiles);
     // one tile per workgroup: nothing to load ahead (a second register slot
     // would only add a round of zero-length loads and an idle iteration)
     const bool one = tiles <= grid;
+    if constexpr (AMAX) {
+        static size_t limit_a1 = 0, limit_a = 0;
+        if (gm.nmat != 1) return kBadShape;
+        return one ? launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, 1, false, true>, grid, 64 * gm.NW, lds, w, x, y,
+                                     gm, stream, limit_a1)
+                   : launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, kPipeSlots, false, true>, grid, 64 * gm.NW, lds, w,
+                                     x, y, gm, stream, limit_a);
+    }
     if (gm.nmat > 1) {
         static size_t limit_g1 = 0, limit_g = 0;
         return one ? launch_with_lds(i4_matvec_pipe<GT, CPW, NWMAX, 1, true>, grid, 64 * gm.NW, lds, w, x, y, gm,
@@ -1459,15 +1509,11 @@ int launch_i4_matvec_generic(const uint8_t *w, const float *x, float *y, int out
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
-int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
-                     hipStream_t stream) {
-    if (out_dim < 1 || in_dim < 1) return kBadShape;
-    if (group_size < 2 || (group_size & 1)) return kBadGroup;
-    if (!w || !x || !y) return kBadShape;  // nothing is launched on a null operand
+namespace {
+
+// The geometry of one matrix for the MFMA kernels (launch_i4_matvec's fast groups).
+Geom one_matrix_geom(const uint8_t *w, float *y, int out_dim, int in_dim, int group_size) {
     const size_t rb = i4_row_bytes(in_dim, group_size);
-    const bool fast_group = (group_size % 8 == 0) && group_size >= 40;
-    if (!fast_group || rb * kTile * 2 >= (1ull << 31))
-        return launch_i4_matvec_generic(w, x, y, out_dim, in_dim, group_size, stream);
     Geom gm;
     gm.M = out_dim;
     gm.K = in_dim;
@@ -1492,6 +1538,23 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
         gm.my[j] = y;
     }
     gm.ksplit = 1;
+    gm.amax_v = nullptr;
+    gm.amax_i = nullptr;
+    return gm;
+}
+
+}  // namespace
+
+int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                     hipStream_t stream) {
+    if (out_dim < 1 || in_dim < 1) return kBadShape;
+    if (group_size < 2 || (group_size & 1)) return kBadGroup;
+    if (!w || !x || !y) return kBadShape;  // nothing is launched on a null operand
+    const size_t rb = i4_row_bytes(in_dim, group_size);
+    const bool fast_group = (group_size % 8 == 0) && group_size >= 40;
+    if (!fast_group || rb * kTile * 2 >= (1ull << 31))
+        return launch_i4_matvec_generic(w, x, y, out_dim, in_dim, group_size, stream);
+    Geom gm = one_matrix_geom(w, y, out_dim, in_dim, group_size);
     int st;
     {
         const I4Mat m{w, x, y, out_dim, in_dim};
@@ -1510,6 +1573,48 @@ int launch_i4_matvec(const uint8_t *w, const float *x, float *y, int out_dim, in
         st = launch_mfma_for<0>(w, x, y, gm, stream);
     if (st == kTooLarge) return launch_i4_matvec_generic(w, x, y, out_dim, in_dim, group_size, stream);
     return st;
+}
+
+namespace {
+
+// The register-path geometry launch_i4_matvec uses for this one matrix, and its workgroup count,
+// when that is its choice at G = 64 with at most cap workgroups: not the set kernel, rows of at
+// most 8 windows (the split-K and longer-row kernels start above), within the register path's
+// activation set-up limit.
+bool amax_plan(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size, int cap, Geom &gm,
+               int &grid) {
+    if (out_dim < 1 || in_dim < 1 || group_size != 64) return false;
+    const size_t rb = i4_row_bytes(in_dim, group_size);
+    if (rb * kTile * 2 >= (1ull << 31)) return false;
+    const I4Mat m{w, x, y, out_dim, in_dim};
+    if (i4_set_fit_takes(1, &m, group_size)) return false;
+    gm = one_matrix_geom(w, y, out_dim, in_dim, group_size);
+    if (gm.T > 8) return false;
+    gm.NW = gm.T;
+    if (static_cast<size_t>(gm.Gr) * 64 / 8 > static_cast<size_t>(64 * gm.NW)) return false;
+    grid = pipe_grid(gm.tile_end[0]);
+    return grid <= cap;
+}
+
+}  // namespace
+
+bool i4_matvec_amax_takes(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                          int cap) {
+    Geom gm;
+    int grid = 0;
+    return amax_plan(w, x, y, out_dim, in_dim, group_size, cap, gm, grid);
+}
+
+int launch_i4_matvec_amax(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                          float *pv, int *pi, int cap, int *parts, hipStream_t stream) {
+    if (out_dim < 1 || in_dim < 1 || !w || !x || !y || !pv || !pi || !parts) return kBadShape;
+    Geom gm;
+    int grid = 0;
+    if (!amax_plan(w, x, y, out_dim, in_dim, group_size, cap, gm, grid)) return kNotFused;
+    gm.amax_v = pv;
+    gm.amax_i = pi;
+    *parts = grid;
+    return launch_pipe<64, 1, 8, true>(w, x, y, gm, stream);
 }
 
 // Matvecs of n (<= 3) matrices that share x, in_dim and group_size (the

@@ -346,20 +346,34 @@ constexpr int kSetMaxBlocksPerCu = 8;
 
 }  // namespace
 
-int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream_t stream) {
-    if (n < 1 || n > kSetMaxMats) return kNotFused;
-    int shape[kSetMaxMats];
+namespace {
+
+// Whether launch_i4_matvec_set_fit launches the set kernel for these matrices; their shapes at shape.
+bool set_fit_shapes(int n, const I4Mat *mats, int group_size, int *shape) {
+    if (n < 1 || n > kSetMaxMats) return false;
     for (int i = 0; i < n; ++i) {
         shape[i] = set_shape(mats[i], group_size);
-        if (shape[i] < 0 || mats[i].M < 1) return kNotFused;
+        if (shape[i] < 0 || mats[i].M < 1) return false;
     }
     const int RL = long_rows_per_wave(mats, shape, n);
     long blocks = 0;
     for (int i = 0; i < n; ++i)
         blocks += shape[i] == 0 ? (mats[i].M + 4 * kSetWaves - 1) / (4 * kSetWaves)
                                 : (mats[i].M + RL * kSetWaves - 1) / (RL * kSetWaves);
-    if (blocks > static_cast<long>(kSetMaxBlocksPerCu) * device_cu_count()) return kNotFused;
+    return blocks <= static_cast<long>(kSetMaxBlocksPerCu) * device_cu_count();
+}
+
+}  // namespace
+
+int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream_t stream) {
+    int shape[kSetMaxMats];
+    if (!set_fit_shapes(n, mats, group_size, shape)) return kNotFused;
     return launch_set(mats, shape, n, stream);
+}
+
+bool i4_set_fit_takes(int n, const I4Mat *mats, int group_size) {
+    int shape[kSetMaxMats];
+    return set_fit_shapes(n, mats, group_size, shape);
 }
 
 bool set_kernel_takes(int K, int group_size) {

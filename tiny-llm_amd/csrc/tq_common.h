@@ -77,6 +77,7 @@ int launch_i4_matvec_set(int n, const I4Mat *mats, int group_size, hipStream_t s
 // The set kernel for a single or fused launch when every matrix takes it and its grid is small
 // enough to beat the MFMA kernels; kNotFused (nothing launched) otherwise.
 int launch_i4_matvec_set_fit(int n, const I4Mat *mats, int group_size, hipStream_t stream);
+bool i4_set_fit_takes(int n, const I4Mat *mats, int group_size);  // whether the call above would launch
 // Activation prologue of a set launch whose matrices all read the same x (the decode engine's
 // fused launches), applied as the activations are loaded:
 //   kind 1: x = silu(x) * x2 (swiglu_ref);
@@ -99,6 +100,14 @@ bool set_kernel_takes(int K, int group_size);
 // does not take the shape or an operand is misaligned.
 int launch_i4_matvec_glu(const I4Mat &gate, const I4Mat &up, int group_size, const SetPrologue &pro,
                          hipStream_t stream);
+// launch_i4_matvec (same kernel, same bits) with each workgroup's argmax of y (argmax_ref: first
+// row of the largest value; NaN never taken) at pv / pi [0 .. *parts): applies where
+// launch_i4_matvec takes the register-path kernel for one matrix at G = 64 with at most cap
+// workgroups; kNotFused (nothing launched) otherwise.
+int launch_i4_matvec_amax(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                          float *pv, int *pi, int cap, int *parts, hipStream_t stream);
+bool i4_matvec_amax_takes(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, int group_size,
+                          int cap);  // whether the call above would launch
 int launch_vq2_matvec(const uint8_t *w, const float *x, float *y, int out_dim, int in_dim, hipStream_t stream);
 // n independent VQ2 matvecs (I4Mat: weights, activations, output, shape) in as few launches as
 // the one-wave-per-row kernel allows; each output has the bits launch_vq2_matvec gives it.
