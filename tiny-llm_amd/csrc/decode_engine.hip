@@ -116,8 +116,43 @@ void launch_add_rmsnorm(float *hidden, const float *delta, const float *delta2, 
 }
 
 // Row `*token` of an fp32 embedding table.
-__global__ void embed_f32_row(const float *table, const int *token, float *out, int n) {
-    const size_t base = static_cast<size_t>(*token) * n;
+// A step's first launch: the position and the token the host wrote to pinned memory (host_io[0],
+// host_io[1]; read at system scope) go to device memory (io[0], io[1]), where the step's later
+// launches read them, and the token's embedding row is decoded into out. i4 rows decode as
+// i4_embed_rows_kernel decodes them: (q - zero) * scale, one subtraction and one product
+// (dequant_i4_row, kernels/ref_ops.h:183-205); fp32 rows are copied.
+__device__ __forceinline__ int pinned_load(const int *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__global__ __launch_bounds__(256) void step_begin_i4(const uint8_t *__restrict__ embed, const int *host_io, int *io,
+                                                     int dim, int group_size, float *__restrict__ out) {
+    const int pos = pinned_load(host_io), tok = pinned_load(host_io + 1);
+    if (threadIdx.x == 0) {
+        io[0] = pos;
+        io[1] = tok;
+    }
+    const int groups = (dim + group_size - 1) / group_size;
+    const int gbytes = kI4Header + group_size / 2;
+    const uint8_t *r = embed + static_cast<size_t>(tok) * groups * gbytes;
+    for (int k = threadIdx.x; k < dim; k += blockDim.x) {
+        const int g = k / group_size, i = k - g * group_size;
+        const uint8_t *gp = r + static_cast<size_t>(g) * gbytes;
+        const float scale = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(gp[0] | (gp[1] << 8))));
+        const float zero = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(gp[2] | (gp[3] << 8))));
+        const uint8_t b = gp[kI4Header + (i >> 1)];
+        const int q = (i & 1) ? (b >> 4) : (b & 0x0F);
+        out[k] = (static_cast<float>(q) - zero) * scale;
+    }
+}
+
+__global__ void step_begin_f32(const float *table, const int *host_io, int *io, float *out, int n) {
+    const int pos = pinned_load(host_io), tok = pinned_load(host_io + 1);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        io[0] = pos;
+        io[1] = tok;
+    }
+    const size_t base = static_cast<size_t>(tok) * n;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = table[base + i];
 }
 
@@ -211,12 +246,18 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial(const float *x,
     }
 }
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_final(const float *pv, const int *pi, int nb, int *out) {
+// The token goes to out and, when host_out is given (pinned memory), to host_out at system scope.
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final(const float *pv, const int *pi, int nb, int *out,
+                                                               int *host_out) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (int b = threadIdx.x; b < nb; b += kArgmaxThreads) better(bv, bi, pv[b], pi[b]);
     block_argmax(bv, bi);
-    if (threadIdx.x == 0) *out = bi == 0x7fffffff ? 0 : bi;
+    if (threadIdx.x == 0) {
+        const int tok = bi == 0x7fffffff ? 0 : bi;
+        *out = tok;
+        if (host_out) __hip_atomic_store(host_out, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 }
 
 // fp16 -> fp32 of the fp16 vectors a VQ2 file may carry (norms, biases); the
@@ -269,7 +310,7 @@ struct Engine {
     float *hidden2 = nullptr;
     size_t rotbuf_floats = 0;
     int *amax_i = nullptr, *dev_io = nullptr;  // dev_io: pos, token, next, run, flow error
-    int *host_io = nullptr;                     // pinned mirror of dev_io
+    int *host_io = nullptr;  // pinned: a step's position and token in (0, 1), its next token out (2)
     // The data-flow step (decode_flow.hip): one cooperative launch for the layers, then the
     // lm_head and the argmax; the graph above stays as the fallback.
     bool flow = false;
@@ -348,11 +389,12 @@ int forward(Engine &e) {
     const int H = e.c.hidden_size, I = e.c.intermediate_size;
     const float eps = e.c.rms_norm_eps;
     int st = kOk;
+    // the position and token from the host's pinned words, and the token's embedding row
     if (e.embed_i4) {
-        st = launch_i4_embed_rows(static_cast<const uint8_t *>(e.embed), e.dev_io + 1, 1, H, e.gs, e.hidden, s);
-        if (st != kOk) return st;
+        step_begin_i4<<<1, 256, 0, s>>>(static_cast<const uint8_t *>(e.embed), e.host_io, e.dev_io, H, e.gs, e.hidden);
     } else {
-        embed_f32_row<<<(H + 255) / 256, 256, 0, s>>>(static_cast<const float *>(e.embed), e.dev_io + 1, e.hidden, H);
+        step_begin_f32<<<(H + 255) / 256, 256, 0, s>>>(static_cast<const float *>(e.embed), e.host_io, e.dev_io,
+                                                        e.hidden, H);
     }
     if (!e.fused) launch_add_rmsnorm(e.hidden, nullptr, nullptr, e.layers[0].in_ln, e.normed, H, eps, s);
     // A fused launch that does not apply returns kNotFused; the engine chose fused layers
@@ -455,12 +497,12 @@ int forward(Engine &e) {
         st = launch_i4_matvec_amax(e.lm_head, e.normed, e.logits, e.c.vocab_size, H, e.gs, e.amax_v, e.amax_i,
                                    kArgmaxParts, &parts, s);
         if (st != kOk) return st == kNotFused ? kLaunchFailed : st;  // (chosen at create where it applies)
-        argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, parts, e.dev_io + 2);
+        argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, parts, e.dev_io + 2, e.host_io + 2);
         return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
     }
     if ((st = mv(e, e.lm_head, e.lm_dtype, e.normed, e.logits, e.c.vocab_size, H, s)) != kOk) return st;
     argmax_partial<<<e.amax_blocks, kArgmaxThreads, 0, s>>>(e.logits, e.c.vocab_size, e.amax_v, e.amax_i);
-    argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, e.amax_blocks, e.dev_io + 2);
+    argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, e.amax_blocks, e.dev_io + 2, e.host_io + 2);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -482,7 +524,7 @@ int flow_forward(Engine &e) {
     const int st = mv(e, e.lm_head, e.lm_dtype, e.normed, e.logits, e.c.vocab_size, e.c.hidden_size, s);
     if (st != kOk) return st;
     argmax_partial<<<e.amax_blocks, kArgmaxThreads, 0, s>>>(e.logits, e.c.vocab_size, e.amax_v, e.amax_i);
-    argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, e.amax_blocks, e.dev_io + 2);
+    argmax_final<<<1, kArgmaxThreads, 0, s>>>(e.amax_v, e.amax_i, e.amax_blocks, e.dev_io + 2, nullptr);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchFailed;
 }
 
@@ -766,6 +808,7 @@ int create(void *model, int max_seq_len, std::string *err, Engine **out) {
         release(e);
         return kHipFailed;
     }
+    for (int i = 0; i < 8; ++i) e->host_io[i] = 0;  // the set-up pass below runs position 0, token 0
     uint8_t *base = static_cast<uint8_t *>(e->arena);
     for (int i = 0; i < 13; ++i) *slots[i] = reinterpret_cast<float *>(base + offs[i]);
     e->amax_i = reinterpret_cast<int *>(base + offs[13]);
@@ -888,9 +931,9 @@ int tqhip_decode_step(void *engine, int token_id) {
         std::fprintf(stderr, "tqhip: decode engine: the data-flow step timed out; using the step graph\n");
         e->flow = false;
     }
-    if (hipMemcpyAsync(e->dev_io, e->host_io, 2 * sizeof(int), hipMemcpyHostToDevice, e->stream) != hipSuccess ||
-        (e->eager ? eager_forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) ||
-        hipMemcpyAsync(e->host_io + 2, e->dev_io + 2, sizeof(int), hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
+    // The step's first launch reads the position and token from host_io (pinned) and its last
+    // launch writes the next token there: no copies around the graph.
+    if ((e->eager ? eager_forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) ||
         hipStreamSynchronize(e->stream) != hipSuccess)
         return kLaunchFailed;
     e->seq_len += 1;
