@@ -22,6 +22,8 @@ Printed (one JSON line on stdout):
   layer_set    that figure, the same launches replayed from a HIP graph, and the
                layer's dependency-ordered 4-launch form (qkv, o, gate/up, down)
   step_runtime_order  the 97-launch step in the reference runtime's call order
+  step_dependent  the 25-launch step with every layer set reading the previous
+               one's outputs (each set waits for the whole set before it)
   graph        the 25-launch step captured into a HIP graph and replayed
   roofline     the kernel with the largest share of the step's time: the set
                kernel (24 of the 25 launches), its 72 cold launches timed back
@@ -139,13 +141,15 @@ class Workload:
         # per matrix, in the order of self.host, read back for the correctness gate
         self.outputs = [dy[(layer, name)] for layer in range(N_LAYERS) for name, _, _ in LAYER] + [dy_lm]
         self.set_steps, self.rt_steps = [], []  # per copy: the 25-launch and the 97-launch step
-        for _ in range(N_COPIES):
+        wdev, wlm = {}, []  # the copies' weight buffers
+        for c in range(N_COPIES):
             set_ops, rt_ops = [], []
             for layer in range(N_LAYERS):
                 m = {}
                 for name, M, K in LAYER:
                     key = {"q": "attn", "k": "attn", "v": "attn", "gate": "mlp", "up": "mlp"}.get(name, name)
-                    m[name] = (self._dev(weights[(layer, name)]), dx[(layer, key)], dy[(layer, name)], M, K)
+                    wdev[(c, layer, name)] = self._dev(weights[(layer, name)])
+                    m[name] = (wdev[(c, layer, name)], dx[(layer, key)], dy[(layer, name)], M, K)
                 arr = tq.i4_set([m[name] for name, _, _ in LAYER])
                 self.keep.append(arr)
                 set_ops.append(tq.set_op(arr, G))
@@ -156,9 +160,33 @@ class Workload:
                            tq.Op(tq.OP_I4_PAIR, g[0].ptr, g[1].ptr, g[2].ptr, g[3], HIDDEN, 1, G,
                                  u[0].ptr, None, u[2].ptr, None, 0),
                            tq.Op(tq.OP_I4_MATVEC, d[0].ptr, d[1].ptr, d[2].ptr, d[3], d[4], 1, G)]
-            lm = tq.Op(tq.OP_I4_MATVEC, self._dev(w_lm).ptr, dx_lm.ptr, dy_lm.ptr, VOCAB, HIDDEN, 1, G)
+            wlm.append(self._dev(w_lm))
+            lm = tq.Op(tq.OP_I4_MATVEC, wlm[c].ptr, dx_lm.ptr, dy_lm.ptr, VOCAB, HIDDEN, 1, G)
             self.set_steps.append(set_ops + [lm])
             self.rt_steps.append(rt_ops + [lm])
+        # The dependent step: the same 25 launches of the same weight copies, but every input of
+        # layer l > 0 is an output of layer l - 1 (attention input <- down, MLP input <- o,
+        # o input <- q, down input <- gate; the lm_head reads the last down output), so each
+        # layer set waits for the whole previous one, as a decode token's layers do. Its own
+        # output buffers (the gate above checks the independent step's).
+        self.dep_steps = []
+        ydep = {(layer, name): self._dev(None, 4 * M) for layer in range(N_LAYERS) for name, M, _ in LAYER}
+        dy_lm_dep = self._dev(None, 4 * VOCAB)
+        feed = {"attn": "down", "mlp": "o", "o": "q", "down": "gate"}
+        for c in range(N_COPIES):
+            dep_ops = []
+            for layer in range(N_LAYERS):
+                m = {}
+                for name, M, K in LAYER:
+                    key = {"q": "attn", "k": "attn", "v": "attn", "gate": "mlp", "up": "mlp"}.get(name, name)
+                    xin = dx[(layer, key)] if layer == 0 else ydep[(layer - 1, feed[key])]
+                    m[name] = (wdev[(c, layer, name)], xin, ydep[(layer, name)], M, K)
+                arr = tq.i4_set([m[name] for name, _, _ in LAYER])
+                self.keep.append(arr)
+                dep_ops.append(tq.set_op(arr, G))
+            dep_ops.append(tq.Op(tq.OP_I4_MATVEC, wlm[c].ptr, ydep[(N_LAYERS - 1, "down")].ptr, dy_lm_dep.ptr, VOCAB,
+                                 HIDDEN, 1, G))
+            self.dep_steps.append(dep_ops)
         self.bytes = N_LAYERS * LAYER_BYTES + algo_bytes(VOCAB, HIDDEN)
         log(f"[bench] workload: {len(self.host)} matvecs per step, {len(self.set_steps[0])} launches as layer sets "
             f"({len(self.rt_steps[0])} in runtime order), {self.bytes / 1e6:.1f} MB algorithmic per step, "
@@ -169,9 +197,9 @@ class Workload:
         self.bufs.append(b)
         return b
 
-    def steps(self, n, runtime_order=False):
+    def steps(self, n, runtime_order=False, dependent=False):
         """The op list of n consecutive steps, rotating over the weight copies."""
-        src = self.rt_steps if runtime_order else self.set_steps
+        src = self.rt_steps if runtime_order else self.dep_steps if dependent else self.set_steps
         return [op for i in range(n) for op in src[i % N_COPIES]]
 
     def layer_sets(self):
@@ -848,6 +876,13 @@ def main():
           "launches_per_step": len(work.rt_steps[0])}
     log(f"[bench] step in the runtime's call order ({rt['launches_per_step']} launches): {ms_rt * 1e3:.1f} us, "
         f"{rt['value']} GB/s")
+    ms_dep = time_ops(tq, work.steps(args.steps, dependent=True), 1, 1, stream) / args.steps
+    dep = {"ms_per_step": round(ms_dep, 4), "value": round(work.bytes / (ms_dep * 1e-3) / 1e9, 1),
+           "launches_per_step": len(work.dep_steps[0]),
+           "chain": "layer l > 0 reads layer l - 1's outputs (attention in <- down, MLP in <- o, o in <- q, "
+                    "down in <- gate); the lm_head reads the last down output"}
+    log(f"[bench] dependent step (each layer set reads the previous one's outputs): {ms_dep * 1e3:.1f} us, "
+        f"{dep['value']} GB/s")
     took("steps")
     ls = layer_set(tq, work, stream, max(2, args.steps // N_COPIES))
     log(f"[bench] layer set: {ls['us']} us as one launch ({ls['us_graph']} us from a HIP graph), "
@@ -947,6 +982,7 @@ def main():
         "us_per_layer_set": ls["us"],
         "layer_set": ls,
         "step_runtime_order": rt,
+        "step_dependent": dep,
         "graph": graph,
         "config": {"workload": "BASELINE configs[1]: Qwen2.5-0.5B-shaped i4 HQQ@64 decode matvec set, batch=1, "
                                "24 layers x (q 896x896, k/v 128x896, o 896x896, gate/up 4864x896, down 896x4864) "
