@@ -46,14 +46,14 @@ struct AttnShared {
 
 // Sum / max over the head's 256 threads (t = the thread's index within them) in a fixed
 // order: a 64-lane butterfly, then the four wave results in wave order. Every thread of the
-// workgroup must call them (they hold a workgroup barrier).
+// workgroup must call them (they hold a workgroup barrier). red is written before the barrier
+// and read after it; the caller passes an array no thread writes again before a later barrier.
 __device__ inline double attn_sum(double v, double *red, int t) {
     v = xor_sum_wave(v);
     if ((t & 63) == 0) red[t >> 6] = v;
     __syncthreads();
     double r = 0.0;
     for (int w = 0; w < kAttnThreads / 64; ++w) r += red[w];
-    __syncthreads();
     return r;
 }
 
@@ -63,7 +63,6 @@ __device__ inline float attn_max(float v, float *red, int t) {
     __syncthreads();
     float r = red[0];
     for (int w = 1; w < kAttnThreads / 64; ++w) r = fmaxf(r, red[w]);
-    __syncthreads();
     return r;
 }
 
@@ -232,7 +231,9 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
             }
             S.sc[j] = dot * scale;
         }
-        __syncthreads();
+        // Each thread reduces only the scores it wrote; the value sums read the others' after
+        // attn_sum's barrier. fred and dred are each written once per chunk, and the chunk ends
+        // with a barrier.
         float cmax = -INFINITY;
         for (int j = t; j < len; j += kAttnThreads) cmax = fmaxf(cmax, S.sc[j]);
         cmax = attn_max(cmax, S.fred, t);
