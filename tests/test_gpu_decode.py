@@ -21,6 +21,9 @@ CASES = {
                                 layers=2),
     "qwen3_qknorm_hd128": dict(hidden=512, n_heads=4, n_kv_heads=2, head_dim=128, inter=1024, vocab=600,
                                layers=2, biases=False, qk_norm=True),
+    # q/k norms on 64-wide heads: the attention's norms and rotation run in wave 0's registers
+    "qwen3_qknorm_hd64": dict(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, inter=1024, vocab=600,
+                              layers=2, biases=False, qk_norm=True),
     "embed_f32_g128_untied": dict(hidden=512, n_heads=8, n_kv_heads=1, head_dim=64, inter=1024, vocab=500,
                                   layers=1, group_size=128, embed_f32=True, tied=False),
     "vq2_qwen25_shape": dict(hidden=896, n_heads=14, n_kv_heads=2, head_dim=64, inter=4864, vocab=2000, layers=2,

@@ -134,8 +134,10 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
     // the q / k norm weights of element t (files without them: the key cache instead, unused)
     const float qnw = attn_ld((qn ? qn : kh) + (t < hd ? t : 0)), knw = attn_ld((kn ? kn : kh) + (t < hd ? t : 0));
     float c = 0.0f, s = 0.0f;
-    if (t < half) {
-        const float inv_freq = powf(theta, -static_cast<float>(2 * t) / static_cast<float>(hd));
+    // (HD 64: lanes half..63 take the angle of element t - half too, for the rotation in registers)
+    if (t < half || (HD == 64 && t < 64)) {
+        const int i = t < half ? t : t - half;
+        const float inv_freq = powf(theta, -static_cast<float>(2 * i) / static_cast<float>(hd));
         const float angle = static_cast<float>(pos) * inv_freq;
         c = cosf(angle);
         s = sinf(angle);
@@ -155,6 +157,34 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
         const int p = slice + u * slices;
         vreg[u] = attn_ld(vh + static_cast<size_t>(p < max_seq ? p : 0) * hd + d);
     }
+    if constexpr (HD == 64) {
+        // The head is wave 0's, element t in lane t: the q / k norms (rmsnorm_ref on the head,
+        // the sum of squares as head_rms_scale forms it) and the rotation (element t with
+        // element t ^ 32, through a row swap) in registers, then one barrier. The same
+        // operations on the same values as the LDS form below.
+        if (t < 64) {
+            if (qn) {
+                const double sq = xor_sum_wave(0.0 + static_cast<double>(qv) * static_cast<double>(qv));
+                const double sk = xor_sum_wave(0.0 + static_cast<double>(kv) * static_cast<double>(kv));
+                const float rq = 1.0f / sqrtf(static_cast<float>(sq / hd) + eps);
+                const float rk = 1.0f / sqrtf(static_cast<float>(sk / hd) + eps);
+                qv = (qv * rq) * qnw;
+                kv = (kv * rk) * knw;
+            }
+            const float qp = lane_xor<32>(qv, t), kp = lane_xor<32>(kv, t);
+            if (t < half) {
+                qv = qv * c - qp * s;
+                kv = kv * c - kp * s;
+            } else {
+                qv = qv * c + qp * s;
+                kv = kv * c + kp * s;
+            }
+            S.qs[t] = qv;
+            S.ks[t] = kv;
+            S.vs[t] = vv;
+        }
+        __syncthreads();
+    } else {
     if (t < hd) {
         S.qs[t] = qv;
         S.ks[t] = kv;
@@ -187,6 +217,7 @@ __device__ inline bool attention_head(AttnShared &S, int t, int head, int heads_
         }
     }
     __syncthreads();
+    }
     if (writes && head % heads_per_kv == 0 && t < hd) {
         attn_st(kcache + (static_cast<size_t>(kvh) * max_seq + pos) * hd + t, S.ks[t]);
         attn_st(vcache + (static_cast<size_t>(kvh) * max_seq + pos) * hd + t, S.vs[t]);
