@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -932,12 +933,25 @@ int tqhip_decode_step(void *engine, int token_id) {
         e->flow = false;
     }
     // The step's first launch reads the position and token from host_io (pinned) and its last
-    // launch writes the next token there: no copies around the graph.
-    if ((e->eager ? eager_forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) ||
-        hipStreamSynchronize(e->stream) != hipSuccess)
-        return kLaunchFailed;
+    // launch writes the next token there: no copies around the graph. The host waits for that
+    // word (the logits were stored by the launch before it); past a bound, or if the word never
+    // comes, the stream is synchronised, which reports a failed launch.
+    __atomic_store_n(&e->host_io[2], -1, __ATOMIC_SEQ_CST);
+    if (e->eager ? eager_forward(*e) != kOk : hipGraphLaunch(e->exec, e->stream) != hipSuccess) return kLaunchFailed;
+    const auto t0 = std::chrono::steady_clock::now();
+    int next = -1;
+    for (unsigned n = 0;; ++n) {
+        next = __atomic_load_n(&e->host_io[2], __ATOMIC_ACQUIRE);
+        if (next >= 0) break;
+        if ((n & 1023) == 1023 && std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(200)) break;
+    }
+    if (next < 0) {
+        if (hipStreamSynchronize(e->stream) != hipSuccess) return kLaunchFailed;
+        next = __atomic_load_n(&e->host_io[2], __ATOMIC_ACQUIRE);
+        if (next < 0) return kLaunchFailed;
+    }
     e->seq_len += 1;
-    return e->host_io[2];
+    return next;
 }
 
 void tqhip_decode_reset(void *engine) {
