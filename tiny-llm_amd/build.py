@@ -24,7 +24,7 @@ LIB = os.path.join(HERE, "libtqhip.so")
 CEIL_LIB = os.path.join(HERE, "libtqceil.so")  # machine-ceiling probes, loaded by bench.py only
 BUILD_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["i4_matvec.hip", "i4_set.hip", "vq2_matvec.hip", "i4_matmul.hip", "biip_rotate.hip", "i4_embed.hip", "decode_engine.hip", "decode_flow.hip", "tqwen_model.cpp", "dispatch.cpp",
+SOURCES = ["i4_matvec.hip", "i4_set.hip", "vq2_matvec.hip", "i4_matmul.hip", "biip_rotate.hip", "i4_embed.hip", "decode_engine.hip", "decode_flow.hip", "host_copy.hip", "tqwen_model.cpp", "dispatch.cpp",
            "capi.cpp", "synth.cpp", "scratch.cpp", "device.cpp"]
 ARCH = os.environ.get("TQHIP_ARCH", "gfx950")
 

@@ -144,6 +144,12 @@ inline size_t prefill_scratch_bytes(int K, int N) {
     return (Kp * 2 * static_cast<size_t>(N) + 255) / 256 * 256 + 4 * static_cast<size_t>(N);
 }
 
+// n floats at d (device) into h (pinned host memory) by `*wgs` workgroups (at most max_wgs, kTooLarge
+// beyond), each storing seq to done[b] at system scope once its slice is stored: the host reads
+// done[0 .. *wgs) until every word holds seq, then h (host_copy.hip).
+int launch_copy_to_host(const float *d, float *h, size_t n, int *done, int max_wgs, int seq, hipStream_t stream,
+                        int *wgs);
+
 // Compute units of the current device, looked up once (1 when there is no device: the launch
 // that follows fails and reports it). Defined in device.cpp.
 int device_cu_count();
